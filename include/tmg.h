@@ -1,0 +1,162 @@
+/*
+ * tmg.h -- C ABI of the MI355X (gfx950) TinyMiniGo decode path.
+ *
+ * This is the drop-in boundary for the reference crate's public model API
+ * (reference src/lib.rs:1-6).  A Rust `extern "C"` block can bind every
+ * entry point one-to-one; INTEGRATION.md shows that binding.
+ *
+ * Conventions
+ *  - Every function returns an int status (TMG_OK == 0, negative = error
+ *    class) unless it is a free/getter; tmg_last_error() gives the context
+ *    string of the last failure on the calling thread, mirroring the
+ *    reference's anyhow context strings.
+ *  - Host pointers are caller-owned.  Model weights and KV caches live in HBM
+ *    for the lifetime of their handles.
+ *  - One model handle is used by one host thread at a time (the reference's
+ *    forward_* take &mut self).  Each model owns one HIP stream.
+ */
+#ifndef TMG_H
+#define TMG_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define TMG_OK 0
+#define TMG_E_INVALID (-1)  /* bad argument, shape mismatch, token out of range */
+#define TMG_E_IO (-2)       /* file open / read / mmap failure */
+#define TMG_E_FORMAT (-3)   /* malformed safetensors header or JSON */
+#define TMG_E_MISSING (-4)  /* missing tensor, config field or config.json */
+#define TMG_E_DTYPE (-5)    /* unsupported tensor dtype */
+#define TMG_E_EMPTY (-6)    /* empty prompt */
+#define TMG_E_CAPACITY (-7) /* KV cache full (max_pos reached) */
+#define TMG_E_DEVICE (-8)   /* HIP error or no usable GPU */
+#define TMG_E_NOMEM (-9)    /* host or device allocation failed */
+
+typedef struct tmg_model tmg_model;
+typedef struct tmg_cache tmg_cache;
+
+/* ModelConfig (reference src/config.rs:6-20). */
+typedef struct tmg_config {
+    uint32_t hidden_size;
+    uint32_t num_hidden_layers;
+    uint32_t num_attention_heads;
+    uint32_t num_key_value_heads;
+    uint32_t head_dim;
+    uint32_t intermediate_size;
+    uint32_t vocab_size;
+    uint32_t bos_token_id;
+    float rms_norm_eps;
+    float rope_theta;
+    uint32_t n_eos;               /* number of valid entries in eos_token_ids */
+    uint32_t eos_token_ids[16];
+    int32_t tied_lm_head;         /* 1 when lm_head.weight is absent (tied to the embedding) */
+} tmg_config;
+
+/* GenParams (reference src/model.rs:597-604). */
+typedef struct tmg_gen_params {
+    uint32_t max_tokens;
+    float temperature;        /* <= 0: greedy argmax */
+    uint32_t top_k;           /* 0: no top-k */
+    float top_p;              /* >= 1: no nucleus cut */
+    float repetition_penalty; /* 1.0: off */
+    uint64_t seed;
+} tmg_gen_params;
+
+/* on_token callback of generate (reference src/model.rs:618, :648). */
+typedef void (*tmg_on_token_fn)(uint32_t token, void *user);
+
+/* Thread-local text of the last error (reference: anyhow context strings,
+ * e.g. src/model.rs:43-47, src/config.rs:22-27). Never NULL. */
+const char *tmg_last_error(void);
+
+/* ModelConfig::load (reference src/config.rs:112-172): parse an HF
+ * config.json with the reference's defaults. */
+int tmg_config_load(const char *config_json_path, tmg_config *out);
+
+/* Model::load (reference src/model.rs:384-389 -> load_model_safetensors,
+ * src/model.rs:181-244): config.json must sit next to the .safetensors file
+ * (src/config.rs:174-184).  Weight matrices must be BF16; they are uploaded
+ * raw to HBM on `device`.  Norm weights and the embedding may be BF16, F16 or
+ * F32 (converted as in src/safetensors_loader.rs:103-147). */
+int tmg_model_load(const char *safetensors_path, int device, tmg_model **out);
+void tmg_model_free(tmg_model *model);
+int tmg_model_config(const tmg_model *model, tmg_config *out);
+
+/* KvCache (reference src/model.rs:250-332) as a preallocated HBM slab of
+ * max_pos rows per layer: f32 keys and values, [pos, n_kv*head_dim] per
+ * layer, like the reference's flat per-layer Vec<f32>. */
+int tmg_cache_new(tmg_model *model, uint32_t max_pos, tmg_cache **out);
+void tmg_cache_free(tmg_cache *cache);
+/* KvCache::len(layer) (src/model.rs:283-285). */
+int tmg_cache_len(const tmg_cache *cache, uint32_t layer, uint32_t *len);
+/* KvCache::reset (src/model.rs:324-331). */
+int tmg_cache_reset(tmg_cache *cache);
+/* KvCache::keys_flat / values_flat (src/model.rs:309-317): copy the layer's
+ * [len, kv_dim] rows to host buffers (either may be NULL). */
+int tmg_cache_read(const tmg_cache *cache, uint32_t layer, float *keys, float *values);
+
+/* Model::forward_token (src/model.rs:392-491): one decode step at
+ * pos = cache length; writes vocab_size logits when `logits` is non-NULL. */
+int tmg_forward_token(tmg_model *model, tmg_cache *cache, uint32_t token, float *logits);
+
+/* Model::forward_seq (src/model.rs:503-590): batched prefill from the current
+ * cache length; writes the last token's logits when non-NULL. */
+int tmg_forward_seq(tmg_model *model, tmg_cache *cache, const uint32_t *tokens, size_t n, float *last_logits);
+
+/* Model::prefill (src/model.rs:494-499): forward_seq that rejects an empty
+ * prompt with TMG_E_EMPTY. */
+int tmg_prefill(tmg_model *model, tmg_cache *cache, const uint32_t *tokens, size_t n, float *last_logits);
+
+/* generate (src/model.rs:614-663).  Tokens are written to out_tokens
+ * (capacity out_cap >= max_tokens), their count to *n_out.  first_logits
+ * (vocab_size floats) and prefill_secs may be NULL.  Sampling (temperature >
+ * 0) runs on the GPU with its own counter-based generator keyed by `seed`:
+ * the reference's rand::StdRng stream is not reproduced. */
+int tmg_generate(tmg_model *model, const uint32_t *prompt, size_t n_prompt, const tmg_gen_params *params,
+                 tmg_on_token_fn on_token, void *user, uint32_t *out_tokens, size_t out_cap, size_t *n_out,
+                 float *first_logits, float *prefill_secs);
+
+/* Kernel level: y[out] = W[out,in] x[in] with W raw BF16 row-major and x, y
+ * f32, all DEVICE pointers (reference tensor::matmul_w / matmul_w_into,
+ * src/tensor.rs:315-338, BF16 case).  `stream` is a hipStream_t (NULL = the
+ * default stream).  in must be a multiple of 8 and W 16-byte aligned. */
+int tmg_gemv_bf16(const uint16_t *w_dev, const float *x_dev, float *y_dev, uint32_t out, uint32_t in,
+                  void *stream);
+
+/* ---------------------------------------------------------------------- */
+/* Measurement entry points.  No counterpart in the reference: they expose  */
+/* the inner loop of generate (src/model.rs:631-656) without the host       */
+/* callback, and per-kernel timing, for benchmarks.                          */
+/* ---------------------------------------------------------------------- */
+
+/* Run n_steps greedy decode steps on the device starting from `token` at the
+ * current cache length (one captured step graph per step; each step is
+ * forward_token followed by argmax, as in generate).  Generated ids go to
+ * tokens_out (n_steps entries, may be NULL); *ms receives the elapsed time
+ * between HIP events recorded on the model's stream around the steps. */
+int tmg_decode_greedy(tmg_model *model, tmg_cache *cache, uint32_t token, uint32_t n_steps, uint32_t *tokens_out,
+                      float *ms);
+
+/* One launched kernel of a decode step, timed with HIP events on the model's
+ * stream; bytes = algorithmic HBM bytes of that launch. */
+typedef struct tmg_kernel_record {
+    char name[48];
+    double bytes;
+    float ms;
+} tmg_kernel_record;
+
+/* Run one decode step kernel by kernel (not from the graph) with an event
+ * pair around each launch.  Advances the cache like forward_token. */
+int tmg_profile_decode_step(tmg_model *model, tmg_cache *cache, uint32_t token, tmg_kernel_record *records,
+                            size_t cap, size_t *n_records);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TMG_H */

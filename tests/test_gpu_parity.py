@@ -1,0 +1,250 @@
+"""GPU parity: the HIP path (through the C ABI) against the oracle.
+
+Tolerances are the ones the decode path is held to: logits within
+max-abs 2e-3 and relative 1e-3 of the oracle (both sides accumulate f32 from
+the same BF16 weights, in different orders), greedy ids identical, and
+argmax / top-k ids exact given those logits.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from conftest import model_root
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+ABS_TOL, REL_TOL = 2e-3, 1e-3
+
+
+def close_logits(a, b, what=""):
+    d = np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))
+    lim = ABS_TOL + REL_TOL * np.abs(np.asarray(b, np.float64))
+    assert np.all(d <= lim), f"{what}: max abs diff {d.max():.3e}"
+    return float(d.max())
+
+
+@pytest.fixture(scope="module")
+def T():
+    import tinyminigo_amd as T
+    return T
+
+
+@pytest.fixture(scope="module")
+def O():
+    from oracle import oracle as O
+    return O
+
+
+@pytest.fixture(scope="module")
+def W():
+    from tinyminigo_amd import workloads as W
+    return W
+
+
+# --- kernel level: the decode GEMV (C1 shapes and ragged ones) ---------------
+
+@pytest.mark.parametrize("out,inp", [(2048, 2048), (6144, 2048), (2048, 6144), (73448, 2048), (24, 64),
+                                     (100, 136), (8, 10240), (1, 8), (2560, 4096)])
+def test_gemv_bf16_vs_oracle(T, O, out, inp):
+    import torch
+    print(f"gemv {out}x{inp}", flush=True)
+    w = T.synth_normal_bf16(2, f"w{out}x{inp}", out * inp, 0.02)
+    x = T.synth_normal_f32(2, f"x{inp}", inp, 1.0)
+    want = O.matmul_w(x, w, out, inp)
+    wd = torch.from_numpy(w.view(np.int16)).cuda()
+    xd = torch.from_numpy(x).cuda()
+    yd = torch.full((out,), float("nan"), device="cuda")
+    T.gemv_bf16(wd.data_ptr(), xd.data_ptr(), yd.data_ptr(), out, inp)
+    torch.cuda.synchronize()
+    got = yd.cpu().numpy()
+    wf = (w.astype(np.uint32) << 16).view(np.float32).astype(np.float64).reshape(out, inp)
+    exact = wf @ x.astype(np.float64)
+    mag = np.abs(wf) @ np.abs(x.astype(np.float64))
+    assert np.all(np.abs(got - exact) <= 2e-6 * mag + 1e-30)
+    assert np.abs(got - want).max() <= 1e-4
+
+
+def test_gemv_small_golden(T):
+    import torch
+    z = np.load(os.path.join(GOLD, "gemv_small.npz"))
+    wd = torch.from_numpy(z["w"].view(np.int16)).cuda()
+    xd = torch.from_numpy(z["x"]).cuda()
+    yd = torch.empty(64, device="cuda")
+    T.gemv_bf16(wd.data_ptr(), xd.data_ptr(), yd.data_ptr(), 64, 128)
+    torch.cuda.synchronize()
+    assert np.abs(yd.cpu().numpy() - z["y"]).max() <= 1e-5
+
+
+# --- C0: tiny Llama, prefill + 40 greedy steps -------------------------------
+
+@pytest.fixture(scope="module")
+def tiny_gpu(T, tiny_path):
+    return T.Model.load(tiny_path)
+
+
+@pytest.fixture(scope="module")
+def fx():
+    return json.load(open(os.path.join(GOLD, "tiny_llama.json")))
+
+
+def test_tiny_prefill_and_greedy_vs_golden(T, tiny_gpu, fx):
+    m = tiny_gpu
+    z = np.load(os.path.join(GOLD, "tiny_llama.npz"))
+    cache = T.KvCache(m, 64)
+    logits = m.forward_seq(fx["prompt"], cache)
+    close_logits(logits, z["prefill_logits"], "prefill")
+    assert cache.len(0) == 16 and cache.len(1) == 16
+    assert np.abs(cache.keys_flat(1).reshape(16, -1) - z["keys_l1"]).max() < 1e-4
+    assert np.abs(cache.values_flat(1).reshape(16, -1) - z["values_l1"]).max() < 1e-4
+    toks = []
+    for i, st in enumerate(fx["steps"]):
+        nxt = int(np.argmax(logits))
+        toks.append(nxt)
+        close_logits(logits[:16], st["first16"], f"step {i}")
+        assert [int(j) for j, _ in st["top8"]][0] == nxt
+        logits = m.forward_token(nxt, cache)
+    assert toks == fx["greedy_tokens"]
+    assert cache.total_len() == 16 + 40
+
+
+def test_tiny_generate_greedy(T, tiny_gpu, fx):
+    seen = []
+    out = T.generate(tiny_gpu, fx["prompt"], T.GenParams(max_tokens=40), on_token=seen.append)
+    assert out.tokens == fx["greedy_tokens"] == seen
+    z = np.load(os.path.join(GOLD, "tiny_llama.npz"))
+    close_logits(out.logits_first_step, z["prefill_logits"], "first logits")
+    assert out.prefill_secs > 0
+
+
+def test_tiny_decode_greedy_entry(T, tiny_gpu, fx):
+    cache = T.KvCache(tiny_gpu, 64)
+    tiny_gpu.forward_seq(fx["prompt"], cache)
+    toks, ms = tiny_gpu.decode_greedy(fx["greedy_tokens"][0], 39, cache)
+    assert list(toks) == fx["greedy_tokens"][1:]
+    assert ms > 0 and cache.total_len() == 16 + 39
+
+
+# --- untied tiny model, teacher-forced random tokens --------------------------
+
+@pytest.fixture(scope="module")
+def untied(T, O, W):
+    import dataclasses
+    wl = dataclasses.replace(W.TINY, name="tiny-llama-untied-s11", tied_lm_head=False, weight_seed=11,
+                             rope_theta=500.0, rms_norm_eps=1e-5)
+    p = W.ensure_model(wl, model_root())
+    return T.Model.load(p), O.OracleModel.load(p), wl
+
+
+def test_untied_teacher_forced_logits_and_cache(T, O, untied):
+    g, o, wl = untied
+    ids = [int(t) for t in T.synth_tokens(21, 80, wl.vocab_size)]
+    gc, oc = T.KvCache(g, 128), o.new_cache()
+    close_logits(g.forward_seq(ids[:20], gc), o.forward_seq(ids[:20], oc), "prefill 20")
+    for i, t in enumerate(ids[20:60]):
+        a, b = g.forward_token(t, gc), o.forward_token(t, oc)
+        close_logits(a, b, f"decode {i}")
+        # top-50 candidate ids identical: same set, same order wherever
+        # neighbours are separated by more than the logit tolerance
+        ta, tb = np.argsort(-a, kind="stable")[:50], np.argsort(-b, kind="stable")[:50]
+        assert set(ta) == set(tb) or np.min(np.abs(np.diff(np.sort(b)[::-1][:51]))) < 2 * ABS_TOL
+        for j in range(50):
+            if ta[j] != tb[j]:
+                assert abs(b[ta[j]] - b[tb[j]]) < 2 * ABS_TOL
+    # a second prefill chunk starting mid-cache (start_pos > 0)
+    close_logits(g.forward_seq(ids[60:80], gc), o.forward_seq(ids[60:80], oc), "prefill at 60")
+    for layer in range(wl.num_hidden_layers):
+        assert gc.len(layer) == oc.len(layer) == 80
+        assert np.abs(gc.keys_flat(layer) - oc.keys_flat(layer)).max() < 1e-4
+        assert np.abs(gc.values_flat(layer) - oc.values_flat(layer)).max() < 1e-4
+    gc.reset()
+    assert gc.total_len() == 0
+    oc2 = o.new_cache()
+    close_logits(g.forward_seq(ids[:5], gc), o.forward_seq(ids[:5], oc2), "after reset")
+
+
+def test_gpu_forward_seq_matches_forward_token(T, untied):
+    g, _, wl = untied
+    ids = [int(t) for t in T.synth_tokens(22, 30, wl.vocab_size)]
+    a_c, b_c = T.KvCache(g, 64), T.KvCache(g, 64)
+    for t in ids:
+        a = g.forward_token(t, a_c)
+    b = g.forward_seq(ids, b_c)
+    assert np.abs(a - b).max() < 1e-2  # reference bound, tests/diff_debug.rs:39
+
+
+def test_gpu_error_paths(T, untied):
+    g, _, wl = untied
+    c = T.KvCache(g, 4)
+    with pytest.raises(T.TmgError, match="TMG_E_EMPTY"):
+        g.prefill([], c)
+    with pytest.raises(T.TmgError, match="out of range"):
+        g.forward_token(wl.vocab_size, c)
+    g.forward_seq([1, 2, 3, 4], c)
+    with pytest.raises(T.TmgError, match="TMG_E_CAPACITY"):
+        g.forward_token(5, c)
+    with pytest.raises(T.TmgError, match="TMG_E_EMPTY"):
+        T.generate(g, [], T.GenParams(max_tokens=3))
+
+
+# --- sampling on the device vs the oracle's sample() with the same draws ----
+
+def device_draw(seed: int, i: int) -> float:
+    M = 2**64 - 1
+
+    def mix(z):
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+        return z ^ (z >> 31)
+
+    h = 0xcbf29ce484222325
+    for ch in b"sample":
+        h = ((h ^ ch) * 0x100000001b3) & M
+    key = mix(((seed * 0x9E3779B97F4A7C15) & M) ^ h)
+    return float(np.float32((mix((key + (i + 1) * 0x9E3779B97F4A7C15) & M) >> 40) * 2.0**-24))
+
+
+@pytest.mark.parametrize("temp,k,p,pen", [(0.8, 50, 0.9, 1.1), (1.0, 0, 1.0, 1.0), (0.0, 0, 1.0, 1.3),
+                                          (0.7, 7, 1.0, 1.0), (1.2, 64, 0.5, 1.05)])
+def test_sampling_teacher_forced(T, O, untied, temp, k, p, pen):
+    g, o, wl = untied
+    prompt = [int(t) for t in T.synth_tokens(23, 12, wl.vocab_size)]
+    out = T.generate(g, prompt, T.GenParams(max_tokens=48, temperature=temp, top_k=k, top_p=p,
+                                            repetition_penalty=pen, seed=42))
+    assert len(out.tokens) == 48
+    ref = O.generate(o, prompt, 48, forced=out.tokens, repetition_penalty=pen, keep_logits=True)
+    mism = 0
+    for i, (tok, lg) in enumerate(zip(out.tokens, ref.step_logits)):
+        tr = O.sample(lg, temp, k, p, device_draw(42, i))
+        if tr.token != tok:
+            mism += 1
+        if temp > 0:
+            assert tok in set(int(c) for c, pr in zip(tr.cand_ids, tr.cand_probs) if pr > 0), f"step {i}"
+    # identical draws on logits equal within tolerance: at most a boundary case
+    assert mism <= 1, f"{mism} of 48 sampled ids differ"
+
+
+# --- C2: the 1B-class model, prefill 64 + greedy decode -----------------------
+
+@pytest.fixture(scope="module")
+def one_b(T, O, W):
+    p = W.ensure_model(W.ONE_B, model_root())
+    return T.Model.load(p), O.OracleModel.load(p)
+
+
+def test_one_b_prefill_and_greedy(T, O, W, one_b):
+    g, o = one_b
+    prompt = [int(t) for t in W.ONE_B.prompt()]
+    steps = 24
+    out = T.generate(g, prompt, T.GenParams(max_tokens=steps))
+    ref = O.generate(o, prompt, steps, keep_logits=True)
+    close_logits(out.logits_first_step, ref.logits_first_step, "1B prefill")
+    assert out.tokens == ref.tokens
+    # per-step logits through forward_token (teacher forcing the shared ids)
+    gc = T.KvCache(g, 128)
+    lg = g.forward_seq(prompt, gc)
+    for i, t in enumerate(ref.tokens[:8]):
+        close_logits(lg, ref.step_logits[i], f"1B step {i}")
+        lg = g.forward_token(t, gc)

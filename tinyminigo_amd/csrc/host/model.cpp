@@ -1,0 +1,843 @@
+// Model load, KV cache, decode step (captured as a hipGraph), prefill and
+// the C ABI entry points of tmg.h.
+#include "model.hpp"
+
+#include <chrono>
+#include <cmath>
+#include <cstring>
+
+namespace tmg {
+
+#define TMG_HIP(expr)                                                                                       \
+    do {                                                                                                    \
+        hipError_t e_ = (expr);                                                                             \
+        if (e_ != hipSuccess)                                                                               \
+            return set_error(TMG_E_DEVICE, std::string("HIP error ") + hipGetErrorString(e_) + " in " #expr \
+                                               " (" __FILE__ ":" + std::to_string(__LINE__) + ")");         \
+    } while (0)
+
+template <class T>
+static int dev_alloc(tmg_model *m, T **p, size_t count) {
+    void *q = nullptr;
+    if (count == 0) count = 1;
+    hipError_t e = hipMalloc(&q, count * sizeof(T));
+    if (e != hipSuccess)
+        return set_error(TMG_E_NOMEM, std::string("hipMalloc of ") + std::to_string(count * sizeof(T)) +
+                                          " bytes failed: " + hipGetErrorString(e));
+    m->allocs.push_back(q);
+    *p = (T *)q;
+    return TMG_OK;
+}
+
+int pinned(tmg_model *m, size_t bytes) {
+    if (m->pin_bytes >= bytes) return TMG_OK;
+    if (m->pin) (void)hipHostFree(m->pin);
+    m->pin = nullptr;
+    m->pin_bytes = 0;
+    TMG_HIP(hipHostMalloc(&m->pin, bytes, hipHostMallocDefault));
+    m->pin_bytes = bytes;
+    return TMG_OK;
+}
+
+static void model_release(tmg_model *m) {
+    if (!m) return;
+    (void)hipSetDevice(m->device);
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    for (void *p : m->allocs) (void)hipFree(p);
+    if (m->pin) (void)hipHostFree(m->pin);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
+    delete m;
+}
+
+// Rope::new + Rope::ensure (reference src/tensor.rs:1005-1023):
+// inv_freq[i] = 1/theta^(2i/hd) with f32 powf; angle = pos * inv_freq[i];
+// sin/cos with libm f32 -- the same calls the reference makes.
+int ensure_rope(tmg_model *m, int npos) {
+    if (npos <= m->rope_npos) return TMG_OK;
+    const int half = m->hd / 2;
+    int cap = m->rope_npos ? m->rope_npos : 64;
+    while (cap < npos) cap *= 2;
+    std::vector<float> inv(half), cs((size_t)cap * half), sn((size_t)cap * half);
+    for (int i = 0; i < half; i++) inv[i] = 1.0f / powf(m->cfg.rope_theta, 2.0f * (float)i / (float)m->hd);
+    for (int p = 0; p < cap; p++)
+        for (int i = 0; i < half; i++) {
+            float ang = (float)p * inv[i];
+            sn[(size_t)p * half + i] = sinf(ang);
+            cs[(size_t)p * half + i] = cosf(ang);
+        }
+    float *dc = nullptr, *ds = nullptr;
+    int rc;
+    if ((rc = dev_alloc(m, &dc, (size_t)cap * half)) || (rc = dev_alloc(m, &ds, (size_t)cap * half))) return rc;
+    TMG_HIP(hipMemcpy(dc, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    TMG_HIP(hipMemcpy(ds, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+    // old tables stay allocated (graphs captured earlier may point at them)
+    m->rope_cos = dc;
+    m->rope_sin = ds;
+    m->rope_npos = cap;
+    return TMG_OK;
+}
+
+// ---------------------------------------------------------------------------
+// load (reference load_model_safetensors, src/model.rs:181-244)
+// ---------------------------------------------------------------------------
+
+static int need(const SafeTensorsFile &f, const std::string &name, const std::vector<uint64_t> &shape,
+                const TensorEntry **out) {
+    const TensorEntry *e = f.find(name);
+    if (!e) return set_error(TMG_E_MISSING, "missing tensor `" + name + "` in safetensors file");
+    uint64_t want = 1;
+    for (auto d : shape) want *= d;
+    if (e->numel() != want) {
+        std::string s;
+        for (auto d : shape) s += (s.empty() ? "" : "x") + std::to_string(d);
+        return set_error(TMG_E_INVALID, "tensor `" + name + "` has " + std::to_string(e->numel()) +
+                                            " elements, expected " + s);
+    }
+    if (e->dtype == DType::Other)
+        return set_error(TMG_E_DTYPE, "unsupported dtype " + e->dtype_name + " for tensor " + name);
+    *out = e;
+    return TMG_OK;
+}
+
+static int need_bf16(const SafeTensorsFile &f, const std::string &name, const std::vector<uint64_t> &shape,
+                     const TensorEntry **out) {
+    int rc = need(f, name, shape, out);
+    if (rc) return rc;
+    if ((*out)->dtype != DType::BF16)
+        return set_error(TMG_E_DTYPE, "tensor " + name + " is " + (*out)->dtype_name +
+                                          ": the GPU decode path streams raw BF16 weight matrices only");
+    return TMG_OK;
+}
+
+static int upload_f32(tmg_model *m, const SafeTensorsFile &f, const TensorEntry *e, float **dst) {
+    std::vector<float> v;
+    int rc = tensor_to_f32(f, *e, &v);
+    if (rc) return rc;
+    if ((rc = dev_alloc(m, dst, v.size()))) return rc;
+    TMG_HIP(hipMemcpy(*dst, v.data(), v.size() * 4, hipMemcpyHostToDevice));
+    return TMG_OK;
+}
+
+static int upload_raw(tmg_model *m, const void *src, size_t bytes, uint16_t **dst) {
+    int rc;
+    if ((rc = dev_alloc(m, dst, bytes / 2))) return rc;
+    TMG_HIP(hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice));
+    return TMG_OK;
+}
+
+// Host-only phase: config.json + every tensor's presence, shape and dtype,
+// so file errors surface before any device work (and without a GPU).
+static int validate_files(tmg_model *m, const std::string &path, SafeTensorsFile *f) {
+    std::string cpath;
+    if (!config_path_for_model(path, &cpath)) return set_error(TMG_E_MISSING, "config.json not found next to " + path);
+    int rc = config_load(cpath, &m->cfg);
+    if (rc) return rc;
+    const tmg_config &c = m->cfg;
+    m->H = c.hidden_size;
+    m->L = c.num_hidden_layers;
+    m->nq = c.num_attention_heads;
+    m->nkv = c.num_key_value_heads;
+    m->hd = c.head_dim;
+    m->I = c.intermediate_size;
+    m->V = c.vocab_size;
+    m->qd = m->nq * m->hd;
+    m->kvd = m->nkv * m->hd;
+    m->qkv_rows = m->qd + 2 * m->kvd;
+    if (m->nkv == 0 || m->nq % m->nkv != 0)
+        return set_error(TMG_E_INVALID, "num_attention_heads must be a multiple of num_key_value_heads");
+    const int group = m->nq / m->nkv;
+    if (group != 1 && group != 2 && group != 4 && group != 8)
+        return set_error(TMG_E_INVALID, "GQA group size " + std::to_string(group) + " is not supported (1, 2, 4, 8)");
+    if (m->hd != 16 && m->hd != 32 && m->hd != 64 && m->hd != 128 && m->hd != 256)
+        return set_error(TMG_E_INVALID, "head_dim " + std::to_string(m->hd) + " is not supported (16..256, power of 2)");
+    if (m->H % 32 || m->qd % 32 || m->I % 32 || m->H > 16384 || m->qd > 16384 || m->I > 16384)
+        return set_error(TMG_E_INVALID, "hidden, q and intermediate sizes must be multiples of 32 and <= 16384");
+    if (m->V == 0) return set_error(TMG_E_INVALID, "vocab_size is 0");
+    if ((rc = f->open(path))) return rc;
+    const uint64_t H = m->H, I = m->I, V = m->V, qd = m->qd, kvd = m->kvd;
+    const TensorEntry *e;
+    if ((rc = need(*f, "model.embed_tokens.weight", {V, H}, &e))) return rc;
+    for (int l = 0; l < m->L; l++) {
+        const std::string p = "model.layers." + std::to_string(l) + ".";
+        if ((rc = need_bf16(*f, p + "self_attn.q_proj.weight", {qd, H}, &e)) ||
+            (rc = need_bf16(*f, p + "self_attn.k_proj.weight", {kvd, H}, &e)) ||
+            (rc = need_bf16(*f, p + "self_attn.v_proj.weight", {kvd, H}, &e)) ||
+            (rc = need_bf16(*f, p + "self_attn.o_proj.weight", {H, qd}, &e)) ||
+            (rc = need_bf16(*f, p + "mlp.gate_proj.weight", {I, H}, &e)) ||
+            (rc = need_bf16(*f, p + "mlp.up_proj.weight", {I, H}, &e)) ||
+            (rc = need_bf16(*f, p + "mlp.down_proj.weight", {H, I}, &e)) ||
+            (rc = need(*f, p + "input_layernorm.weight", {H}, &e)) ||
+            (rc = need(*f, p + "post_attention_layernorm.weight", {H}, &e)))
+            return rc;
+    }
+    if ((rc = need(*f, "model.norm.weight", {H}, &e))) return rc;
+    if (f->find("lm_head.weight")) {
+        if ((rc = need_bf16(*f, "lm_head.weight", {V, H}, &e))) return rc;
+    } else if (f->find("model.embed_tokens.weight")->dtype != DType::BF16) {
+        return set_error(TMG_E_DTYPE, "tied lm_head needs a BF16 embedding table on the GPU path");
+    }
+    return TMG_OK;
+}
+
+// Device phase: upload into the HBM layout.
+static int load_model(tmg_model *m, const SafeTensorsFile &f) {
+    int rc;
+    const int group = m->nq / m->nkv;
+    const uint64_t H = m->H, I = m->I, V = m->V, qd = m->qd, kvd = m->kvd;
+
+    // embedding: raw BF16 on the device, else converted to f32 as the reference does
+    const TensorEntry *emb;
+    if ((rc = need(f, "model.embed_tokens.weight", {V, H}, &emb))) return rc;
+    if (emb->dtype == DType::BF16) {
+        if ((rc = upload_raw(m, f.data(*emb), V * H * 2, &m->embed_bf16))) return rc;
+    } else {
+        if ((rc = upload_f32(m, f, emb, &m->embed_f32))) return rc;
+    }
+
+    const int half = m->hd / 2;
+    std::vector<uint16_t> stage;
+    m->layers.resize(m->L);
+    for (int l = 0; l < m->L; l++) {
+        const std::string p = "model.layers." + std::to_string(l) + ".";
+        const TensorEntry *wq, *wk, *wv, *wo, *wg, *wu, *wd, *n1, *n2;
+        if ((rc = need_bf16(f, p + "self_attn.q_proj.weight", {qd, H}, &wq)) ||
+            (rc = need_bf16(f, p + "self_attn.k_proj.weight", {kvd, H}, &wk)) ||
+            (rc = need_bf16(f, p + "self_attn.v_proj.weight", {kvd, H}, &wv)) ||
+            (rc = need_bf16(f, p + "self_attn.o_proj.weight", {H, qd}, &wo)) ||
+            (rc = need_bf16(f, p + "mlp.gate_proj.weight", {I, H}, &wg)) ||
+            (rc = need_bf16(f, p + "mlp.up_proj.weight", {I, H}, &wu)) ||
+            (rc = need_bf16(f, p + "mlp.down_proj.weight", {H, I}, &wd)) ||
+            (rc = need(f, p + "input_layernorm.weight", {H}, &n1)) ||
+            (rc = need(f, p + "post_attention_layernorm.weight", {H}, &n2)))
+            return rc;
+        tmg_model::Layer &ly = m->layers[l];
+        // QKV: logical rows [q; k; v]; physical row 2P = (head, j), 2P+1 = (head, j+hd/2)
+        stage.resize((size_t)m->qkv_rows * H);
+        const uint16_t *src[3] = {(const uint16_t *)f.data(*wq), (const uint16_t *)f.data(*wk),
+                                  (const uint16_t *)f.data(*wv)};
+        const int sec_rows[3] = {m->qd, m->kvd, m->kvd};
+        int P = 0;
+        for (int sct = 0; sct < 3; sct++)
+            for (int hh = 0; hh < sec_rows[sct] / m->hd; hh++)
+                for (int j = 0; j < half; j++, P++) {
+                    memcpy(&stage[(size_t)(2 * P) * H], src[sct] + ((size_t)hh * m->hd + j) * H, H * 2);
+                    memcpy(&stage[(size_t)(2 * P + 1) * H], src[sct] + ((size_t)hh * m->hd + j + half) * H, H * 2);
+                }
+        if ((rc = upload_raw(m, stage.data(), stage.size() * 2, &ly.qkv))) return rc;
+        if ((rc = upload_raw(m, f.data(*wo), H * qd * 2, &ly.o))) return rc;
+        stage.resize((size_t)2 * I * H);
+        const uint16_t *g = (const uint16_t *)f.data(*wg), *u = (const uint16_t *)f.data(*wu);
+        for (uint64_t r = 0; r < I; r++) {
+            memcpy(&stage[(2 * r) * H], g + r * H, H * 2);
+            memcpy(&stage[(2 * r + 1) * H], u + r * H, H * 2);
+        }
+        if ((rc = upload_raw(m, stage.data(), stage.size() * 2, &ly.gu))) return rc;
+        if ((rc = upload_raw(m, f.data(*wd), H * I * 2, &ly.down))) return rc;
+        if ((rc = upload_f32(m, f, n1, &ly.in_norm)) || (rc = upload_f32(m, f, n2, &ly.post_norm))) return rc;
+    }
+    const TensorEntry *fn;
+    if ((rc = need(f, "model.norm.weight", {H}, &fn)) || (rc = upload_f32(m, f, fn, &m->final_norm))) return rc;
+
+    // lm_head: dedicated tensor if present, else tied to the embedding
+    // (src/model.rs:230-233); tying reuses the raw BF16 table, which equals
+    // the reference's f32 copy element for element.
+    if (f.find("lm_head.weight")) {
+        const TensorEntry *lm;
+        if ((rc = need_bf16(f, "lm_head.weight", {V, H}, &lm))) return rc;
+        if ((rc = upload_raw(m, f.data(*lm), V * H * 2, &m->lm_head))) return rc;
+        m->cfg.tied_lm_head = 0;
+    } else {
+        if (!m->embed_bf16)
+            return set_error(TMG_E_DTYPE, "tied lm_head needs a BF16 embedding table on the GPU path");
+        m->lm_head = m->embed_bf16;
+        m->cfg.tied_lm_head = 1;
+    }
+
+    // decode scratch
+    if ((rc = dev_alloc(m, &m->x, H)) || (rc = dev_alloc(m, &m->q, qd)) || (rc = dev_alloc(m, &m->attn_out, qd)) ||
+        (rc = dev_alloc(m, &m->h, I)) || (rc = dev_alloc(m, &m->logits, V)))
+        return rc;
+    m->attn_nsplit = std::max(1, std::min(64, 512 / m->nkv));
+    m->attn_min_chunk = 16;
+    if ((rc = dev_alloc(m, &m->attn_part, (size_t)m->nkv * m->attn_nsplit * group * m->hd)) ||
+        (rc = dev_alloc(m, &m->attn_ml, (size_t)m->nkv * m->attn_nsplit * group * 2)) ||
+        (rc = dev_alloc(m, &m->attn_counter, (size_t)m->nkv)))
+        return rc;
+    TMG_HIP(hipMemset(m->attn_counter, 0, sizeof(unsigned) * m->nkv));
+    if ((rc = ensure_rope(m, 64))) return rc;
+    if ((rc = pinned(m, (size_t)std::max<uint64_t>(V * 4, 1 << 16)))) return rc;
+    TMG_HIP(hipDeviceSynchronize());
+    return TMG_OK;
+}
+
+// ---------------------------------------------------------------------------
+// decode step (reference Model::forward_token, src/model.rs:392-491, plus the
+// argmax of generate, src/model.rs:636-637)
+// ---------------------------------------------------------------------------
+
+void LaunchRecorder::begin(const char *name, double bytes) {
+    tmg_kernel_record r{};
+    snprintf(r.name, sizeof(r.name), "%s", name);
+    r.bytes = bytes;
+    recs.push_back(r);
+    hipEvent_t e;
+    (void)hipEventCreate(&e);
+    (void)hipEventRecord(e, stream);
+    evs.push_back(e);
+}
+
+void LaunchRecorder::end() {
+    hipEvent_t e;
+    (void)hipEventCreate(&e);
+    (void)hipEventRecord(e, stream);
+    evs.push_back(e);
+}
+
+int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mode) {
+    hipStream_t s = m->stream;
+    const int H = m->H, I = m->I, qd = m->qd, kvd = m->kvd;
+    const double n_ctx_est = (double)c->len + 1;
+    for (int l = 0; l < m->L; l++) {
+        const tmg_model::Layer &ly = m->layers[l];
+        float *kc = c->k + (size_t)l * c->max_pos * kvd;
+        float *vc = c->v + (size_t)l * c->max_pos * kvd;
+
+        GemvArgs qa{};
+        qa.W = ly.qkv;
+        qa.out = m->qkv_rows;
+        qa.in = H;
+        qa.x = m->x;
+        qa.norm_w = ly.in_norm;
+        qa.eps = m->cfg.rms_norm_eps;
+        qa.rope_cos = m->rope_cos;
+        qa.rope_sin = m->rope_sin;
+        qa.pos = &c->st->pos;
+        qa.hd = m->hd;
+        qa.nq = m->nq;
+        qa.nkv = m->nkv;
+        qa.q_out = m->q;
+        qa.k_cache = kc;
+        qa.v_cache = vc;
+        int pro = PRO_NORM;
+        if (l == 0) {
+            pro = PRO_EMBED_NORM;
+            qa.token = &c->st->cur_token;
+            qa.embed_bf16 = m->embed_bf16;
+            qa.embed_f32 = m->embed_f32;
+            qa.x_store = m->x;
+        }
+        if (rec) rec->begin("gemv_qkv_rope", (double)m->qkv_rows * H * 2 + H * 8.0 + (qd + 2 * kvd) * 4.0);
+        TMG_HIP(launch_gemv(pro, EPI_QKV, qa, s));
+        if (rec) rec->end();
+
+        AttnArgs aa{};
+        aa.q = m->q;
+        aa.k_cache = kc;
+        aa.v_cache = vc;
+        aa.nq = m->nq;
+        aa.nkv = m->nkv;
+        aa.hd = m->hd;
+        aa.T = 1;
+        aa.pos_dev = &c->st->pos;
+        aa.scale = 1.0f / sqrtf((float)m->hd);
+        aa.nsplit = m->attn_nsplit;
+        aa.min_chunk = m->attn_min_chunk;
+        aa.part = m->attn_part;
+        aa.part_ml = m->attn_ml;
+        aa.counter = m->attn_counter;
+        aa.out_f32 = m->attn_out;
+        if (rec) rec->begin("attn_decode", 2.0 * n_ctx_est * kvd * 4 + 2.0 * qd * 4);
+        TMG_HIP(launch_attn(aa, s));
+        if (rec) rec->end();
+
+        GemvArgs oa{};
+        oa.W = ly.o;
+        oa.out = H;
+        oa.in = qd;
+        oa.x = m->attn_out;
+        oa.y = m->x;
+        if (rec) rec->begin("gemv_o_resid", (double)H * qd * 2 + qd * 4.0 + H * 8.0);
+        TMG_HIP(launch_gemv(PRO_PLAIN, EPI_RESID, oa, s));
+        if (rec) rec->end();
+
+        GemvArgs ga{};
+        ga.W = ly.gu;
+        ga.out = 2 * I;
+        ga.in = H;
+        ga.x = m->x;
+        ga.norm_w = ly.post_norm;
+        ga.eps = m->cfg.rms_norm_eps;
+        ga.y = m->h;
+        if (rec) rec->begin("gemv_gateup_swiglu", 2.0 * I * H * 2 + H * 8.0 + I * 4.0);
+        TMG_HIP(launch_gemv(PRO_NORM, EPI_SWIGLU, ga, s));
+        if (rec) rec->end();
+
+        GemvArgs da{};
+        da.W = ly.down;
+        da.out = H;
+        da.in = I;
+        da.x = m->h;
+        da.y = m->x;
+        if (rec) rec->begin("gemv_down_resid", (double)H * I * 2 + I * 4.0 + H * 8.0);
+        TMG_HIP(launch_gemv(PRO_PLAIN, EPI_RESID, da, s));
+        if (rec) rec->end();
+    }
+    GemvArgs la{};
+    la.W = m->lm_head;
+    la.out = m->V;
+    la.in = H;
+    la.x = m->x;
+    la.norm_w = m->final_norm;
+    la.eps = m->cfg.rms_norm_eps;
+    la.y = m->logits;
+    la.argmax_key = mode == SEL_ARGMAX ? &c->st->argmax_key : nullptr;
+    if (rec) rec->begin("gemv_lmhead_argmax", (double)m->V * H * 2 + H * 8.0 + m->V * 4.0);
+    TMG_HIP(launch_gemv(PRO_NORM, EPI_LOGITS, la, s));
+    if (rec) rec->end();
+    if (rec) rec->begin(mode == SEL_ARGMAX ? "finalize" : "sample", mode == SEL_ARGMAX ? 0.0 : m->V * 4.0);
+    int rc = enqueue_select(m, c, mode, 1);
+    if (rec) rec->end();
+    return rc;
+}
+
+int enqueue_select(tmg_model *m, tmg_cache *c, int mode, int advance_pos) {
+    if (mode == SEL_ARGMAX) {
+        FinalizeArgs fa{c->st, c->history, advance_pos, m->V};
+        TMG_HIP(launch_finalize(fa, m->stream));
+        return TMG_OK;
+    }
+    SampleArgs sa{};
+    sa.logits = m->logits;
+    sa.V = m->V;
+    sa.st = c->st;
+    sa.seen = c->seen;
+    sa.seen_rw = c->seen;
+    sa.cand = mode == SEL_FULL ? nullptr : c->cand;
+    sa.history = c->history;
+    sa.greedy = mode == SEL_PENALTY_ARGMAX;
+    sa.advance_pos = advance_pos;
+    TMG_HIP(launch_sample(sa, m->stream));
+    return TMG_OK;
+}
+
+int get_step_graph(tmg_model *m, tmg_cache *c, int mode) {
+    if (c->graphs[mode]) return TMG_OK;
+    TMG_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_decode_step(m, c, nullptr, mode);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(m->stream, &g);
+    if (rc) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    TMG_HIP(e);
+    hipGraphExec_t ex = nullptr;
+    e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        TMG_HIP(e);
+    }
+    c->graph_src[mode] = g;
+    c->graphs[mode] = ex;
+    return TMG_OK;
+}
+
+int set_state(tmg_model *m, tmg_cache *c, int token, bool reset_step) {
+    // one small H2D write of the host-known fields; the step counter and the
+    // argmax key are reset together with the position when asked
+    DevState st{};
+    st.pos = (int)c->len;
+    st.cur_token = token;
+    st.step = 0;
+    st.argmax_key = kArgmaxInit;
+    if (reset_step) {
+        const size_t n = offsetof(DevState, temperature);
+        memcpy(m->pin, &st, n);
+        TMG_HIP(hipMemcpyAsync(c->st, m->pin, n, hipMemcpyHostToDevice, m->stream));
+    } else {
+        int v[2] = {st.pos, st.cur_token};
+        memcpy(m->pin, v, sizeof(v));
+        TMG_HIP(hipMemcpyAsync(c->st, m->pin, sizeof(v), hipMemcpyHostToDevice, m->stream));
+    }
+    return TMG_OK;
+}
+
+// ---------------------------------------------------------------------------
+// prefill (reference Model::forward_seq, src/model.rs:503-590)
+// ---------------------------------------------------------------------------
+
+static int ensure_prefill(tmg_model *m, int T) {
+    if (T <= m->pf_cap) return TMG_OK;
+    int cap = std::max(T, 64);
+    // earlier buffers are released lazily with the model
+    int rc;
+    if ((rc = dev_alloc(m, &m->pf_tokens, cap)) || (rc = dev_alloc(m, &m->pf_x, (size_t)cap * m->H)) ||
+        (rc = dev_alloc(m, &m->pf_q, (size_t)cap * m->qd)) || (rc = dev_alloc(m, &m->pf_hi, (size_t)cap * m->H)) ||
+        (rc = dev_alloc(m, &m->pf_lo, (size_t)cap * m->H)) || (rc = dev_alloc(m, &m->pf_ahi, (size_t)cap * m->qd)) ||
+        (rc = dev_alloc(m, &m->pf_alo, (size_t)cap * m->qd)) || (rc = dev_alloc(m, &m->pf_hhi, (size_t)cap * m->I)) ||
+        (rc = dev_alloc(m, &m->pf_hlo, (size_t)cap * m->I)))
+        return rc;
+    m->pf_cap = cap;
+    return TMG_OK;
+}
+
+// Runs the batched prefill; leaves the last token's logits in m->logits and
+// their argmax in st->argmax_key.
+int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
+    const int T = (int)n;
+    const int H = m->H, I = m->I, qd = m->qd, kvd = m->kvd;
+    hipStream_t s = m->stream;
+    int rc;
+    if ((rc = ensure_prefill(m, T))) return rc;
+    if ((rc = ensure_rope(m, (int)c->len + T + 1))) return rc;
+    if ((rc = pinned(m, (size_t)T * 4 + 64 + (size_t)m->V * 4))) return rc;
+    memcpy(m->pin, tokens, (size_t)T * 4);
+    TMG_HIP(hipMemcpyAsync(m->pf_tokens, m->pin, (size_t)T * 4, hipMemcpyHostToDevice, s));
+    TMG_HIP(launch_embed_gather(m->pf_tokens, T, H, m->embed_bf16, m->embed_f32, m->pf_x, s));
+    const int start = (int)c->len;
+    for (int l = 0; l < m->L; l++) {
+        const tmg_model::Layer &ly = m->layers[l];
+        float *kc = c->k + (size_t)l * c->max_pos * kvd;
+        float *vc = c->v + (size_t)l * c->max_pos * kvd;
+        TMG_HIP(launch_rmsnorm_split(m->pf_x, ly.in_norm, m->cfg.rms_norm_eps, T, H, m->pf_hi, m->pf_lo, s));
+        GemmArgs g{};
+        g.W = ly.qkv;
+        g.Bhi = m->pf_hi;
+        g.Blo = m->pf_lo;
+        g.M = m->qkv_rows;
+        g.N = T;
+        g.K = H;
+        g.rope_cos = m->rope_cos;
+        g.rope_sin = m->rope_sin;
+        g.start = start;
+        g.hd = m->hd;
+        g.nq = m->nq;
+        g.nkv = m->nkv;
+        g.q_out = m->pf_q;
+        g.k_cache = kc;
+        g.v_cache = vc;
+        TMG_HIP(launch_gemm(GEPI_QKV, g, s));
+
+        AttnArgs aa{};
+        aa.q = m->pf_q;
+        aa.k_cache = kc;
+        aa.v_cache = vc;
+        aa.nq = m->nq;
+        aa.nkv = m->nkv;
+        aa.hd = m->hd;
+        aa.T = T;
+        aa.start = start;
+        aa.scale = 1.0f / sqrtf((float)m->hd);
+        aa.nsplit = 1;
+        aa.min_chunk = 1;
+        aa.out_hi = m->pf_ahi;
+        aa.out_lo = m->pf_alo;
+        TMG_HIP(launch_attn(aa, s));
+
+        GemmArgs o{};
+        o.W = ly.o;
+        o.Bhi = m->pf_ahi;
+        o.Blo = m->pf_alo;
+        o.M = H;
+        o.N = T;
+        o.K = qd;
+        o.y = m->pf_x;
+        TMG_HIP(launch_gemm(GEPI_RESID, o, s));
+
+        TMG_HIP(launch_rmsnorm_split(m->pf_x, ly.post_norm, m->cfg.rms_norm_eps, T, H, m->pf_hi, m->pf_lo, s));
+        GemmArgs gu{};
+        gu.W = ly.gu;
+        gu.Bhi = m->pf_hi;
+        gu.Blo = m->pf_lo;
+        gu.M = 2 * I;
+        gu.N = T;
+        gu.K = H;
+        gu.h_hi = m->pf_hhi;
+        gu.h_lo = m->pf_hlo;
+        TMG_HIP(launch_gemm(GEPI_SWIGLU, gu, s));
+
+        GemmArgs d{};
+        d.W = ly.down;
+        d.Bhi = m->pf_hhi;
+        d.Blo = m->pf_hlo;
+        d.M = H;
+        d.N = T;
+        d.K = I;
+        d.y = m->pf_x;
+        TMG_HIP(launch_gemm(GEPI_RESID, d, s));
+    }
+    // final norm of the last row (batch association) + lm_head + argmax
+    GemvArgs la{};
+    la.W = m->lm_head;
+    la.out = m->V;
+    la.in = H;
+    la.x = m->pf_x + (size_t)(T - 1) * H;
+    la.norm_w = m->final_norm;
+    la.eps = m->cfg.rms_norm_eps;
+    la.y = m->logits;
+    la.argmax_key = &c->st->argmax_key;
+    TMG_HIP(launch_gemv(PRO_NORM_BATCH, EPI_LOGITS, la, s));
+    c->len += (uint32_t)T;
+    // the device position follows the host mirror after a prefill
+    memcpy((char *)m->pin + ((size_t)T * 4 + 63) / 64 * 64, &c->len, 4);
+    TMG_HIP(hipMemcpyAsync(&c->st->pos, (char *)m->pin + ((size_t)T * 4 + 63) / 64 * 64, 4, hipMemcpyHostToDevice, s));
+    return TMG_OK;
+}
+
+}  // namespace tmg
+
+using namespace tmg;
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+
+extern "C" int tmg_model_load(const char *path, int device, tmg_model **out) {
+    clear_error();
+    if (!path || !out) return set_error(TMG_E_INVALID, "null argument");
+    *out = nullptr;
+    tmg_model *m = new tmg_model();
+    SafeTensorsFile f;
+    int rc = validate_files(m, path, &f);
+    if (rc) {
+        delete m;
+        return rc;
+    }
+    int ndev = 0;
+    hipError_t e = hipGetDeviceCount(&ndev);
+    if (e != hipSuccess || ndev == 0) {
+        delete m;
+        return set_error(TMG_E_DEVICE, "no HIP device available");
+    }
+    if (device < 0 || device >= ndev) {
+        delete m;
+        return set_error(TMG_E_INVALID, "device index out of range");
+    }
+    m->device = device;
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
+        model_release(m);
+        return set_error(TMG_E_DEVICE, "cannot create a HIP stream on the device");
+    }
+    rc = load_model(m, f);
+    if (rc) {
+        std::string msg = tmg_last_error();
+        model_release(m);
+        return set_error(rc, msg);
+    }
+    *out = m;
+    return TMG_OK;
+}
+
+extern "C" void tmg_model_free(tmg_model *m) { model_release(m); }
+
+extern "C" int tmg_model_config(const tmg_model *m, tmg_config *out) {
+    if (!m || !out) return set_error(TMG_E_INVALID, "null argument");
+    *out = m->cfg;
+    return TMG_OK;
+}
+
+extern "C" int tmg_cache_new(tmg_model *m, uint32_t max_pos, tmg_cache **out) {
+    clear_error();
+    if (!m || !out || max_pos == 0) return set_error(TMG_E_INVALID, "bad argument to tmg_cache_new");
+    *out = nullptr;
+    (void)hipSetDevice(m->device);
+    tmg_cache *c = new tmg_cache();
+    c->model = m;
+    c->max_pos = max_pos;
+    const size_t n = (size_t)m->L * max_pos * m->kvd;
+    int rc = TMG_OK;
+    void *k = nullptr, *v = nullptr, *st = nullptr, *hist = nullptr;
+    if (hipMalloc(&k, n * 4) != hipSuccess || hipMalloc(&v, n * 4) != hipSuccess ||
+        hipMalloc(&st, sizeof(DevState)) != hipSuccess || hipMalloc(&hist, ((size_t)max_pos + 2) * 4) != hipSuccess)
+        rc = set_error(TMG_E_NOMEM, "KV cache allocation of " + std::to_string(2 * n * 4) + " bytes failed");
+    c->k = (float *)k;
+    c->v = (float *)v;
+    c->st = (DevState *)st;
+    c->history = (int *)hist;
+    const size_t seen_words = ((size_t)m->V + 31) / 32;
+    const size_t nslices = ((size_t)m->V + kSampleSlice - 1) / kSampleSlice;
+    void *seen = nullptr, *cand = nullptr;
+    if (!rc && (hipMalloc(&seen, seen_words * 4) != hipSuccess ||
+                hipMalloc(&cand, nslices * kSampleMaxK * 8) != hipSuccess))
+        rc = set_error(TMG_E_NOMEM, "sampler buffer allocation failed");
+    c->seen = (unsigned *)seen;
+    c->cand = (unsigned long long *)cand;
+    if (!rc && hipMemset(c->seen, 0, seen_words * 4) != hipSuccess) rc = set_error(TMG_E_DEVICE, "hipMemset failed");
+    if (!rc) {
+        DevState init{};
+        init.argmax_key = kArgmaxInit;
+        init.temperature = 0.0f;
+        init.top_p = 1.0f;
+        init.penalty = 1.0f;
+        if (hipMemcpy(c->st, &init, sizeof(init), hipMemcpyHostToDevice) != hipSuccess)
+            rc = set_error(TMG_E_DEVICE, "state upload failed");
+    }
+    if (!rc) rc = ensure_rope(m, (int)max_pos + 1);
+    if (!rc) rc = set_state(m, c, 0, true);
+    if (!rc && hipStreamSynchronize(m->stream) != hipSuccess) rc = set_error(TMG_E_DEVICE, "stream sync failed");
+    if (rc) {
+        tmg_cache_free(c);
+        return rc;
+    }
+    *out = c;
+    return TMG_OK;
+}
+
+extern "C" void tmg_cache_free(tmg_cache *c) {
+    if (!c) return;
+    (void)hipSetDevice(c->model->device);
+    (void)hipStreamSynchronize(c->model->stream);
+    for (int i = 0; i < 4; i++) {
+        if (c->graphs[i]) (void)hipGraphExecDestroy(c->graphs[i]);
+        if (c->graph_src[i]) (void)hipGraphDestroy(c->graph_src[i]);
+    }
+    (void)hipFree(c->seen);
+    (void)hipFree(c->cand);
+    (void)hipFree(c->k);
+    (void)hipFree(c->v);
+    (void)hipFree(c->st);
+    (void)hipFree(c->history);
+    delete c;
+}
+
+extern "C" int tmg_cache_len(const tmg_cache *c, uint32_t layer, uint32_t *len) {
+    if (!c || !len) return set_error(TMG_E_INVALID, "null argument");
+    if (layer >= (uint32_t)c->model->L) return set_error(TMG_E_INVALID, "layer index out of range");
+    *len = c->len;
+    return TMG_OK;
+}
+
+extern "C" int tmg_cache_reset(tmg_cache *c) {
+    if (!c) return set_error(TMG_E_INVALID, "null argument");
+    (void)hipSetDevice(c->model->device);
+    c->len = 0;
+    int rc = set_state(c->model, c, 0, true);
+    if (rc) return rc;
+    TMG_HIP(hipStreamSynchronize(c->model->stream));
+    return TMG_OK;
+}
+
+extern "C" int tmg_cache_read(const tmg_cache *c, uint32_t layer, float *keys, float *values) {
+    if (!c) return set_error(TMG_E_INVALID, "null argument");
+    tmg_model *m = c->model;
+    if (layer >= (uint32_t)m->L) return set_error(TMG_E_INVALID, "layer index out of range");
+    (void)hipSetDevice(m->device);
+    TMG_HIP(hipStreamSynchronize(m->stream));
+    const size_t off = (size_t)layer * c->max_pos * m->kvd, bytes = (size_t)c->len * m->kvd * 4;
+    if (keys && bytes) TMG_HIP(hipMemcpy(keys, c->k + off, bytes, hipMemcpyDeviceToHost));
+    if (values && bytes) TMG_HIP(hipMemcpy(values, c->v + off, bytes, hipMemcpyDeviceToHost));
+    return TMG_OK;
+}
+
+static int fetch_logits(tmg_model *m, float *logits) {
+    if (logits) {
+        TMG_HIP(hipMemcpyAsync(m->pin, m->logits, (size_t)m->V * 4, hipMemcpyDeviceToHost, m->stream));
+        TMG_HIP(hipStreamSynchronize(m->stream));
+        memcpy(logits, m->pin, (size_t)m->V * 4);
+    } else {
+        TMG_HIP(hipStreamSynchronize(m->stream));
+    }
+    return TMG_OK;
+}
+
+extern "C" int tmg_forward_token(tmg_model *m, tmg_cache *c, uint32_t token, float *logits) {
+    clear_error();
+    if (!m || !c || c->model != m) return set_error(TMG_E_INVALID, "bad model/cache handle");
+    if (token >= (uint32_t)m->V) return set_error(TMG_E_INVALID, "token id " + std::to_string(token) + " out of range");
+    if (c->len >= c->max_pos) return set_error(TMG_E_CAPACITY, "KV cache full (max_pos " + std::to_string(c->max_pos) + ")");
+    (void)hipSetDevice(m->device);
+    int rc;
+    if ((rc = get_step_graph(m, c, SEL_ARGMAX))) return rc;
+    if ((rc = set_state(m, c, (int)token, false))) return rc;
+    TMG_HIP(hipGraphLaunch(c->graphs[SEL_ARGMAX], m->stream));
+    c->len += 1;
+    return fetch_logits(m, logits);
+}
+
+extern "C" int tmg_forward_seq(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n, float *last_logits) {
+    clear_error();
+    if (!m || !c || c->model != m || (!tokens && n)) return set_error(TMG_E_INVALID, "bad argument");
+    if (n == 0) return set_error(TMG_E_EMPTY, "empty prompt");
+    for (size_t i = 0; i < n; i++)
+        if (tokens[i] >= (uint32_t)m->V) return set_error(TMG_E_INVALID, "token id out of range");
+    if ((uint64_t)c->len + n > c->max_pos) return set_error(TMG_E_CAPACITY, "KV cache full");
+    (void)hipSetDevice(m->device);
+    int rc = run_prefill(m, c, tokens, n);
+    if (rc) return rc;
+    return fetch_logits(m, last_logits);
+}
+
+extern "C" int tmg_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n, float *last_logits) {
+    if (n == 0) return set_error(TMG_E_EMPTY, "empty prompt");
+    return tmg_forward_seq(m, c, tokens, n, last_logits);
+}
+
+extern "C" int tmg_gemv_bf16(const uint16_t *w, const float *x, float *y, uint32_t out, uint32_t in, void *stream) {
+    if (!w || !x || !y || out == 0 || in == 0) return set_error(TMG_E_INVALID, "bad argument to tmg_gemv_bf16");
+    if (in % 8 != 0 || in > 16384) return set_error(TMG_E_INVALID, "in must be a multiple of 8 and <= 16384");
+    if (((uintptr_t)w & 15) || ((uintptr_t)x & 15)) return set_error(TMG_E_INVALID, "W and x must be 16-byte aligned");
+    GemvArgs a{};
+    a.W = w;
+    a.out = (int)out;
+    a.in = (int)in;
+    a.x = x;
+    a.y = y;
+    TMG_HIP(launch_gemv(PRO_PLAIN, EPI_STORE, a, (hipStream_t)stream));
+    return TMG_OK;
+}
+
+extern "C" int tmg_decode_greedy(tmg_model *m, tmg_cache *c, uint32_t token, uint32_t n_steps, uint32_t *tokens_out,
+                                 float *ms) {
+    clear_error();
+    if (!m || !c || c->model != m) return set_error(TMG_E_INVALID, "bad model/cache handle");
+    if (token >= (uint32_t)m->V) return set_error(TMG_E_INVALID, "token id out of range");
+    if ((uint64_t)c->len + n_steps > c->max_pos) return set_error(TMG_E_CAPACITY, "KV cache full");
+    (void)hipSetDevice(m->device);
+    int rc;
+    if ((rc = get_step_graph(m, c, SEL_ARGMAX))) return rc;
+    if ((rc = set_state(m, c, (int)token, true))) return rc;
+    hipEvent_t e0, e1;
+    TMG_HIP(hipEventCreate(&e0));
+    TMG_HIP(hipEventCreate(&e1));
+    TMG_HIP(hipEventRecord(e0, m->stream));
+    for (uint32_t i = 0; i < n_steps; i++) TMG_HIP(hipGraphLaunch(c->graphs[SEL_ARGMAX], m->stream));
+    TMG_HIP(hipEventRecord(e1, m->stream));
+    TMG_HIP(hipEventSynchronize(e1));
+    float el = 0.f;
+    TMG_HIP(hipEventElapsedTime(&el, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    c->len += n_steps;
+    if (ms) *ms = el;
+    if (tokens_out && n_steps) {
+        if ((rc = pinned(m, (size_t)n_steps * 4))) return rc;
+        TMG_HIP(hipMemcpy(m->pin, c->history, (size_t)n_steps * 4, hipMemcpyDeviceToHost));
+        memcpy(tokens_out, m->pin, (size_t)n_steps * 4);
+    }
+    return TMG_OK;
+}
+
+extern "C" int tmg_profile_decode_step(tmg_model *m, tmg_cache *c, uint32_t token, tmg_kernel_record *records,
+                                       size_t cap, size_t *n_records) {
+    clear_error();
+    if (!m || !c || c->model != m) return set_error(TMG_E_INVALID, "bad model/cache handle");
+    if (token >= (uint32_t)m->V) return set_error(TMG_E_INVALID, "token id out of range");
+    if (c->len >= c->max_pos) return set_error(TMG_E_CAPACITY, "KV cache full");
+    (void)hipSetDevice(m->device);
+    int rc;
+    if ((rc = set_state(m, c, (int)token, true))) return rc;
+    LaunchRecorder rec{m->stream, {}, {}};
+    rc = enqueue_decode_step(m, c, &rec, SEL_ARGMAX);
+    TMG_HIP(hipStreamSynchronize(m->stream));
+    c->len += 1;
+    size_t n = rec.recs.size();
+    for (size_t i = 0; i < n && i < cap; i++) {
+        float el = 0.f;
+        (void)hipEventElapsedTime(&el, rec.evs[2 * i], rec.evs[2 * i + 1]);
+        rec.recs[i].ms = el;
+        if (records) records[i] = rec.recs[i];
+    }
+    for (auto e : rec.evs) (void)hipEventDestroy(e);
+    if (n_records) *n_records = std::min(n, cap);
+    return rc;
+}

@@ -1,0 +1,97 @@
+// Device-resident model and KV cache.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <vector>
+
+#include "../kernels/kernels.hpp"
+#include "common.hpp"
+
+struct tmg_model {
+    tmg_config cfg{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int H = 0, L = 0, nq = 0, nkv = 0, hd = 0, I = 0, V = 0, qd = 0, kvd = 0, qkv_rows = 0;
+
+    struct Layer {
+        uint16_t *qkv = nullptr;   // [qkv_rows, H]: rows (j, j+hd/2) of every q/k/v head adjacent
+        uint16_t *o = nullptr;     // [H, qd]
+        uint16_t *gu = nullptr;    // [2I, H]: gate row p at 2p, up row p at 2p+1
+        uint16_t *down = nullptr;  // [H, I]
+        float *in_norm = nullptr, *post_norm = nullptr;  // [H]
+    };
+    std::vector<Layer> layers;
+    float *final_norm = nullptr;
+    uint16_t *embed_bf16 = nullptr;  // [V, H] when the file stores BF16
+    float *embed_f32 = nullptr;      // [V, H] otherwise (converted like the reference)
+    uint16_t *lm_head = nullptr;     // [V, H]; the embedding when tied
+
+    // RoPE cos/sin tables [npos][hd/2], built on the host with libm exactly
+    // like the reference's Rope (src/tensor.rs:1005-1023) and uploaded.
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    int rope_npos = 0;
+
+    // decode scratch
+    float *x = nullptr, *q = nullptr, *attn_out = nullptr, *h = nullptr, *logits = nullptr;
+    float *attn_part = nullptr, *attn_ml = nullptr;
+    unsigned *attn_counter = nullptr;
+    int attn_nsplit = 1, attn_min_chunk = 16;
+
+    // prefill scratch, grown on demand
+    int pf_cap = 0;
+    int *pf_tokens = nullptr;
+    float *pf_x = nullptr, *pf_q = nullptr;
+    uint16_t *pf_hi = nullptr, *pf_lo = nullptr, *pf_ahi = nullptr, *pf_alo = nullptr, *pf_hhi = nullptr,
+             *pf_hlo = nullptr;
+
+    // pinned host staging
+    void *pin = nullptr;
+    size_t pin_bytes = 0;
+
+    std::vector<void *> allocs;
+};
+
+struct tmg_cache {
+    tmg_model *model = nullptr;
+    uint32_t max_pos = 0;
+    float *k = nullptr, *v = nullptr;  // [L][max_pos][kvd]
+    tmg::DevState *st = nullptr;       // device
+    int *history = nullptr;            // device, max_pos + 2 entries
+    uint32_t len = 0;                  // host mirror of st->pos
+    unsigned *seen = nullptr;          // bitmap of generated ids (repetition penalty)
+    unsigned long long *cand = nullptr;  // sampler candidates
+    // one captured step graph per token-selection mode (tmg::SelectMode)
+    hipGraphExec_t graphs[4] = {nullptr, nullptr, nullptr, nullptr};
+    hipGraph_t graph_src[4] = {nullptr, nullptr, nullptr, nullptr};
+};
+
+namespace tmg {
+
+// Per-launch timing hook used by tmg_profile_decode_step.
+struct LaunchRecorder {
+    hipStream_t stream;
+    std::vector<tmg_kernel_record> recs;
+    std::vector<hipEvent_t> evs;
+    void begin(const char *name, double bytes);
+    void end();
+};
+
+// How a step turns logits into the next token.
+enum SelectMode {
+    SEL_ARGMAX = 0,          // greedy, argmax fused into the lm_head GEMV
+    SEL_PENALTY_ARGMAX = 1,  // greedy after the repetition penalty
+    SEL_TOPK = 2,            // temperature sampling with 0 < top_k <= kSampleMaxK
+    SEL_FULL = 3,            // temperature sampling over the whole vocabulary
+};
+
+int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mode);
+int enqueue_select(tmg_model *m, tmg_cache *c, int mode, int advance_pos);
+int get_step_graph(tmg_model *m, tmg_cache *c, int mode);
+int set_state(tmg_model *m, tmg_cache *c, int token, bool reset_step);
+int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n);
+int ensure_rope(tmg_model *m, int npos);
+int pinned(tmg_model *m, size_t bytes);
+
+}  // namespace tmg

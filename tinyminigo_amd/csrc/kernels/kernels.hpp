@@ -1,0 +1,142 @@
+// Launch interface of the gfx950 kernels.  Host code includes this header;
+// the kernels themselves live in decode.hip / prefill.hip / sample.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace tmg {
+
+// Packed argmax key: (orderable f32 bits << 32) | (0xFFFFFFFF - index), so a
+// 64-bit atomicMax keeps the largest value and, among equal values, the
+// lowest index -- the tie rule of the reference argmax (src/tensor.rs:1063).
+// The initial key stands for (-inf, index 0): all -inf/NaN logits give 0.
+constexpr unsigned long long kArgmaxInit = (0x007FFFFFull << 32) | 0xFFFFFFFFull;
+
+// Per-cache device state read and advanced by the captured decode step.
+struct DevState {
+    int pos;                        // cache length = write position of the next token
+    int cur_token;                  // input token of the next step
+    int step;                       // index into the generated-token history
+    int pad;
+    unsigned long long argmax_key;  // running argmax of the current logits
+    // sampling parameters of the running generate call (GenParams,
+    // src/model.rs:597-604), read by the sampling kernels
+    float temperature;
+    int top_k;   // 0 or >= vocab: no top-k
+    float top_p;
+    float penalty;
+    unsigned long long seed;
+};
+
+enum GemvPro { PRO_PLAIN = 0, PRO_NORM = 1, PRO_NORM_BATCH = 2, PRO_EMBED_NORM = 3 };
+enum GemvEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3, EPI_LOGITS = 4 };
+
+struct GemvArgs {
+    const uint16_t *W;  // [out, in] BF16 rows (pair-interleaved for SWIGLU/QKV)
+    int out, in;
+    const float *x;       // activation (PRO_PLAIN) or residual stream (PRO_NORM*)
+    const float *norm_w;  // [in] f32 RMSNorm weight
+    float eps;
+    // PRO_EMBED_NORM: x is gathered from the embedding row of *token
+    const int *token;
+    const uint16_t *embed_bf16;  // [V, in] (one of the two is set)
+    const float *embed_f32;
+    float *x_store;  // block 0 stores the gathered row (the residual stream)
+    // epilogue
+    float *y;  // STORE/LOGITS: y[out]; RESID: y[out] += ; SWIGLU: y[out/2]
+    // EPI_QKV
+    const float *rope_cos, *rope_sin;  // [pos][hd/2]
+    const int *pos;
+    int hd, nq, nkv;
+    float *q_out;            // [nq*hd]
+    float *k_cache, *v_cache;  // layer base, [pos][nkv*hd]
+    // EPI_LOGITS
+    unsigned long long *argmax_key;  // may be null
+};
+
+hipError_t launch_gemv(int pro, int epi, const GemvArgs &a, hipStream_t s);
+
+struct AttnArgs {
+    const float *q;  // [T][nq*hd], RoPE applied
+    const float *k_cache, *v_cache;  // layer base, [pos][nkv*hd]
+    int nq, nkv, hd;
+    int T;            // query rows (1 for decode)
+    int start;        // position of query row 0 (decode: *pos_dev is used when pos_dev != null)
+    const int *pos_dev;
+    float scale;      // 1/sqrt(hd)
+    int nsplit;       // grid.x
+    int min_chunk;    // minimum positions per active split
+    float *part;      // [T][nkv][nsplit][group][hd] partial outputs
+    float *part_ml;   // [T][nkv][nsplit][group][2] (max, sum)
+    unsigned *counter;  // [T][nkv] arrival counters (zero at rest)
+    float *out_f32;   // [T][nq*hd] (decode), or null
+    uint16_t *out_hi, *out_lo;  // [T][nq*hd] split-bf16 output (prefill), or null
+};
+
+hipError_t launch_attn(const AttnArgs &a, hipStream_t s);
+
+struct FinalizeArgs {
+    DevState *st;
+    int *history;  // generated ids, indexed by st->step
+    int advance_pos;  // 1 after a decode step, 0 after prefill
+    int V;            // ids outside [0, V) become 0 before they index anything
+};
+
+hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t s);
+
+// ---- prefill -------------------------------------------------------------
+
+hipError_t launch_embed_gather(const int *tokens, int T, int H, const uint16_t *embed_bf16, const float *embed_f32,
+                               float *x, hipStream_t s);
+
+// Row-wise RMSNorm with the batch association v*(inv*w), written as
+// split-bf16 hi/lo operands for the MFMA GEMM.
+hipError_t launch_rmsnorm_split(const float *x, const float *w, float eps, int T, int H, uint16_t *hi, uint16_t *lo,
+                                hipStream_t s);
+
+enum GemmEpi { GEPI_STORE = 0, GEPI_RESID = 1, GEPI_SWIGLU = 2, GEPI_QKV = 3 };
+
+struct GemmArgs {
+    const uint16_t *W;  // [M, K] BF16
+    const uint16_t *Bhi, *Blo;  // [N, K] split-bf16 activations
+    int M, N, K;
+    // epilogues
+    float *y;  // STORE: [N][M]; RESID: [N][M] +=
+    uint16_t *h_hi, *h_lo;  // SWIGLU: [N][M/2]
+    // QKV
+    const float *rope_cos, *rope_sin;
+    int start;  // position of token 0
+    int hd, nq, nkv;
+    float *q_out;  // [N][nq*hd]
+    float *k_cache, *v_cache;
+};
+
+hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s);
+
+// Copy row `row` of x[T,H] to dst[H] (last prefill row -> decode residual).
+hipError_t launch_copy_row(const float *x, int row, int H, float *dst, hipStream_t s);
+
+// ---- sampling --------------------------------------------------------------
+
+// Largest top_k the device sampler supports, and the per-workgroup slice of
+// the vocabulary the first pass sorts.
+constexpr int kSampleMaxK = 64;
+constexpr int kSampleSlice = 2048;
+
+struct SampleArgs {
+    float *logits;  // [V]; penalized in place like the reference
+    int V;
+    DevState *st;
+    const unsigned *seen;  // bitmap of generated ids (repetition penalty)
+    unsigned *seen_rw;     // same bitmap, updated with the chosen id
+    unsigned long long *cand;  // [nslices][kSampleMaxK] packed (value, id) keys; null selects the full-vocabulary path
+    int *history;
+    int greedy;       // temperature <= 0: argmax of the penalized logits
+    int advance_pos;  // 1 after a decode step, 0 after prefill
+};
+
+hipError_t launch_sample(const SampleArgs &a, hipStream_t s);
+
+}  // namespace tmg

@@ -1,0 +1,272 @@
+"""Python mirror of the reference crate's model API over libtmg's C ABI.
+
+Names and argument meanings follow the reference (src/model.rs, src/config.rs):
+``Model.load``, ``Model.forward_token``, ``Model.prefill``,
+``Model.forward_seq``, ``KvCache`` and ``generate`` with ``GenParams`` /
+``GenOutput``.  Errors raise ``TmgError`` carrying the library's context text
+(the reference returns anyhow errors with the same kind of context).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Callable, List, Optional, Sequence
+
+import numpy as np
+
+from ._lib import (
+    ON_TOKEN, TmgError, check, lib, tmg_config, tmg_gen_params, tmg_kernel_record, tmg_synth_spec,
+)
+
+__all__ = [
+    "ModelConfig", "Model", "KvCache", "GenParams", "GenOutput", "generate", "gemv_bf16",
+    "synth_model", "synth_tokens", "synth_normal_bf16", "synth_normal_f32", "TmgError",
+]
+
+
+def _u32(a: Sequence[int]) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.uint32))
+
+
+def _fptr(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+@dataclass
+class ModelConfig:
+    """ModelConfig (src/config.rs:6-20)."""
+
+    hidden_size: int
+    num_hidden_layers: int
+    num_attention_heads: int
+    num_key_value_heads: int
+    head_dim: int
+    intermediate_size: int
+    rms_norm_eps: float
+    rope_theta: float
+    vocab_size: int
+    eos_token_ids: List[int] = field(default_factory=list)
+    bos_token_id: int = 0
+    tied_lm_head: bool = False
+
+    @classmethod
+    def _from_c(cls, c: tmg_config) -> "ModelConfig":
+        return cls(
+            hidden_size=c.hidden_size, num_hidden_layers=c.num_hidden_layers,
+            num_attention_heads=c.num_attention_heads, num_key_value_heads=c.num_key_value_heads,
+            head_dim=c.head_dim, intermediate_size=c.intermediate_size, rms_norm_eps=c.rms_norm_eps,
+            rope_theta=c.rope_theta, vocab_size=c.vocab_size,
+            eos_token_ids=[c.eos_token_ids[i] for i in range(c.n_eos)], bos_token_id=c.bos_token_id,
+            tied_lm_head=bool(c.tied_lm_head),
+        )
+
+    @classmethod
+    def load(cls, path: str) -> "ModelConfig":
+        """ModelConfig::load (src/config.rs:112-172)."""
+        c = tmg_config()
+        check(lib.tmg_config_load(path.encode(), C.byref(c)))
+        return cls._from_c(c)
+
+
+class Model:
+    """Model (src/model.rs:338-591): weights resident in HBM on one GPU."""
+
+    def __init__(self, handle: C.c_void_p):
+        self._h = handle
+        c = tmg_config()
+        check(lib.tmg_model_config(self._h, C.byref(c)))
+        self.config = ModelConfig._from_c(c)
+
+    @classmethod
+    def load(cls, path: str, device: int = 0) -> "Model":
+        """Model::load (src/model.rs:384-389)."""
+        h = C.c_void_p()
+        check(lib.tmg_model_load(str(path).encode(), device, C.byref(h)))
+        return cls(h)
+
+    def close(self) -> None:
+        if self._h:
+            lib.tmg_model_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def new_cache(self, max_pos: int) -> "KvCache":
+        return KvCache(self, max_pos)
+
+    def forward_token(self, token: int, cache: "KvCache", want_logits: bool = True) -> Optional[np.ndarray]:
+        """Model::forward_token (src/model.rs:392-491)."""
+        out = np.empty(self.config.vocab_size, np.float32) if want_logits else None
+        check(lib.tmg_forward_token(self._h, cache._h, int(token), _fptr(out)))
+        return out
+
+    def forward_seq(self, tokens: Sequence[int], cache: "KvCache", want_logits: bool = True) -> Optional[np.ndarray]:
+        """Model::forward_seq (src/model.rs:503-590)."""
+        t = _u32(tokens)
+        out = np.empty(self.config.vocab_size, np.float32) if want_logits else None
+        check(lib.tmg_forward_seq(self._h, cache._h, t.ctypes.data_as(C.POINTER(C.c_uint32)), t.size, _fptr(out)))
+        return out
+
+    def prefill(self, tokens: Sequence[int], cache: "KvCache") -> np.ndarray:
+        """Model::prefill (src/model.rs:494-499)."""
+        t = _u32(tokens)
+        out = np.empty(self.config.vocab_size, np.float32)
+        check(lib.tmg_prefill(self._h, cache._h, t.ctypes.data_as(C.POINTER(C.c_uint32)), t.size, _fptr(out)))
+        return out
+
+    # -- measurement helpers (no reference counterpart) ----------------------
+
+    def decode_greedy(self, token: int, n_steps: int, cache: "KvCache"):
+        """n_steps device-resident greedy steps; returns (tokens, elapsed ms)."""
+        toks = np.empty(max(n_steps, 1), np.uint32)
+        ms = C.c_float()
+        check(lib.tmg_decode_greedy(self._h, cache._h, int(token), int(n_steps),
+                                    toks.ctypes.data_as(C.POINTER(C.c_uint32)), C.byref(ms)))
+        return toks[:n_steps], ms.value
+
+    def profile_decode_step(self, token: int, cache: "KvCache"):
+        """One decode step launched kernel by kernel with HIP events around each
+        launch: list of (name, algorithmic bytes, ms)."""
+        recs = (tmg_kernel_record * 4096)()
+        n = C.c_size_t()
+        check(lib.tmg_profile_decode_step(self._h, cache._h, int(token), recs, 4096, C.byref(n)))
+        return [(recs[i].name.decode(), recs[i].bytes, recs[i].ms) for i in range(n.value)]
+
+
+class KvCache:
+    """KvCache (src/model.rs:250-332) as a preallocated HBM slab of max_pos rows."""
+
+    def __init__(self, model: Model, max_pos: int):
+        self.model = model
+        self.max_pos = max_pos
+        h = C.c_void_p()
+        check(lib.tmg_cache_new(model._h, int(max_pos), C.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if self._h:
+            lib.tmg_cache_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def len(self, layer: int) -> int:
+        v = C.c_uint32()
+        check(lib.tmg_cache_len(self._h, layer, C.byref(v)))
+        return v.value
+
+    def total_len(self) -> int:
+        return self.len(0)
+
+    def reset(self) -> None:
+        check(lib.tmg_cache_reset(self._h))
+
+    def _read(self, layer: int):
+        cfg = self.model.config
+        kvd = cfg.num_key_value_heads * cfg.head_dim
+        n = self.len(layer)
+        k = np.empty(n * kvd, np.float32)
+        v = np.empty(n * kvd, np.float32)
+        check(lib.tmg_cache_read(self._h, layer, _fptr(k), _fptr(v)))
+        return k, v
+
+    def keys_flat(self, layer: int) -> np.ndarray:
+        return self._read(layer)[0]
+
+    def values_flat(self, layer: int) -> np.ndarray:
+        return self._read(layer)[1]
+
+
+@dataclass
+class GenParams:
+    """GenParams (src/model.rs:597-604)."""
+
+    max_tokens: int = 64
+    temperature: float = 0.0
+    top_k: int = 0
+    top_p: float = 1.0
+    repetition_penalty: float = 1.0
+    seed: int = 42
+
+
+@dataclass
+class GenOutput:
+    """GenOutput (src/model.rs:606-611)."""
+
+    tokens: List[int]
+    logits_first_step: np.ndarray
+    prefill_secs: float
+
+
+def generate(model: Model, prompt_tokens: Sequence[int], params: GenParams,
+             on_token: Optional[Callable[[int], None]] = None) -> GenOutput:
+    """generate (src/model.rs:614-663)."""
+    t = _u32(prompt_tokens)
+    p = tmg_gen_params(params.max_tokens, params.temperature, params.top_k, params.top_p,
+                       params.repetition_penalty, params.seed)
+    out = np.empty(max(params.max_tokens, 1), np.uint32)
+    first = np.empty(model.config.vocab_size, np.float32)
+    n_out = C.c_size_t()
+    secs = C.c_float()
+    err: List[BaseException] = []
+
+    def _cb(tok, _user):
+        if on_token is not None and not err:
+            try:
+                on_token(int(tok))
+            except BaseException as e:  # surfaced after the call returns
+                err.append(e)
+
+    cb = ON_TOKEN(_cb)
+    check(lib.tmg_generate(model._h, t.ctypes.data_as(C.POINTER(C.c_uint32)), t.size, C.byref(p), cb, None,
+                           out.ctypes.data_as(C.POINTER(C.c_uint32)), out.size, C.byref(n_out), _fptr(first),
+                           C.byref(secs)))
+    if err:
+        raise err[0]
+    return GenOutput(tokens=[int(x) for x in out[:n_out.value]], logits_first_step=first,
+                     prefill_secs=secs.value)
+
+
+def gemv_bf16(w_dev: int, x_dev: int, y_dev: int, out: int, in_: int, stream: int = 0) -> None:
+    """tensor::matmul_w (src/tensor.rs:315-338) on device pointers."""
+    check(lib.tmg_gemv_bf16(C.c_void_p(w_dev), C.c_void_p(x_dev), C.c_void_p(y_dev), out, in_,
+                            C.c_void_p(stream)))
+
+
+# -- synthetic inputs ---------------------------------------------------------
+
+def synth_model(directory: str, *, hidden_size: int, num_hidden_layers: int, num_attention_heads: int,
+                num_key_value_heads: int, head_dim: int, intermediate_size: int, vocab_size: int,
+                rms_norm_eps: float, rope_theta: float, tied_lm_head: bool, seed: int,
+                stddev: float = 0.02) -> str:
+    """Write <directory>/model.safetensors + config.json; returns the model path."""
+    spec = tmg_synth_spec(hidden_size, num_hidden_layers, num_attention_heads, num_key_value_heads, head_dim,
+                          intermediate_size, vocab_size, rms_norm_eps, rope_theta, int(tied_lm_head), seed, stddev)
+    check(lib.tmg_synth_model(str(directory).encode(), C.byref(spec)))
+    return str(directory) + "/model.safetensors"
+
+
+def synth_tokens(seed: int, n: int, vocab: int) -> np.ndarray:
+    out = np.empty(max(n, 1), np.uint32)
+    check(lib.tmg_synth_tokens(seed, n, vocab, out.ctypes.data_as(C.POINTER(C.c_uint32))))
+    return out[:n]
+
+
+def synth_normal_bf16(seed: int, name: str, n: int, stddev: float) -> np.ndarray:
+    out = np.empty(max(n, 1), np.uint16)
+    check(lib.tmg_synth_normal_bf16(seed, name.encode(), n, stddev, out.ctypes.data_as(C.POINTER(C.c_uint16))))
+    return out[:n]
+
+
+def synth_normal_f32(seed: int, name: str, n: int, stddev: float) -> np.ndarray:
+    out = np.empty(max(n, 1), np.float32)
+    check(lib.tmg_synth_normal_f32(seed, name.encode(), n, stddev, out.ctypes.data_as(C.POINTER(C.c_float))))
+    return out[:n]
