@@ -1,0 +1,200 @@
+#!/usr/bin/env python3
+"""Decode/prefill benchmark of the TinyMiniGo decode path on one MI355X.
+
+Workload (default): the 1B-class MiniCPM5-shaped synthetic model (hidden
+2048, 24 layers, 16/8 heads, head_dim 128, SwiGLU 6144, vocab 73448, untied
+lm_head, BF16 N(0, 0.02) weights from seed 3), a 64-token prompt (seed 4),
+batched prefill, then greedy decode.  A step is one decode token: the whole
+forward_token (24 layers + lm_head) plus the argmax that picks the next id,
+replayed from a captured hipGraph with inputs resident in HBM.
+
+    python bench.py [--gpus 1] [--steps 256] [--warmup 16]
+
+Prints ONE JSON line.  `value` = decode tokens/s over the timed steps;
+`roofline` = the dominant kernel's algorithmic HBM bytes per launch over its
+average launch time (HIP events on the model's stream); `cpu_baseline` = the
+CPU oracle (C restatement of the reference Rust path, reference threading)
+timed on this host on a bounded sample of the same decode.
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+METRIC = "decode tok/s + % HBM roofline (1B-class bf16, 1 MI355X); prefill tok/s"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(path, prompt, n_ctx0, seconds):
+    """The oracle decoding the same model on this host's cores: one prefill
+    of the prompt, then decode steps until about `seconds` have passed."""
+    from oracle import oracle as O
+    m = O.OracleModel.load(path)
+    cache = m.new_cache()
+    t0 = time.perf_counter()
+    logits = m.prefill(prompt, cache)
+    prefill_s = time.perf_counter() - t0
+    n, t0 = 0, time.perf_counter()
+    tok = int(O.argmax(logits))
+    while True:
+        logits = m.forward_token(tok, cache)
+        tok = int(O.argmax(logits))
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 256:
+            break
+    threads = max(1, O.lib.om_num_threads() // 4)
+    return {
+        "value": round(n / el, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+        "sample": (f"oracle (C restatement of the reference CPU path, GEMV on max(1,ncores/4)={threads} threads of "
+                   f"{os.cpu_count()} on '{cpu_model()}', AVX2={bool(O.lib.om_uses_avx2())}): {n} greedy decode "
+                   f"steps after a {len(prompt)}-token prefill ({len(prompt) / prefill_s:.1f} prefill tok/s)"),
+        "prefill_tok_s": round(len(prompt) / prefill_s, 2),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prefill-reps", type=int, default=5)
+    ap.add_argument("--profile-steps", type=int, default=8)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--model-dir", default=os.environ.get("TMG_MODEL_DIR",
+                                                           os.path.join(tempfile.gettempdir(), "tmg_models")))
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build runs the decode path on a single MI355X "
+              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+
+    import tinyminigo_amd as T
+    from tinyminigo_amd import workloads as W
+
+    wl = W.ONE_B
+    t0 = time.perf_counter()
+    path = W.ensure_model(wl, args.model_dir)
+    log(f"model ready at {path} ({time.perf_counter() - t0:.1f}s)")
+    prompt = [int(t) for t in wl.prompt()]
+    K, Wm = args.steps, args.warmup
+    m = T.Model.load(path)
+    log("model loaded")
+
+    # prefill tok/s: median over repetitions on fresh caches
+    pf = []
+    for _ in range(args.prefill_reps):
+        c = T.KvCache(m, wl.prompt_len + K + Wm + 8)
+        t = time.perf_counter()
+        logits = m.forward_seq(prompt, c, want_logits=False)
+        pf.append(time.perf_counter() - t)
+        c.close()
+    prefill_s = float(np.median(pf))
+    log(f"prefill {wl.prompt_len} tokens: {prefill_s * 1e3:.2f} ms")
+
+    # warmup on its own cache, then the timed steps on a fresh one
+    cache = T.KvCache(m, wl.prompt_len + max(K, Wm) + args.profile_steps + 8)
+    logits = m.forward_seq(prompt, cache)
+    first = int(np.argmax(logits))
+    if Wm:
+        wc = T.KvCache(m, wl.prompt_len + Wm + 8)
+        m.forward_seq(prompt, wc, want_logits=False)
+        m.decode_greedy(first, Wm, wc)
+        wc.close()
+    # torch is not imported: a second HIP runtime in the process would leave
+    # one of the two without a device; synchronize through libtmg's runtime
+    from tinyminigo_amd.hip import synchronize as sync
+    sync()
+    t = time.perf_counter()
+    toks, ev_ms = m.decode_greedy(first, K, cache)
+    sync()
+    wall = time.perf_counter() - t
+    ms_per_step = wall * 1e3 / K
+    n_ctx_avg = wl.prompt_len + (K + 1) / 2.0
+    step_bytes = wl.decode_bytes(int(round(n_ctx_avg)))
+    log(f"decode {K} steps: {wall * 1e3:.1f} ms wall, {ev_ms:.1f} ms events -> {K / wall:.1f} tok/s")
+
+    # per-kernel timing: steps launched kernel by kernel with HIP events
+    per = {}
+    tok = int(toks[-1])
+    for _ in range(args.profile_steps):
+        recs = m.profile_decode_step(tok, cache)
+        for name, nbytes, ms in recs:
+            d = per.setdefault(name, [0, 0.0, 0.0])
+            d[0] += 1
+            d[1] += nbytes
+            d[2] += ms
+    dom = max(per.items(), key=lambda kv: kv[1][2])
+    name, (n, nbytes, ms) = dom
+    kern_ms = ms / n
+    achieved = (nbytes / n) / (kern_ms * 1e-3) / 1e9
+    step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+    kernels = {k: {"launches": v[0], "avg_us": round(v[2] / v[0] * 1e3, 2),
+                   "GB_s": round((v[1] / v[0]) / (v[2] / v[0] * 1e-3) / 1e9, 1) if v[1] else None,
+                   "share": round(v[2] / sum(x[2] for x in per.values()), 3)} for k, v in per.items()}
+
+    cpu = None
+    if not args.no_cpu:
+        log("timing the CPU baseline")
+        cpu = cpu_baseline(path, prompt, wl.prompt_len, args.cpu_seconds)
+
+    out = {
+        "metric": METRIC,
+        "value": round(K / wall, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": Wm,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{wl.name}: {wl.prompt_len}-token prompt, batched prefill, {K} greedy decode steps",
+            "model": "MiniCPM5-shaped Llama (random init)", "hidden": wl.hidden_size,
+            "layers": wl.num_hidden_layers, "heads": wl.num_attention_heads, "kv_heads": wl.num_key_value_heads,
+            "head_dim": wl.head_dim, "intermediate": wl.intermediate_size, "vocab": wl.vocab_size,
+            "global_batch": 1, "seq_len": wl.prompt_len + K, "parallelism": "none (1 GPU)",
+            "arith": "BF16 weights, f32 activations/accumulation, f32 KV cache",
+        },
+        "prefill_tok_s": round(wl.prompt_len / prefill_s, 1),
+        "prefill_ms": round(prefill_s * 1e3, 3),
+        "decode_ms_events": round(ev_ms, 3),
+        "step_hbm": {"bytes_per_token": step_bytes, "n_ctx_avg": n_ctx_avg, "achieved_GB_s": round(step_gbs, 1),
+                     "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "kernel": name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": nbytes / n, "avg_launch_us": round(kern_ms * 1e3, 3)},
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -31,10 +31,3 @@ def oracle_mod():
     from oracle import oracle as O
     return O
 
-
-def gpu_available() -> bool:
-    try:
-        import torch
-        return torch.cuda.is_available()
-    except Exception:
-        return False

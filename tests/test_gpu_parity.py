@@ -49,17 +49,17 @@ def W():
 @pytest.mark.parametrize("out,inp", [(2048, 2048), (6144, 2048), (2048, 6144), (73448, 2048), (24, 64),
                                      (100, 136), (8, 10240), (1, 8), (2560, 4096)])
 def test_gemv_bf16_vs_oracle(T, O, out, inp):
-    import torch
+    from tinyminigo_amd.hip import DeviceBuffer, synchronize
     print(f"gemv {out}x{inp}", flush=True)
     w = T.synth_normal_bf16(2, f"w{out}x{inp}", out * inp, 0.02)
     x = T.synth_normal_f32(2, f"x{inp}", inp, 1.0)
     want = O.matmul_w(x, w, out, inp)
-    wd = torch.from_numpy(w.view(np.int16)).cuda()
-    xd = torch.from_numpy(x).cuda()
-    yd = torch.full((out,), float("nan"), device="cuda")
-    T.gemv_bf16(wd.data_ptr(), xd.data_ptr(), yd.data_ptr(), out, inp)
-    torch.cuda.synchronize()
-    got = yd.cpu().numpy()
+    wd, xd = DeviceBuffer.from_array(w), DeviceBuffer.from_array(x)
+    yd = DeviceBuffer(out * 4)
+    yd.fill_byte(0xFF)  # NaN pattern: every row must be written
+    T.gemv_bf16(wd.addr, xd.addr, yd.addr, out, inp)
+    synchronize()
+    got = yd.to_array(np.float32, out)
     wf = (w.astype(np.uint32) << 16).view(np.float32).astype(np.float64).reshape(out, inp)
     exact = wf @ x.astype(np.float64)
     mag = np.abs(wf) @ np.abs(x.astype(np.float64))
@@ -68,14 +68,13 @@ def test_gemv_bf16_vs_oracle(T, O, out, inp):
 
 
 def test_gemv_small_golden(T):
-    import torch
+    from tinyminigo_amd.hip import DeviceBuffer, synchronize
     z = np.load(os.path.join(GOLD, "gemv_small.npz"))
-    wd = torch.from_numpy(z["w"].view(np.int16)).cuda()
-    xd = torch.from_numpy(z["x"]).cuda()
-    yd = torch.empty(64, device="cuda")
-    T.gemv_bf16(wd.data_ptr(), xd.data_ptr(), yd.data_ptr(), 64, 128)
-    torch.cuda.synchronize()
-    assert np.abs(yd.cpu().numpy() - z["y"]).max() <= 1e-5
+    wd, xd = DeviceBuffer.from_array(z["w"]), DeviceBuffer.from_array(z["x"])
+    yd = DeviceBuffer(64 * 4)
+    T.gemv_bf16(wd.addr, xd.addr, yd.addr, 64, 128)
+    synchronize()
+    assert np.abs(yd.to_array(np.float32, 64) - z["y"]).max() <= 1e-5
 
 
 # --- C0: tiny Llama, prefill + 40 greedy steps -------------------------------
@@ -248,3 +247,19 @@ def test_one_b_prefill_and_greedy(T, O, W, one_b):
     for i, t in enumerate(ref.tokens[:8]):
         close_logits(lg, ref.step_logits[i], f"1B step {i}")
         lg = g.forward_token(t, gc)
+
+
+@pytest.mark.parametrize("max_pos", [64, 512, 1024])
+def test_decode_attention_split_modes(T, O, untied, max_pos):
+    # max_pos 64: one split (direct output); 512: up to 8 splits merged in the
+    # o_proj prologue; 1024: up to 16 splits merged by the combine kernel
+    g, o, wl = untied
+    n = min(max_pos, 700)
+    ids = [int(t) for t in T.synth_tokens(31, n, wl.vocab_size)]
+    gc, oc = T.KvCache(g, max_pos), o.new_cache()
+    close_logits(g.forward_seq(ids[:40], gc), o.forward_seq(ids[:40], oc), "prefill")
+    for i in range(40, n):
+        a, b = g.forward_token(ids[i], gc), o.forward_token(ids[i], oc)
+        if i % 37 == 0 or i == n - 1:
+            close_logits(a, b, f"pos {i}")
+    assert gc.total_len() == n

@@ -257,13 +257,11 @@ static int load_model(tmg_model *m, const SafeTensorsFile &f) {
     if ((rc = dev_alloc(m, &m->x, H)) || (rc = dev_alloc(m, &m->q, qd)) || (rc = dev_alloc(m, &m->attn_out, qd)) ||
         (rc = dev_alloc(m, &m->h, I)) || (rc = dev_alloc(m, &m->logits, V)))
         return rc;
-    m->attn_nsplit = std::max(1, std::min(64, 512 / m->nkv));
-    m->attn_min_chunk = 16;
-    if ((rc = dev_alloc(m, &m->attn_part, (size_t)m->nkv * m->attn_nsplit * group * m->hd)) ||
-        (rc = dev_alloc(m, &m->attn_ml, (size_t)m->nkv * m->attn_nsplit * group * 2)) ||
-        (rc = dev_alloc(m, &m->attn_counter, (size_t)m->nkv)))
+    if ((rc = dev_alloc(m, &m->attn_part, (size_t)m->nkv * kMaxSplits * group * m->hd)) ||
+        (rc = dev_alloc(m, &m->attn_ml, (size_t)m->nkv * kMaxSplits * group * 2)))
         return rc;
-    TMG_HIP(hipMemset(m->attn_counter, 0, sizeof(unsigned) * m->nkv));
+    m->argmax_nparts = gemv_blocks(m->V, m->H);
+    if ((rc = dev_alloc(m, &m->argmax_part, (size_t)m->argmax_nparts))) return rc;
     if ((rc = ensure_rope(m, 64))) return rc;
     if ((rc = pinned(m, (size_t)std::max<uint64_t>(V * 4, 1 << 16)))) return rc;
     TMG_HIP(hipDeviceSynchronize());
@@ -340,15 +338,21 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
         aa.T = 1;
         aa.pos_dev = &c->st->pos;
         aa.scale = 1.0f / sqrtf((float)m->hd);
-        aa.nsplit = m->attn_nsplit;
-        aa.min_chunk = m->attn_min_chunk;
+        aa.nsplit = c->attn_nsplit;
+        aa.min_chunk = kMinChunk;
         aa.part = m->attn_part;
         aa.part_ml = m->attn_ml;
-        aa.counter = m->attn_counter;
-        aa.out_f32 = m->attn_out;
+        aa.out_f32 = c->attn_nsplit == 1 ? m->attn_out : nullptr;
         if (rec) rec->begin("attn_decode", 2.0 * n_ctx_est * kvd * 4 + 2.0 * qd * 4);
         TMG_HIP(launch_attn(aa, s));
         if (rec) rec->end();
+        const bool fused = c->attn_nsplit > 1 && c->attn_nsplit <= kFusedSplits;
+        if (c->attn_nsplit > kFusedSplits) {
+            aa.out_f32 = m->attn_out;
+            if (rec) rec->begin("attn_combine", 0.0);
+            TMG_HIP(launch_attn_combine(aa, s));
+            if (rec) rec->end();
+        }
 
         GemvArgs oa{};
         oa.W = ly.o;
@@ -356,8 +360,17 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
         oa.in = qd;
         oa.x = m->attn_out;
         oa.y = m->x;
+        if (fused) {
+            oa.part = m->attn_part;
+            oa.part_ml = m->attn_ml;
+            oa.pos = &c->st->pos;
+            oa.nsplit = c->attn_nsplit;
+            oa.min_chunk = kMinChunk;
+            oa.hd = m->hd;
+            oa.group = m->nq / m->nkv;
+        }
         if (rec) rec->begin("gemv_o_resid", (double)H * qd * 2 + qd * 4.0 + H * 8.0);
-        TMG_HIP(launch_gemv(PRO_PLAIN, EPI_RESID, oa, s));
+        TMG_HIP(launch_gemv(fused ? PRO_ATTN_COMBINE : PRO_PLAIN, EPI_RESID, oa, s));
         if (rec) rec->end();
 
         GemvArgs ga{};
@@ -390,7 +403,7 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
     la.norm_w = m->final_norm;
     la.eps = m->cfg.rms_norm_eps;
     la.y = m->logits;
-    la.argmax_key = mode == SEL_ARGMAX ? &c->st->argmax_key : nullptr;
+    la.argmax_part = mode == SEL_ARGMAX ? m->argmax_part : nullptr;
     if (rec) rec->begin("gemv_lmhead_argmax", (double)m->V * H * 2 + H * 8.0 + m->V * 4.0);
     TMG_HIP(launch_gemv(PRO_NORM, EPI_LOGITS, la, s));
     if (rec) rec->end();
@@ -402,7 +415,7 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
 
 int enqueue_select(tmg_model *m, tmg_cache *c, int mode, int advance_pos) {
     if (mode == SEL_ARGMAX) {
-        FinalizeArgs fa{c->st, c->history, advance_pos, m->V};
+        FinalizeArgs fa{c->st, c->history, advance_pos, m->V, m->argmax_part, m->argmax_nparts};
         TMG_HIP(launch_finalize(fa, m->stream));
         return TMG_OK;
     }
@@ -482,7 +495,7 @@ static int ensure_prefill(tmg_model *m, int T) {
 }
 
 // Runs the batched prefill; leaves the last token's logits in m->logits and
-// their argmax in st->argmax_key.
+// the per-workgroup argmax keys in m->argmax_part.
 int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
     const int T = (int)n;
     const int H = m->H, I = m->I, qd = m->qd, kvd = m->kvd;
@@ -575,7 +588,7 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
     la.norm_w = m->final_norm;
     la.eps = m->cfg.rms_norm_eps;
     la.y = m->logits;
-    la.argmax_key = &c->st->argmax_key;
+    la.argmax_part = m->argmax_part;
     TMG_HIP(launch_gemv(PRO_NORM_BATCH, EPI_LOGITS, la, s));
     c->len += (uint32_t)T;
     // the device position follows the host mirror after a prefill
@@ -644,6 +657,7 @@ extern "C" int tmg_cache_new(tmg_model *m, uint32_t max_pos, tmg_cache **out) {
     tmg_cache *c = new tmg_cache();
     c->model = m;
     c->max_pos = max_pos;
+    c->attn_nsplit = (int)std::min<uint32_t>(kMaxSplits, (max_pos + kMinChunk - 1) / kMinChunk);
     const size_t n = (size_t)m->L * max_pos * m->kvd;
     int rc = TMG_OK;
     void *k = nullptr, *v = nullptr, *st = nullptr, *hist = nullptr;
@@ -794,13 +808,23 @@ extern "C" int tmg_decode_greedy(tmg_model *m, tmg_cache *c, uint32_t token, uin
     if ((uint64_t)c->len + n_steps > c->max_pos) return set_error(TMG_E_CAPACITY, "KV cache full");
     (void)hipSetDevice(m->device);
     int rc;
-    if ((rc = get_step_graph(m, c, SEL_ARGMAX))) return rc;
+    // TMG_DECODE_GRAPH=0 launches the same kernels one by one instead of
+    // replaying the captured graph (for tools that cannot trace graph launches)
+    const char *eg = getenv("TMG_DECODE_GRAPH");
+    const bool eager = eg && eg[0] == '0';
+    if (!eager && (rc = get_step_graph(m, c, SEL_ARGMAX))) return rc;
     if ((rc = set_state(m, c, (int)token, true))) return rc;
     hipEvent_t e0, e1;
     TMG_HIP(hipEventCreate(&e0));
     TMG_HIP(hipEventCreate(&e1));
     TMG_HIP(hipEventRecord(e0, m->stream));
-    for (uint32_t i = 0; i < n_steps; i++) TMG_HIP(hipGraphLaunch(c->graphs[SEL_ARGMAX], m->stream));
+    for (uint32_t i = 0; i < n_steps; i++) {
+        if (eager) {
+            if ((rc = enqueue_decode_step(m, c, nullptr, SEL_ARGMAX))) return rc;
+        } else {
+            TMG_HIP(hipGraphLaunch(c->graphs[SEL_ARGMAX], m->stream));
+        }
+    }
     TMG_HIP(hipEventRecord(e1, m->stream));
     TMG_HIP(hipEventSynchronize(e1));
     float el = 0.f;

@@ -35,9 +35,9 @@ struct tmg_model {
 
     // decode scratch
     float *x = nullptr, *q = nullptr, *attn_out = nullptr, *h = nullptr, *logits = nullptr;
-    float *attn_part = nullptr, *attn_ml = nullptr;
-    unsigned *attn_counter = nullptr;
-    int attn_nsplit = 1, attn_min_chunk = 16;
+    float *attn_part = nullptr, *attn_ml = nullptr;  // split-K partials (up to kMaxSplits)
+    unsigned long long *argmax_part = nullptr;       // per-workgroup argmax keys of the lm_head
+    int argmax_nparts = 0;
 
     // prefill scratch, grown on demand
     int pf_cap = 0;
@@ -60,6 +60,7 @@ struct tmg_cache {
     tmg::DevState *st = nullptr;       // device
     int *history = nullptr;            // device, max_pos + 2 entries
     uint32_t len = 0;                  // host mirror of st->pos
+    int attn_nsplit = 1;               // split-K width of decode attention for this cache
     unsigned *seen = nullptr;          // bitmap of generated ids (repetition penalty)
     unsigned long long *cand = nullptr;  // sampler candidates
     // one captured step graph per token-selection mode (tmg::SelectMode)
@@ -68,6 +69,14 @@ struct tmg_cache {
 };
 
 namespace tmg {
+
+// Decode attention: each split covers at least kMinChunk positions; a cache
+// of max_pos rows uses up to ceil(max_pos / kMinChunk) splits (at most
+// kMaxSplits).  Up to kFusedSplits the merge runs in the o_proj GEMV
+// prologue; above that a combine kernel runs first.
+constexpr int kMinChunk = 64;
+constexpr int kMaxSplits = 64;
+constexpr int kFusedSplits = 8;
 
 // Per-launch timing hook used by tmg_profile_decode_step.
 struct LaunchRecorder {

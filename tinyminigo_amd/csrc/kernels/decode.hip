@@ -56,6 +56,51 @@ __device__ __forceinline__ void load_act(const float *src, const uint16_t *src_b
     }
 }
 
+// Split count of a decode attention row at context n_ctx: the same formula in
+// the attention kernel, its combine kernel and the fused combine prologue.
+__device__ __forceinline__ int active_splits(int n_ctx, int nsplit, int min_chunk) {
+    return min(nsplit, (n_ctx + min_chunk - 1) / min_chunk);
+}
+
+// The attention output for this thread's 8 consecutive dims (one head),
+// merged from the active splits: o = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s.
+template <int KC>
+__device__ __forceinline__ void load_attn(const GemvArgs &a, int t, float (&xv)[KC][8]) {
+    const int n_ctx = *a.pos + 1;
+    const int active = active_splits(n_ctx, a.nsplit, a.min_chunk);
+#pragma unroll
+    for (int c = 0; c < KC; c++) {
+        const int k = c * kChunk + t * 8;
+#pragma unroll
+        for (int j = 0; j < 8; j++) xv[c][j] = 0.0f;
+        if (k >= a.in) continue;
+        const int h = k / a.hd, d = k - h * a.hd;
+        const int g = h / a.group, hq = h - g * a.group;
+        const size_t base = (size_t)g * a.nsplit * a.group + hq;  // + s * group
+        float M = -INFINITY;
+        for (int sp = 0; sp < active; sp++) M = fmaxf(M, a.part_ml[(base + (size_t)sp * a.group) * 2]);
+        float L = 0.0f;
+        for (int sp = 0; sp < active; sp++) {
+            const size_t pi = base + (size_t)sp * a.group;
+            const float m = a.part_ml[pi * 2];
+            const float w = (m == -INFINITY) ? 0.0f : expf(m - M);
+            L = fmaf(a.part_ml[pi * 2 + 1], w, L);
+            const float4 o0 = *reinterpret_cast<const float4 *>(a.part + pi * a.hd + d);
+            const float4 o1 = *reinterpret_cast<const float4 *>(a.part + pi * a.hd + d + 4);
+            xv[c][0] = fmaf(o0.x, w, xv[c][0]);
+            xv[c][1] = fmaf(o0.y, w, xv[c][1]);
+            xv[c][2] = fmaf(o0.z, w, xv[c][2]);
+            xv[c][3] = fmaf(o0.w, w, xv[c][3]);
+            xv[c][4] = fmaf(o1.x, w, xv[c][4]);
+            xv[c][5] = fmaf(o1.y, w, xv[c][5]);
+            xv[c][6] = fmaf(o1.z, w, xv[c][6]);
+            xv[c][7] = fmaf(o1.w, w, xv[c][7]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) xv[c][j] = xv[c][j] / L;
+    }
+}
+
 template <int KC, int R, int PRO, int EPI>
 __global__ __launch_bounds__(kBlock) void gemv_kernel(const GemvArgs a) {
     __shared__ float red[4][R];
@@ -76,7 +121,11 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(const GemvArgs a) {
             src = a.embed_f32 + (size_t)tok * in;
         }
     }
-    load_act<KC>(src, src_bf, in, t, xv);
+    if constexpr (PRO == PRO_ATTN_COMBINE) {
+        load_attn<KC>(a, t, xv);
+    } else {
+        load_act<KC>(src, src_bf, in, t, xv);
+    }
     if constexpr (PRO == PRO_EMBED_NORM) {
         if (blockIdx.x == 0) {
 #pragma unroll
@@ -90,7 +139,7 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(const GemvArgs a) {
             }
         }
     }
-    if constexpr (PRO != PRO_PLAIN) {
+    if constexpr (PRO != PRO_PLAIN && PRO != PRO_ATTN_COMBINE) {
         float ss[1] = {0.0f};
 #pragma unroll
         for (int c = 0; c < KC; c++)
@@ -171,14 +220,14 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(const GemvArgs a) {
                     a.y[row] = v;
             }
             if constexpr (EPI == EPI_LOGITS) {
-                if (a.argmax_key) {
+                if (a.argmax_part) {
                     unsigned long long key = (ok && v == v) ? argmax_key(v, (uint32_t)row) : 0ull;
 #pragma unroll
                     for (int off = R / 2; off > 0; off >>= 1) {
                         const unsigned long long o = shfl_xor_u64(key, off);
                         key = o > key ? o : key;
                     }
-                    if (t == 0 && key != 0ull) atomicMax(a.argmax_key, key);
+                    if (t == 0) a.argmax_part[blockIdx.x] = key;
                 }
             }
         }
@@ -249,8 +298,10 @@ hipError_t launch_pe(const GemvArgs &a, hipStream_t s) {
 // Grid (nsplit, nkv, T).  A workgroup owns one KV head and one slice of the
 // positions of one query row, and serves all `GROUP` query heads of that KV
 // head from each K/V load.  Positions are processed in LDS chunks of 256 with
-// a running (max, sum) rescale; splits are combined by the last workgroup to
-// arrive (an arrival counter per (row, KV head) -- no workgroup ever waits).
+// a running (max, sum) rescale.  A row covered by one split is written out
+// directly; otherwise every split writes (o, max, sum) partials that are merged
+// after the kernel boundary, which also publishes them across the XCDs' L2s
+// without any in-kernel fence.
 // ---------------------------------------------------------------------------
 
 template <int HD, int GROUP>
@@ -261,13 +312,12 @@ __global__ __launch_bounds__(kBlock) void attn_kernel(const AttnArgs a) {
     __shared__ float s_p[GROUP][CH];
     __shared__ float s_red[NTEAM][GROUP][HD];
     __shared__ float scratch[4 * GROUP];
-    __shared__ int s_last;
 
     const int split = blockIdx.x, g = blockIdx.y, ti = blockIdx.z;
     const int t = threadIdx.x, lt = t % TS, team = t / TS;
     const int qpos = (a.pos_dev ? *a.pos_dev : a.start) + ti;
     const int n_ctx = qpos + 1;
-    const int active = min(a.nsplit, (n_ctx + a.min_chunk - 1) / a.min_chunk);
+    const int active = active_splits(n_ctx, a.nsplit, a.min_chunk);
     if (split >= active) return;
     const int chunk = (n_ctx + active - 1) / active;
     const int t0 = split * chunk, t1 = min(n_ctx, t0 + chunk);
@@ -370,7 +420,7 @@ __global__ __launch_bounds__(kBlock) void attn_kernel(const AttnArgs a) {
     }
 
     const size_t row_hd = (size_t)ti * qd + g * GROUP * HD;
-    if (active == 1) {
+    if (active == 1 && (a.out_f32 || a.out_hi)) {
 #pragma unroll
         for (int e = 0; e < (GROUP * HD + kBlock - 1) / kBlock; e++) {
             const int idx = t + e * kBlock;
@@ -383,7 +433,8 @@ __global__ __launch_bounds__(kBlock) void attn_kernel(const AttnArgs a) {
         return;
     }
 
-    // publish this split's partial, then let the last arrival combine
+    // publish this split's partial; the merge runs after the kernel boundary
+    // (fused into the o_proj GEMV prologue, or attn_combine_kernel)
     const size_t pbase = (((size_t)ti * a.nkv + g) * a.nsplit + split) * GROUP;
 #pragma unroll
     for (int e = 0; e < (GROUP * HD + kBlock - 1) / kBlock; e++) {
@@ -394,38 +445,29 @@ __global__ __launch_bounds__(kBlock) void attn_kernel(const AttnArgs a) {
         a.part_ml[(pbase + t) * 2 + 0] = m_run[t];
         a.part_ml[(pbase + t) * 2 + 1] = l_run[t];
     }
-    __threadfence();
-    __syncthreads();
-    unsigned *ctr = a.counter + (size_t)ti * a.nkv + g;
-    if (t == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == (unsigned)(active - 1));
+}
+
+// One thread per (query head, dim) of decode row 0.
+__global__ __launch_bounds__(kBlock) void attn_combine_kernel(const AttnArgs a) {
+    const int idx = blockIdx.x * kBlock + threadIdx.x;
+    if (idx >= a.nq * a.hd) return;
+    const int group = a.nq / a.nkv;
+    const int h = idx / a.hd, d = idx - h * a.hd;
+    const int g = h / group, hq = h - g * group;
+    const int n_ctx = *a.pos_dev + 1;
+    const int active = active_splits(n_ctx, a.nsplit, a.min_chunk);
+    const size_t base = (size_t)g * a.nsplit * group + hq;
+    float M = -INFINITY;
+    for (int sp = 0; sp < active; sp++) M = fmaxf(M, a.part_ml[(base + (size_t)sp * group) * 2]);
+    float L = 0.0f, O = 0.0f;
+    for (int sp = 0; sp < active; sp++) {
+        const size_t pi = base + (size_t)sp * group;
+        const float m = a.part_ml[pi * 2];
+        const float w = (m == -INFINITY) ? 0.0f : expf(m - M);
+        L = fmaf(a.part_ml[pi * 2 + 1], w, L);
+        O = fmaf(a.part[pi * a.hd + d], w, O);
     }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const size_t base0 = ((size_t)ti * a.nkv + g) * a.nsplit * GROUP;
-#pragma unroll
-    for (int e = 0; e < (GROUP * HD + kBlock - 1) / kBlock; e++) {
-        const int idx = t + e * kBlock;
-        if (idx < GROUP * HD) {
-            const int h = idx / HD;
-            float M = -INFINITY;
-            for (int sp = 0; sp < active; sp++) M = fmaxf(M, a.part_ml[(base0 + (size_t)sp * GROUP + h) * 2]);
-            float L = 0.0f, O = 0.0f;
-            for (int sp = 0; sp < active; sp++) {
-                const size_t pi = base0 + (size_t)sp * GROUP + h;
-                const float m = a.part_ml[pi * 2];
-                const float w = (m == -INFINITY) ? 0.0f : expf(m - M);
-                L = fmaf(a.part_ml[pi * 2 + 1], w, L);
-                O = fmaf(a.part[pi * HD + (idx % HD)], w, O);
-            }
-            const float o = O / L;
-            if (a.out_f32) a.out_f32[row_hd + idx] = o;
-            if (a.out_hi) split_bf16(o, a.out_hi + row_hd + idx, a.out_lo + row_hd + idx);
-        }
-    }
-    if (t == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    a.out_f32[idx] = O / L;
 }
 
 template <int HD>
@@ -447,10 +489,24 @@ hipError_t launch_attn_hd(const AttnArgs &a, hipStream_t s) {
 // appended to the history, and the cache position advances.
 // ---------------------------------------------------------------------------
 
-__global__ void finalize_kernel(const FinalizeArgs a) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+__global__ __launch_bounds__(1024) void finalize_kernel(const FinalizeArgs a) {
+    __shared__ unsigned long long red[16];
+    unsigned long long best = kArgmaxInit;
+    for (int i = threadIdx.x; i < a.nparts; i += blockDim.x) {
+        const unsigned long long k = a.argmax_part[i];
+        best = k > best ? k : best;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = shfl_xor_u64(best, off);
+        best = o > best ? o : best;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) best = red[w] > best ? red[w] : best;
     DevState *st = a.st;
-    const unsigned long long key = st->argmax_key;
+    const unsigned long long key = best;
     int tok = (int)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
     if (tok < 0 || tok >= a.V) tok = 0;
     st->cur_token = tok;
@@ -467,6 +523,7 @@ hipError_t launch_gemv(int pro, int epi, const GemvArgs &a, hipStream_t s) {
     if (pro == P && epi == E) return launch_pe<P, E>(a, s);
     TMG_PE(PRO_PLAIN, EPI_STORE)
     TMG_PE(PRO_PLAIN, EPI_RESID)
+    TMG_PE(PRO_ATTN_COMBINE, EPI_RESID)
     TMG_PE(PRO_NORM, EPI_SWIGLU)
     TMG_PE(PRO_NORM, EPI_QKV)
     TMG_PE(PRO_EMBED_NORM, EPI_QKV)
@@ -487,8 +544,19 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {
     }
 }
 
+hipError_t launch_attn_combine(const AttnArgs &a, hipStream_t s) {
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((a.nq * a.hd + kBlock - 1) / kBlock), dim3(kBlock), 0, s, a);
+    return hipGetLastError();
+}
+
+int gemv_blocks(int out, int in) {
+    const int kc = (in + kChunk - 1) / kChunk;
+    const int R = kc <= 2 ? 8 : 4;
+    return (out + R - 1) / R;
+}
+
 hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(finalize_kernel, dim3(1), dim3(1024), 0, s, a);
     return hipGetLastError();
 }
 

@@ -30,7 +30,7 @@ struct DevState {
     unsigned long long seed;
 };
 
-enum GemvPro { PRO_PLAIN = 0, PRO_NORM = 1, PRO_NORM_BATCH = 2, PRO_EMBED_NORM = 3 };
+enum GemvPro { PRO_PLAIN = 0, PRO_NORM = 1, PRO_NORM_BATCH = 2, PRO_EMBED_NORM = 3, PRO_ATTN_COMBINE = 4 };
 enum GemvEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3, EPI_LOGITS = 4 };
 
 struct GemvArgs {
@@ -52,11 +52,17 @@ struct GemvArgs {
     int hd, nq, nkv;
     float *q_out;            // [nq*hd]
     float *k_cache, *v_cache;  // layer base, [pos][nkv*hd]
-    // EPI_LOGITS
-    unsigned long long *argmax_key;  // may be null
+    // EPI_LOGITS: one packed (value, row) argmax key per workgroup, or null
+    unsigned long long *argmax_part;
+    // PRO_ATTN_COMBINE: the activation is the attention output, merged from
+    // the split-K partials of the decode attention kernel (see AttnArgs)
+    const float *part, *part_ml;
+    int nsplit, min_chunk, group;
 };
 
 hipError_t launch_gemv(int pro, int epi, const GemvArgs &a, hipStream_t s);
+// Workgroups (= argmax partials) of a GEMV launch with `out` rows of `in`.
+int gemv_blocks(int out, int in);
 
 struct AttnArgs {
     const float *q;  // [T][nq*hd], RoPE applied
@@ -70,18 +76,22 @@ struct AttnArgs {
     int min_chunk;    // minimum positions per active split
     float *part;      // [T][nkv][nsplit][group][hd] partial outputs
     float *part_ml;   // [T][nkv][nsplit][group][2] (max, sum)
-    unsigned *counter;  // [T][nkv] arrival counters (zero at rest)
-    float *out_f32;   // [T][nq*hd] (decode), or null
+    float *out_f32;   // [T][nq*hd] when one split covers the row, or null
     uint16_t *out_hi, *out_lo;  // [T][nq*hd] split-bf16 output (prefill), or null
 };
 
 hipError_t launch_attn(const AttnArgs &a, hipStream_t s);
+// Merges the split-K partials of a decode attention launch into out_f32
+// (used when the merge is not fused into the o_proj GEMV prologue).
+hipError_t launch_attn_combine(const AttnArgs &a, hipStream_t s);
 
 struct FinalizeArgs {
     DevState *st;
     int *history;  // generated ids, indexed by st->step
     int advance_pos;  // 1 after a decode step, 0 after prefill
     int V;            // ids outside [0, V) become 0 before they index anything
+    const unsigned long long *argmax_part;  // per-workgroup keys of the lm_head GEMV
+    int nparts;
 };
 
 hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t s);

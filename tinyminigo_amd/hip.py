@@ -1,0 +1,103 @@
+"""Device-memory plumbing through the HIP runtime that libtmg.so links.
+
+Tests and benchmarks need raw device buffers for the kernel-level entry
+point (tmg_gemv_bf16).  They must come from the same HIP runtime instance as
+libtmg's own allocations: importing a second runtime into the process (for
+example the one bundled with a PyTorch wheel) leaves one of the two without a
+usable device.  This module binds libamdhip64 by the soname libtmg resolved.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib  # noqa: F401  (libtmg.so first, so the soname below is the one it loaded)
+
+_hip = C.CDLL("libamdhip64.so.7")
+_hip.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+_hip.hipFree.argtypes = [C.c_void_p]
+_hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+_hip.hipMemset.argtypes = [C.c_void_p, C.c_int, C.c_size_t]
+_hip.hipDeviceSynchronize.argtypes = []
+_hip.hipGetDeviceCount.argtypes = [C.POINTER(C.c_int)]
+_hip.hipGetErrorString.restype = C.c_char_p
+_hip.hipGetErrorString.argtypes = [C.c_int]
+_hip.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+_hip.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+_hip.hipEventSynchronize.argtypes = [C.c_void_p]
+_hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+_hip.hipEventDestroy.argtypes = [C.c_void_p]
+
+H2D, D2H, D2D = 1, 2, 3
+
+
+def _ok(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what}: {_hip.hipGetErrorString(rc).decode()}")
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    return n.value if _hip.hipGetDeviceCount(C.byref(n)) == 0 else 0
+
+
+def synchronize() -> None:
+    _ok(_hip.hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+
+class DeviceBuffer:
+    """A hipMalloc'd buffer freed with the object."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = nbytes
+        self.ptr = C.c_void_p()
+        _ok(_hip.hipMalloc(C.byref(self.ptr), max(nbytes, 1)), "hipMalloc")
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        _ok(_hip.hipMemcpy(b.ptr, a.ctypes.data, a.nbytes, H2D), "hipMemcpy H2D")
+        return b
+
+    @property
+    def addr(self) -> int:
+        return self.ptr.value
+
+    def to_array(self, dtype, count: int) -> np.ndarray:
+        out = np.empty(count, dtype)
+        _ok(_hip.hipMemcpy(out.ctypes.data, self.ptr, out.nbytes, D2H), "hipMemcpy D2H")
+        return out
+
+    def fill_byte(self, v: int) -> None:
+        _ok(_hip.hipMemset(self.ptr, v, self.nbytes), "hipMemset")
+
+    def __del__(self):
+        if getattr(self, "ptr", None) is not None and self.ptr.value:
+            _hip.hipFree(self.ptr)
+            self.ptr = C.c_void_p()
+
+
+class Timer:
+    """HIP events on the null stream around a region."""
+
+    def __init__(self):
+        self.a, self.b = C.c_void_p(), C.c_void_p()
+        _ok(_hip.hipEventCreate(C.byref(self.a)), "hipEventCreate")
+        _ok(_hip.hipEventCreate(C.byref(self.b)), "hipEventCreate")
+
+    def start(self):
+        _ok(_hip.hipEventRecord(self.a, None), "hipEventRecord")
+
+    def stop(self) -> float:
+        _ok(_hip.hipEventRecord(self.b, None), "hipEventRecord")
+        _ok(_hip.hipEventSynchronize(self.b), "hipEventSynchronize")
+        ms = C.c_float()
+        _ok(_hip.hipEventElapsedTime(C.byref(ms), self.a, self.b), "hipEventElapsedTime")
+        return ms.value
+
+    def __del__(self):
+        for e in (self.a, self.b):
+            if e.value:
+                _hip.hipEventDestroy(e)
