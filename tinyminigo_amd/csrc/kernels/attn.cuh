@@ -1,0 +1,182 @@
+// GQA attention over the f32 KV cache as a device function shared by the
+// standalone attention kernel (decode.hip) and the persistent decode kernel.
+//
+// Reference: decode attention src/model.rs:434-459, attention_batch
+// src/tensor.rs:1099-1139, softmax src/tensor.rs:1055-1060.
+//
+// One call handles one (query row, KV head, split) item: positions
+// [t0, t1) of the row's context, for all GROUP query heads of the KV head, so
+// every K/V load serves GROUP heads.  TS = HD/4 lanes own one position (a
+// float4 of K and of V each); the 256 threads form NTEAM such teams.  Each
+// team keeps its own online-softmax state (running max, sum, output) over the
+// positions it visits, so the chunk loop has no block-wide synchronization;
+// K and V of a 64-position chunk are loaded together and the next chunk is
+// prefetched while the current one is computed.  Teams are merged in LDS at
+// the end.
+#pragma once
+
+#include "coh.cuh"
+#include "common.cuh"
+#include "kernels.hpp"
+
+namespace tmg {
+
+template <int HD, int GROUP>
+struct AttnShared {
+    static constexpr int TS = HD / 4;
+    static constexpr int NTEAM = kBlock / TS;
+    float o[NTEAM][GROUP][HD];
+    float m[NTEAM][GROUP];
+    float l[NTEAM][GROUP];
+};
+
+// With out_f32/out_hi null, or more than one active split, writes (o, max,
+// sum) partials (a split without positions writes max = -inf, sum = 0);
+// otherwise writes the normalized row.
+template <int HD, int GROUP, bool COH>
+__device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, int ti, int qpos, int active,
+                                          AttnShared<HD, GROUP> &sm) {
+    constexpr int TS = HD / 4;
+    constexpr int NTEAM = kBlock / TS;
+    constexpr int J = NTEAM >= 64 ? 1 : 64 / NTEAM;  // positions per team per chunk
+    constexpr int CH = NTEAM * J;
+    const int t = threadIdx.x, lt = t % TS, team = t / TS;
+    const int n_ctx = qpos + 1;
+    const int chunk = (n_ctx + active - 1) / active;
+    const int t0 = split * chunk, t1 = min(n_ctx, t0 + chunk);
+    const int kvd = a.nkv * HD;
+    const int qd = a.nq * HD;
+    const float *kbase = a.k_cache + g * HD + lt * 4;
+    const float *vbase = a.v_cache + g * HD + lt * 4;
+
+    float4 qv[GROUP];
+    const float *qrow = a.q + (size_t)ti * qd;
+#pragma unroll
+    for (int h = 0; h < GROUP; h++) qv[h] = ldf4<COH>(qrow + (g * GROUP + h) * HD + lt * 4);
+
+    float m_run[GROUP], l_run[GROUP];
+    float4 o_acc[GROUP];
+#pragma unroll
+    for (int h = 0; h < GROUP; h++) {
+        m_run[h] = -INFINITY;
+        l_run[h] = 0.0f;
+        o_acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+
+    float4 kr[J], vr[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int p = t0 + team + j * NTEAM;
+        // positions past t1 hold zeros: their weight is 0 and 0 * garbage could be NaN
+        kr[j] = vr[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (p < t1) {
+            kr[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
+            vr[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
+        }
+    }
+    for (int c0 = t0; c0 < t1; c0 += CH) {
+        float4 kn[J], vn[J];
+        const bool more = c0 + CH < t1;
+        if (more) {
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                const int p = c0 + CH + team + j * NTEAM;
+                kn[j] = vn[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (p < t1) {
+                    kn[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
+                    vn[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
+                }
+            }
+        }
+        // scores of this team's positions (every lane of the team gets them)
+        float s[J][GROUP];
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            const bool ok = c0 + team + j * NTEAM < t1;
+#pragma unroll
+            for (int h = 0; h < GROUP; h++) {
+                float d = 0.0f;
+                if (ok) {
+                    d = qv[h].x * kr[j].x;
+                    d = fmaf(qv[h].y, kr[j].y, d);
+                    d = fmaf(qv[h].z, kr[j].z, d);
+                    d = fmaf(qv[h].w, kr[j].w, d);
+                }
+                d = group_sum<TS>(d);
+                s[j][h] = ok ? d * a.scale : -INFINITY;
+            }
+        }
+        // online softmax update of the team's state
+#pragma unroll
+        for (int h = 0; h < GROUP; h++) {
+            float mc = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < J; j++) mc = fmaxf(mc, s[j][h]);
+            if (mc == -INFINITY) continue;  // no position of this team in the chunk
+            const float m_new = fmaxf(m_run[h], mc);
+            const float corr = (m_run[h] == -INFINITY) ? 0.0f : expf(m_run[h] - m_new);
+            float l = l_run[h] * corr;
+            float4 o = make_float4(o_acc[h].x * corr, o_acc[h].y * corr, o_acc[h].z * corr, o_acc[h].w * corr);
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                const float p = (s[j][h] == -INFINITY) ? 0.0f : expf(s[j][h] - m_new);
+                l += p;
+                o.x = fmaf(p, vr[j].x, o.x);
+                o.y = fmaf(p, vr[j].y, o.y);
+                o.z = fmaf(p, vr[j].z, o.z);
+                o.w = fmaf(p, vr[j].w, o.w);
+            }
+            m_run[h] = m_new;
+            l_run[h] = l;
+            o_acc[h] = o;
+        }
+        if (more) {
+#pragma unroll
+            for (int j = 0; j < J; j++) {
+                kr[j] = kn[j];
+                vr[j] = vn[j];
+            }
+        }
+    }
+
+    // merge the NTEAM team states
+#pragma unroll
+    for (int h = 0; h < GROUP; h++) {
+        *reinterpret_cast<float4 *>(&sm.o[team][h][lt * 4]) = o_acc[h];
+        if (lt == 0) {
+            sm.m[team][h] = m_run[h];
+            sm.l[team][h] = l_run[h];
+        }
+    }
+    __syncthreads();
+    const size_t row_hd = (size_t)ti * qd + g * GROUP * HD;
+    const size_t pbase = (((size_t)ti * a.nkv + g) * a.nsplit + split) * GROUP;
+    const bool direct = active == 1 && (a.out_f32 || a.out_hi);
+    for (int idx = t; idx < GROUP * HD; idx += kBlock) {
+        const int h = idx / HD, d = idx % HD;
+        float M = -INFINITY;
+#pragma unroll 8
+        for (int tm = 0; tm < NTEAM; tm++) M = fmaxf(M, sm.m[tm][h]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll 8
+        for (int tm = 0; tm < NTEAM; tm++) {
+            const float mt = sm.m[tm][h];
+            const float w = (mt == -INFINITY) ? 0.0f : expf(mt - M);
+            L = fmaf(sm.l[tm][h], w, L);
+            O = fmaf(sm.o[tm][h][d], w, O);
+        }
+        if (direct) {
+            const float o = O / L;
+            if (a.out_f32) stf<COH>(a.out_f32 + row_hd + idx, o);
+            if (a.out_hi) split_bf16(o, a.out_hi + row_hd + idx, a.out_lo + row_hd + idx);
+        } else {
+            stf<COH>(a.part + (pbase + h) * HD + d, O);
+            if (d == 0) {
+                stf<COH>(a.part_ml + (pbase + h) * 2 + 0, M);
+                stf<COH>(a.part_ml + (pbase + h) * 2 + 1, L);
+            }
+        }
+    }
+}
+
+}  // namespace tmg

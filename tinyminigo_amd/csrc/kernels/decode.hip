@@ -11,265 +11,30 @@
 // fuse the RMSNorm (reference rms_norm_into, src/tensor.rs:969-977) or the
 // embedding gather; epilogues fuse the residual add, SwiGLU, RoPE + KV-cache
 // append, or logits + a running argmax.
+#include "attn.cuh"
 #include "common.cuh"
+#include "gemv.cuh"
 #include "kernels.hpp"
 
 namespace tmg {
 namespace {
 
-constexpr int kChunk = kBlock * 8;  // elements per chunk: 8 per thread
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-template <int KC>
-__device__ __forceinline__ void load_act(const float *src, const uint16_t *src_bf, int in, int t,
-                                         float (&xv)[KC][8]) {
-#pragma unroll
-    for (int c = 0; c < KC; c++) {
-        const int k = c * kChunk + t * 8;
-        if (k < in) {
-            if (src_bf) {
-                const uint4 u = *reinterpret_cast<const uint4 *>(src_bf + k);
-                xv[c][0] = bf16_lo(u.x);
-                xv[c][1] = bf16_hi(u.x);
-                xv[c][2] = bf16_lo(u.y);
-                xv[c][3] = bf16_hi(u.y);
-                xv[c][4] = bf16_lo(u.z);
-                xv[c][5] = bf16_hi(u.z);
-                xv[c][6] = bf16_lo(u.w);
-                xv[c][7] = bf16_hi(u.w);
-            } else {
-                const float4 a = *reinterpret_cast<const float4 *>(src + k);
-                const float4 b = *reinterpret_cast<const float4 *>(src + k + 4);
-                xv[c][0] = a.x;
-                xv[c][1] = a.y;
-                xv[c][2] = a.z;
-                xv[c][3] = a.w;
-                xv[c][4] = b.x;
-                xv[c][5] = b.y;
-                xv[c][6] = b.z;
-                xv[c][7] = b.w;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; j++) xv[c][j] = 0.0f;
-        }
-    }
-}
-
-// Split count of a decode attention row at context n_ctx: the same formula in
-// the attention kernel, its combine kernel and the fused combine prologue.
-__device__ __forceinline__ int active_splits(int n_ctx, int nsplit, int min_chunk) {
-    return min(nsplit, (n_ctx + min_chunk - 1) / min_chunk);
-}
-
-// The attention output for this thread's 8 consecutive dims (one head),
-// merged from the active splits: o = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s.
-template <int KC>
-__device__ __forceinline__ void load_attn(const GemvArgs &a, int t, float (&xv)[KC][8]) {
-    const int n_ctx = *a.pos + 1;
-    const int active = active_splits(n_ctx, a.nsplit, a.min_chunk);
-#pragma unroll
-    for (int c = 0; c < KC; c++) {
-        const int k = c * kChunk + t * 8;
-#pragma unroll
-        for (int j = 0; j < 8; j++) xv[c][j] = 0.0f;
-        if (k >= a.in) continue;
-        const int h = k / a.hd, d = k - h * a.hd;
-        const int g = h / a.group, hq = h - g * a.group;
-        const size_t base = (size_t)g * a.nsplit * a.group + hq;  // + s * group
-        float M = -INFINITY;
-        for (int sp = 0; sp < active; sp++) M = fmaxf(M, a.part_ml[(base + (size_t)sp * a.group) * 2]);
-        float L = 0.0f;
-        for (int sp = 0; sp < active; sp++) {
-            const size_t pi = base + (size_t)sp * a.group;
-            const float m = a.part_ml[pi * 2];
-            const float w = (m == -INFINITY) ? 0.0f : expf(m - M);
-            L = fmaf(a.part_ml[pi * 2 + 1], w, L);
-            const float4 o0 = *reinterpret_cast<const float4 *>(a.part + pi * a.hd + d);
-            const float4 o1 = *reinterpret_cast<const float4 *>(a.part + pi * a.hd + d + 4);
-            xv[c][0] = fmaf(o0.x, w, xv[c][0]);
-            xv[c][1] = fmaf(o0.y, w, xv[c][1]);
-            xv[c][2] = fmaf(o0.z, w, xv[c][2]);
-            xv[c][3] = fmaf(o0.w, w, xv[c][3]);
-            xv[c][4] = fmaf(o1.x, w, xv[c][4]);
-            xv[c][5] = fmaf(o1.y, w, xv[c][5]);
-            xv[c][6] = fmaf(o1.z, w, xv[c][6]);
-            xv[c][7] = fmaf(o1.w, w, xv[c][7]);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j++) xv[c][j] = xv[c][j] / L;
-    }
-}
-
 template <int KC, int R, int PRO, int EPI>
 __global__ __launch_bounds__(kBlock) void gemv_kernel(const GemvArgs a) {
     __shared__ float red[4][R];
     __shared__ float scratch[4];
-    const int t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6;
-    const int in = a.in;
-
-    // ---- prologue: activation into registers ------------------------------
+    WeightRegs<KC, R> W;
+    gemv_load<KC, R>(a, blockIdx.x, W);  // weights first: independent of the prologue
+    const int pos = (EPI == EPI_QKV || PRO == PRO_ATTN_COMBINE) ? *a.pos : 0;
+    const int tok = PRO == PRO_EMBED_NORM ? *a.token : 0;
     float xv[KC][8];
-    const float *src = a.x;
-    const uint16_t *src_bf = nullptr;
-    if constexpr (PRO == PRO_EMBED_NORM) {
-        const int tok = *a.token;
-        if (a.embed_bf16) {
-            src_bf = a.embed_bf16 + (size_t)tok * in;
-        } else {
-            src = a.embed_f32 + (size_t)tok * in;
-        }
-    }
-    if constexpr (PRO == PRO_ATTN_COMBINE) {
-        load_attn<KC>(a, t, xv);
-    } else {
-        load_act<KC>(src, src_bf, in, t, xv);
-    }
-    if constexpr (PRO == PRO_EMBED_NORM) {
-        if (blockIdx.x == 0) {
-#pragma unroll
-            for (int c = 0; c < KC; c++) {
-                const int k = c * kChunk + t * 8;
-                if (k < in) {
-                    *reinterpret_cast<float4 *>(a.x_store + k) = make_float4(xv[c][0], xv[c][1], xv[c][2], xv[c][3]);
-                    *reinterpret_cast<float4 *>(a.x_store + k + 4) =
-                        make_float4(xv[c][4], xv[c][5], xv[c][6], xv[c][7]);
-                }
-            }
-        }
-    }
-    if constexpr (PRO != PRO_PLAIN && PRO != PRO_ATTN_COMBINE) {
-        float ss[1] = {0.0f};
-#pragma unroll
-        for (int c = 0; c < KC; c++)
-#pragma unroll
-            for (int j = 0; j < 8; j++) ss[0] += xv[c][j] * xv[c][j];
-        block_sum_n<1>(ss, scratch);
-        const float inv = 1.0f / sqrtf(ss[0] / (float)in + a.eps);
-#pragma unroll
-        for (int c = 0; c < KC; c++) {
-            const int k = c * kChunk + t * 8;
-            if (k < in) {
-                const float4 w0 = *reinterpret_cast<const float4 *>(a.norm_w + k);
-                const float4 w1 = *reinterpret_cast<const float4 *>(a.norm_w + k + 4);
-                const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    // decode: (v*inv)*w; batch (prefill): v*(inv*w) -- the
-                    // reference's two associations (src/tensor.rs:951, :975)
-                    if constexpr (PRO == PRO_NORM_BATCH)
-                        xv[c][j] = __fmul_rn(xv[c][j], __fmul_rn(inv, w[j]));
-                    else
-                        xv[c][j] = __fmul_rn(__fmul_rn(xv[c][j], inv), w[j]);
-                }
-            }
-        }
-    }
-
-    // ---- main loop: issue every row load, then the FMAs --------------------
-    const int row0 = blockIdx.x * R;
-    u32x4 wv[R][KC];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const int row = min(row0 + r, a.out - 1);
-        const u32x4 *wr = reinterpret_cast<const u32x4 *>(a.W + (size_t)row * in);
-#pragma unroll
-        for (int c = 0; c < KC; c++) {
-            const int k = c * kChunk + t * 8;
-            wv[r][c] = (k < in) ? __builtin_nontemporal_load(wr + (k >> 3)) : u32x4{0u, 0u, 0u, 0u};
-        }
-    }
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-        for (int c = 0; c < KC; c++) {
-            const u32x4 u = wv[r][c];
-            s0 = fmaf(xv[c][0], bf16_lo(u.x), s0);
-            s1 = fmaf(xv[c][1], bf16_hi(u.x), s1);
-            s0 = fmaf(xv[c][2], bf16_lo(u.y), s0);
-            s1 = fmaf(xv[c][3], bf16_hi(u.y), s1);
-            s0 = fmaf(xv[c][4], bf16_lo(u.z), s0);
-            s1 = fmaf(xv[c][5], bf16_hi(u.z), s1);
-            s0 = fmaf(xv[c][6], bf16_lo(u.w), s0);
-            s1 = fmaf(xv[c][7], bf16_hi(u.w), s1);
-        }
-        acc[r] = s0 + s1;
-    }
-
-    // ---- reduction --------------------------------------------------------
-    {
-        constexpr int LR = R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
-        const float s = multi_wave_sum<R>(acc, lane);
-        if ((lane & ((64 >> LR) - 1)) == 0) red[wave][lane >> (6 - LR)] = s;
-    }
-    __syncthreads();
-
-    // ---- epilogue ---------------------------------------------------------
-    if constexpr (EPI == EPI_STORE || EPI == EPI_RESID || EPI == EPI_LOGITS) {
-        if (t < R) {
-            const int row = row0 + t;
-            const float v = (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
-            const bool ok = row < a.out;
-            if (ok) {
-                if constexpr (EPI == EPI_RESID)
-                    a.y[row] += v;
-                else
-                    a.y[row] = v;
-            }
-            if constexpr (EPI == EPI_LOGITS) {
-                if (a.argmax_part) {
-                    unsigned long long key = (ok && v == v) ? argmax_key(v, (uint32_t)row) : 0ull;
-#pragma unroll
-                    for (int off = R / 2; off > 0; off >>= 1) {
-                        const unsigned long long o = shfl_xor_u64(key, off);
-                        key = o > key ? o : key;
-                    }
-                    if (t == 0) a.argmax_part[blockIdx.x] = key;
-                }
-            }
-        }
-    } else {
-        if (t < R / 2) {
-            const int P = row0 / 2 + t;  // global pair index
-            const float va = (red[0][2 * t] + red[1][2 * t]) + (red[2][2 * t] + red[3][2 * t]);
-            const float vb = (red[0][2 * t + 1] + red[1][2 * t + 1]) + (red[2][2 * t + 1] + red[3][2 * t + 1]);
-            if (2 * P + 1 < a.out) {
-                if constexpr (EPI == EPI_SWIGLU) {
-                    a.y[P] = swiglu(va, vb);
-                } else {  // EPI_QKV: pair (j, j + hd/2) of head P / (hd/2)
-                    const int half = a.hd >> 1;
-                    const int head = P / half, j = P - head * half;
-                    const int pos = *a.pos;
-                    const int kvd = a.nkv * a.hd;
-                    if (head < a.nq + a.nkv) {
-                        float oa, ob;
-                        rope_pair(va, vb, a.rope_cos[(size_t)pos * half + j], a.rope_sin[(size_t)pos * half + j], &oa,
-                                  &ob);
-                        if (head < a.nq) {
-                            a.q_out[head * a.hd + j] = oa;
-                            a.q_out[head * a.hd + j + half] = ob;
-                        } else {
-                            float *kr = a.k_cache + (size_t)pos * kvd + (head - a.nq) * a.hd;
-                            kr[j] = oa;
-                            kr[j + half] = ob;
-                        }
-                    } else {
-                        float *vr = a.v_cache + (size_t)pos * kvd + (head - a.nq - a.nkv) * a.hd;
-                        vr[j] = va;
-                        vr[j + half] = vb;
-                    }
-                }
-            }
-        }
-    }
+    gemv_prologue<KC, PRO, false>(a, tok, pos, xv, scratch, blockIdx.x == 0);
+    gemv_finish<KC, R, EPI, false>(a, blockIdx.x, pos, W, xv, red);
 }
 
 template <int KC, int PRO, int EPI>
 hipError_t launch_kc(const GemvArgs &a, hipStream_t s) {
-    constexpr int R = KC <= 2 ? 8 : 4;
+    constexpr int R = gemv_rows<KC>();
     const int grid = (a.out + R - 1) / R;
     hipLaunchKernelGGL((gemv_kernel<KC, R, PRO, EPI>), dim3(grid), dim3(kBlock), 0, s, a);
     return hipGetLastError();
@@ -292,159 +57,21 @@ hipError_t launch_pe(const GemvArgs &a, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// Attention (reference: decode src/model.rs:434-459; prefill attention_batch
-// src/tensor.rs:1099-1139; softmax src/tensor.rs:1055-1060).
-//
-// Grid (nsplit, nkv, T).  A workgroup owns one KV head and one slice of the
-// positions of one query row, and serves all `GROUP` query heads of that KV
-// head from each K/V load.  Positions are processed in LDS chunks of 256 with
-// a running (max, sum) rescale.  A row covered by one split is written out
-// directly; otherwise every split writes (o, max, sum) partials that are merged
-// after the kernel boundary, which also publishes them across the XCDs' L2s
-// without any in-kernel fence.
+// Attention: grid (nsplit, nkv, T), one attn_item per workgroup.  A row
+// covered by one split is written out directly; otherwise every split writes
+// (o, max, sum) partials that are merged after the kernel boundary (fused
+// into the o_proj GEMV prologue, or attn_combine_kernel), which also publishes
+// them across the XCDs' L2s without any in-kernel fence.
 // ---------------------------------------------------------------------------
 
 template <int HD, int GROUP>
 __global__ __launch_bounds__(kBlock) void attn_kernel(const AttnArgs a) {
-    constexpr int TS = HD / 4;            // lanes per position, float4 each
-    constexpr int NTEAM = kBlock / TS;    // positions in flight per block
-    constexpr int CH = 256;               // positions per LDS chunk
-    __shared__ float s_p[GROUP][CH];
-    __shared__ float s_red[NTEAM][GROUP][HD];
-    __shared__ float scratch[4 * GROUP];
-
+    __shared__ AttnShared<HD, GROUP> sm;
     const int split = blockIdx.x, g = blockIdx.y, ti = blockIdx.z;
-    const int t = threadIdx.x, lt = t % TS, team = t / TS;
     const int qpos = (a.pos_dev ? *a.pos_dev : a.start) + ti;
-    const int n_ctx = qpos + 1;
-    const int active = active_splits(n_ctx, a.nsplit, a.min_chunk);
+    const int active = active_splits(qpos + 1, a.nsplit, a.min_chunk);
     if (split >= active) return;
-    const int chunk = (n_ctx + active - 1) / active;
-    const int t0 = split * chunk, t1 = min(n_ctx, t0 + chunk);
-    const int kvd = a.nkv * HD;
-    const int qd = a.nq * HD;
-    const float *kbase = a.k_cache + g * HD + lt * 4;
-    const float *vbase = a.v_cache + g * HD + lt * 4;
-
-    float4 qv[GROUP];
-    const float *qrow = a.q + (size_t)ti * qd;
-#pragma unroll
-    for (int h = 0; h < GROUP; h++) qv[h] = *reinterpret_cast<const float4 *>(qrow + (g * GROUP + h) * HD + lt * 4);
-
-    float m_run[GROUP], l_run[GROUP];
-    float4 o_acc[GROUP];
-#pragma unroll
-    for (int h = 0; h < GROUP; h++) {
-        m_run[h] = -INFINITY;
-        l_run[h] = 0.0f;
-        o_acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-
-    for (int c0 = t0; c0 < t1; c0 += CH) {
-        const int n = min(CH, t1 - c0);
-        // scores s = (q . k) * scale
-        for (int i = team; i < n; i += NTEAM) {
-            const float4 k = *reinterpret_cast<const float4 *>(kbase + (size_t)(c0 + i) * kvd);
-#pragma unroll
-            for (int h = 0; h < GROUP; h++) {
-                float d = qv[h].x * k.x;
-                d = fmaf(qv[h].y, k.y, d);
-                d = fmaf(qv[h].z, k.z, d);
-                d = fmaf(qv[h].w, k.w, d);
-                d = group_sum<TS>(d);
-                if (lt == 0) s_p[h][i] = d * a.scale;
-            }
-        }
-        __syncthreads();
-        float mx[GROUP];
-#pragma unroll
-        for (int h = 0; h < GROUP; h++) {
-            mx[h] = -INFINITY;
-            for (int i = t; i < n; i += kBlock) mx[h] = fmaxf(mx[h], s_p[h][i]);
-        }
-        block_max_n<GROUP>(mx, scratch);
-        float sm[GROUP], corr[GROUP];
-#pragma unroll
-        for (int h = 0; h < GROUP; h++) {
-            const float m_new = fmaxf(m_run[h], mx[h]);
-            corr[h] = (m_run[h] == -INFINITY) ? 0.0f : expf(m_run[h] - m_new);
-            m_run[h] = m_new;
-            sm[h] = 0.0f;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int h = 0; h < GROUP; h++)
-            for (int i = t; i < n; i += kBlock) {
-                const float p = expf(s_p[h][i] - m_run[h]);
-                s_p[h][i] = p;
-                sm[h] += p;
-            }
-        block_sum_n<GROUP>(sm, scratch);
-#pragma unroll
-        for (int h = 0; h < GROUP; h++) {
-            l_run[h] = l_run[h] * corr[h] + sm[h];
-            o_acc[h].x *= corr[h];
-            o_acc[h].y *= corr[h];
-            o_acc[h].z *= corr[h];
-            o_acc[h].w *= corr[h];
-        }
-        // o += p * v
-        for (int i = team; i < n; i += NTEAM) {
-            const float4 v = *reinterpret_cast<const float4 *>(vbase + (size_t)(c0 + i) * kvd);
-#pragma unroll
-            for (int h = 0; h < GROUP; h++) {
-                const float p = s_p[h][i];
-                o_acc[h].x = fmaf(p, v.x, o_acc[h].x);
-                o_acc[h].y = fmaf(p, v.y, o_acc[h].y);
-                o_acc[h].z = fmaf(p, v.z, o_acc[h].z);
-                o_acc[h].w = fmaf(p, v.w, o_acc[h].w);
-            }
-        }
-        __syncthreads();
-    }
-
-    // reduce the per-team partial outputs
-#pragma unroll
-    for (int h = 0; h < GROUP; h++) *reinterpret_cast<float4 *>(&s_red[team][h][lt * 4]) = o_acc[h];
-    __syncthreads();
-    float o_fin[(GROUP * HD + kBlock - 1) / kBlock];
-#pragma unroll
-    for (int e = 0; e < (GROUP * HD + kBlock - 1) / kBlock; e++) {
-        const int idx = t + e * kBlock;
-        float s = 0.0f;
-        if (idx < GROUP * HD) {
-            const int h = idx / HD, d = idx % HD;
-            for (int tm = 0; tm < NTEAM; tm++) s += s_red[tm][h][d];
-        }
-        o_fin[e] = s;
-    }
-
-    const size_t row_hd = (size_t)ti * qd + g * GROUP * HD;
-    if (active == 1 && (a.out_f32 || a.out_hi)) {
-#pragma unroll
-        for (int e = 0; e < (GROUP * HD + kBlock - 1) / kBlock; e++) {
-            const int idx = t + e * kBlock;
-            if (idx < GROUP * HD) {
-                const float o = o_fin[e] / l_run[idx / HD];
-                if (a.out_f32) a.out_f32[row_hd + idx] = o;
-                if (a.out_hi) split_bf16(o, a.out_hi + row_hd + idx, a.out_lo + row_hd + idx);
-            }
-        }
-        return;
-    }
-
-    // publish this split's partial; the merge runs after the kernel boundary
-    // (fused into the o_proj GEMV prologue, or attn_combine_kernel)
-    const size_t pbase = (((size_t)ti * a.nkv + g) * a.nsplit + split) * GROUP;
-#pragma unroll
-    for (int e = 0; e < (GROUP * HD + kBlock - 1) / kBlock; e++) {
-        const int idx = t + e * kBlock;
-        if (idx < GROUP * HD) a.part[pbase * HD + idx] = o_fin[e];
-    }
-    if (t < GROUP) {
-        a.part_ml[(pbase + t) * 2 + 0] = m_run[t];
-        a.part_ml[(pbase + t) * 2 + 1] = l_run[t];
-    }
+    attn_item<HD, GROUP, false>(a, split, g, ti, qpos, active, sm);
 }
 
 // One thread per (query head, dim) of decode row 0.
@@ -492,9 +119,15 @@ hipError_t launch_attn_hd(const AttnArgs &a, hipStream_t s) {
 __global__ __launch_bounds__(1024) void finalize_kernel(const FinalizeArgs a) {
     __shared__ unsigned long long red[16];
     unsigned long long best = kArgmaxInit;
-    for (int i = threadIdx.x; i < a.nparts; i += blockDim.x) {
-        const unsigned long long k = a.argmax_part[i];
-        best = k > best ? k : best;
+    for (int i0 = threadIdx.x; i0 < a.nparts; i0 += 8 * blockDim.x) {
+        unsigned long long k[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = i0 + u * blockDim.x;
+            k[u] = i < a.nparts ? a.argmax_part[i] : 0ull;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) best = k[u] > best ? k[u] : best;
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -551,7 +184,7 @@ hipError_t launch_attn_combine(const AttnArgs &a, hipStream_t s) {
 
 int gemv_blocks(int out, int in) {
     const int kc = (in + kChunk - 1) / kChunk;
-    const int R = kc <= 2 ? 8 : 4;
+    const int R = kc <= 2 ? 8 : 4;  // gemv_rows<KC>()
     return (out + R - 1) / R;
 }
 
