@@ -46,6 +46,10 @@ struct tmg_model {
     uint16_t *pf_hi = nullptr, *pf_lo = nullptr, *pf_ahi = nullptr, *pf_alo = nullptr, *pf_hhi = nullptr,
              *pf_hlo = nullptr;
 
+    // persistent decode kernel for this model's shape (null: graph path only)
+    const void *pk = nullptr;
+    int pk_grid = 0;
+
     // pinned host staging
     void *pin = nullptr;
     size_t pin_bytes = 0;
@@ -63,6 +67,9 @@ struct tmg_cache {
     int attn_nsplit = 1;               // split-K width of decode attention for this cache
     unsigned *seen = nullptr;          // bitmap of generated ids (repetition penalty)
     unsigned long long *cand = nullptr;  // sampler candidates
+    tmg::GridBar *bar = nullptr;       // persistent-kernel barrier counters
+    tmg::PersistPlan *plan = nullptr;  // persistent-kernel argument blocks
+    bool persist_broken = false;       // a barrier timed out: use the graph path
     // one captured step graph per token-selection mode (tmg::SelectMode)
     hipGraphExec_t graphs[4] = {nullptr, nullptr, nullptr, nullptr};
     hipGraph_t graph_src[4] = {nullptr, nullptr, nullptr, nullptr};
@@ -102,5 +109,9 @@ int set_state(tmg_model *m, tmg_cache *c, int token, bool reset_step);
 int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n);
 int ensure_rope(tmg_model *m, int npos);
 int pinned(tmg_model *m, size_t bytes);
+// Greedy decode steps in one persistent launch when the model and cache
+// allow it (*used = false otherwise, nothing enqueued).
+int enqueue_persistent(tmg_model *m, tmg_cache *c, int steps, bool *used);
+int check_persistent(tmg_model *m, tmg_cache *c);
 
 }  // namespace tmg

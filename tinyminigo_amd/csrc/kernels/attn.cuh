@@ -12,7 +12,8 @@
 // positions it visits, so the chunk loop has no block-wide synchronization;
 // K and V of a 64-position chunk are loaded together and the next chunk is
 // prefetched while the current one is computed.  Teams are merged in LDS at
-// the end.
+// the end.  PREFETCH = false drops the next-chunk double buffer (for the
+// register budget of the persistent kernel).
 #pragma once
 
 #include "coh.cuh"
@@ -33,7 +34,7 @@ struct AttnShared {
 // With out_f32/out_hi null, or more than one active split, writes (o, max,
 // sum) partials (a split without positions writes max = -inf, sum = 0);
 // otherwise writes the normalized row.
-template <int HD, int GROUP, bool COH>
+template <int HD, int GROUP, bool COH, bool PREFETCH = true>
 __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, int ti, int qpos, int active,
                                           AttnShared<HD, GROUP> &sm) {
     constexpr int TS = HD / 4;
@@ -77,7 +78,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
     for (int c0 = t0; c0 < t1; c0 += CH) {
         float4 kn[J], vn[J];
         const bool more = c0 + CH < t1;
-        if (more) {
+        if (PREFETCH && more) {
 #pragma unroll
             for (int j = 0; j < J; j++) {
                 const int p = c0 + CH + team + j * NTEAM;
@@ -131,10 +132,23 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
             o_acc[h] = o;
         }
         if (more) {
+            if constexpr (PREFETCH) {
 #pragma unroll
-            for (int j = 0; j < J; j++) {
-                kr[j] = kn[j];
-                vr[j] = vn[j];
+                for (int j = 0; j < J; j++) {
+                    kr[j] = kn[j];
+                    vr[j] = vn[j];
+                }
+            } else {
+                // load the next chunk after this one is consumed (fewer registers)
+#pragma unroll
+                for (int j = 0; j < J; j++) {
+                    const int p = c0 + CH + team + j * NTEAM;
+                    kr[j] = vr[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (p < t1) {
+                        kr[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
+                        vr[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
+                    }
+                }
             }
         }
     }
