@@ -12,7 +12,8 @@ replayed from a captured hipGraph with inputs resident in HBM.
 
 Prints ONE JSON line.  `value` = decode tokens/s over the timed steps;
 `roofline` = the dominant kernel's algorithmic HBM bytes per launch over its
-average launch time (HIP events on the model's stream); `cpu_baseline` = the
+average launch time (its launches of one step replayed back to back from a
+graph between HIP events on the model's stream); `cpu_baseline` = the
 CPU oracle (C restatement of the reference Rust path, reference threading)
 timed on this host on a bounded sample of the same decode.
 """
@@ -73,6 +74,55 @@ def cpu_baseline(path, prompt, n_ctx0, seconds):
     }
 
 
+C1_SHAPES = [(2048, 2048), (6144, 2048), (2048, 6144), (73448, 2048)]
+MALL_BYTES = 256 << 20  # MI355X last-level (Infinity) cache
+
+
+def gemv_sweep(T):
+    """matmul_w (src/tensor.rs:315-338) at the decode GEMV shapes through the
+    kernel-level entry point tmg_gemv_bf16.  W BF16 N(0, 0.02) and x N(0, 1)
+    from seed 2.  HBM-cold: the launches of one replay rotate over enough
+    copies of W (>= 1 GiB) that none is still in the last-level cache;
+    MALL-hot: the same number of launches on one copy.  Bytes per launch =
+    2*out*in + 4*in + 4*out; each figure is the per-launch average over
+    graph replays (HIP events on the launch stream)."""
+    from tinyminigo_amd import hip as H
+    stream = H.Stream()
+    res = []
+    for out, inp in C1_SHAPES:
+        w = T.synth_normal_bf16(2, f"w{out}x{inp}", out * inp, 0.02)
+        x = T.synth_normal_f32(2, f"x{inp}", inp, 1.0)
+        wbytes = w.nbytes
+        ncopy = max(4, min(128, -(-(4 * MALL_BYTES) // wbytes)))
+        w0 = H.DeviceBuffer.from_array(w)
+        ws = [w0] + [H.DeviceBuffer(wbytes) for _ in range(ncopy - 1)]
+        for b in ws[1:]:
+            H.copy_device(b, w0, wbytes)
+        xd, yd = H.DeviceBuffer.from_array(x), H.DeviceBuffer(out * 4)
+        H.synchronize()
+        nbytes = 2 * out * inp + 4 * inp + 4 * out
+        row = {"shape": f"{out}x{inp}", "bytes": nbytes, "copies": ncopy}
+        for kind, pick in (("cold", lambda i: ws[i]), ("hot", lambda i: w0)):
+            g = H.Graph(stream, lambda st: [T.gemv_bf16(pick(i).addr, xd.addr, yd.addr, out, inp, st.addr)
+                                            for i in range(ncopy)])
+            g.launch()
+            stream.synchronize()
+            reps = max(3, 2000 // ncopy)
+            tm = H.Timer(stream)
+            tm.start()
+            for _ in range(reps):
+                g.launch()
+            us = tm.stop() * 1e3 / (reps * ncopy)
+            row[f"{kind}_us"] = round(us, 3)
+            row[f"{kind}_GB_s"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+            del g
+        res.append(row)
+        del ws, w0, xd, yd
+        log(f"gemv {out}x{inp}: cold {row['cold_us']} us ({row['cold_GB_s']} GB/s), "
+            f"hot {row['hot_us']} us ({row['hot_GB_s']} GB/s)")
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -82,6 +132,7 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=8)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the GEMV shape sweep")
     ap.add_argument("--model-dir", default=os.environ.get("TMG_MODEL_DIR",
                                                            os.path.join(tempfile.gettempdir(), "tmg_models")))
     args = ap.parse_args()
@@ -137,24 +188,25 @@ def main():
     step_bytes = wl.decode_bytes(int(round(n_ctx_avg)))
     log(f"decode {K} steps: {wall * 1e3:.1f} ms wall, {ev_ms:.1f} ms events -> {K / wall:.1f} tok/s")
 
-    # per-kernel timing: steps launched kernel by kernel with HIP events
+    # per-kernel timing: each kernel kind's launches of one step replayed back
+    # to back from a graph between HIP events on the library's stream
     per = {}
     tok = int(toks[-1])
     for _ in range(args.profile_steps):
-        recs = m.profile_decode_step(tok, cache)
-        for name, nbytes, ms in recs:
-            d = per.setdefault(name, [0, 0.0, 0.0])
-            d[0] += 1
-            d[1] += nbytes
-            d[2] += ms
-    dom = max(per.items(), key=lambda kv: kv[1][2])
-    name, (n, nbytes, ms) = dom
-    kern_ms = ms / n
-    achieved = (nbytes / n) / (kern_ms * 1e-3) / 1e9
+        for name, nbytes, ms, launches in m.profile_decode_step(tok, cache):
+            d = per.setdefault(name, [launches, nbytes, []])
+            d[2].append(ms)
+    per = {k: (v[0], v[1], float(np.median(v[2]))) for k, v in per.items()}
+    step_kern_ms = sum(n * ms for n, _, ms in per.values())
+    # dominant kernel: largest share of the step's kernel time
+    name, (n_launch, nbytes, kern_ms) = max(per.items(), key=lambda kv: kv[1][0] * kv[1][2])
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
     step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
-    kernels = {k: {"launches": v[0], "avg_us": round(v[2] / v[0] * 1e3, 2),
-                   "GB_s": round((v[1] / v[0]) / (v[2] / v[0] * 1e-3) / 1e9, 1) if v[1] else None,
-                   "share": round(v[2] / sum(x[2] for x in per.values()), 3)} for k, v in per.items()}
+    kernels = {k: {"launches": n, "avg_us": round(ms * 1e3, 2),
+                   "GB_s": round(b / (ms * 1e-3) / 1e9, 1) if b else None,
+                   "share": round(n * ms / step_kern_ms, 3)} for k, (n, b, ms) in per.items()}
+
+    sweep = None if args.no_sweep else gemv_sweep(T)
 
     cpu = None
     if not args.no_cpu:
@@ -189,8 +241,10 @@ def main():
                      "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "kernel": name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": nbytes / n, "avg_launch_us": round(kern_ms * 1e3, 3)},
+                     "bytes_per_launch": nbytes, "avg_launch_us": round(kern_ms * 1e3, 3),
+                     "launches_per_step": n_launch},
         "kernels": kernels,
+        "gemv_sweep": sweep,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -145,13 +145,17 @@ int tmg_decode_greedy(tmg_model *model, tmg_cache *cache, uint32_t token, uint32
 /* One launched kernel of a decode step, timed with HIP events on the model's
  * stream; bytes = algorithmic HBM bytes of that launch. */
 typedef struct tmg_kernel_record {
-    char name[48];
-    double bytes;
-    float ms;
+    char name[48];     /* kernel kind, e.g. "gemv_gateup_swiglu" */
+    double bytes;      /* algorithmic HBM bytes of one launch */
+    float ms;          /* average duration of one launch */
+    uint32_t launches; /* launches of this kind in one decode step */
 } tmg_kernel_record;
 
-/* Run one decode step kernel by kernel (not from the graph) with an event
- * pair around each launch.  Advances the cache like forward_token. */
+/* Per-kernel timing of one decode step at the cache's current position: for
+ * each kernel kind, that kind's launches of one step are captured into a graph
+ * and replayed back to back between two HIP events.  One record per kind, in
+ * launch order.  Leaves the cache as it was (length and contents up to len).
+ * No counterpart in the reference (measurement only). */
 int tmg_profile_decode_step(tmg_model *model, tmg_cache *cache, uint32_t token, tmg_kernel_record *records,
                             size_t cap, size_t *n_records);
 

@@ -65,7 +65,7 @@ class tmg_gen_params(C.Structure):
 
 
 class tmg_kernel_record(C.Structure):
-    _fields_ = [("name", C.c_char * 48), ("bytes", C.c_double), ("ms", C.c_float)]
+    _fields_ = [("name", C.c_char * 48), ("bytes", C.c_double), ("ms", C.c_float), ("launches", C.c_uint32)]
 
 
 class tmg_synth_spec(C.Structure):

@@ -3,7 +3,9 @@
 #include "model.hpp"
 
 #include <chrono>
+#include <algorithm>
 #include <memory>
+#include <string>
 #include <cmath>
 #include <cstring>
 
@@ -288,22 +290,10 @@ static int load_model(tmg_model *m, const SafeTensorsFile &f) {
 // argmax of generate, src/model.rs:636-637)
 // ---------------------------------------------------------------------------
 
-void LaunchRecorder::begin(const char *name, double bytes) {
-    tmg_kernel_record r{};
-    snprintf(r.name, sizeof(r.name), "%s", name);
-    r.bytes = bytes;
-    recs.push_back(r);
-    hipEvent_t e;
-    (void)hipEventCreate(&e);
-    (void)hipEventRecord(e, stream);
-    evs.push_back(e);
-}
-
-void LaunchRecorder::end() {
-    hipEvent_t e;
-    (void)hipEventCreate(&e);
-    (void)hipEventRecord(e, stream);
-    evs.push_back(e);
+bool LaunchRecorder::want(const char *name, double b) {
+    names.push_back(name);
+    bytes.push_back(b);
+    return !none && (!only || strcmp(only, name) == 0);
 }
 
 int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mode) {
@@ -339,9 +329,7 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
             qa.embed_f32 = m->embed_f32;
             qa.x_store = m->x;
         }
-        if (rec) rec->begin("gemv_qkv_rope", (double)m->qkv_rows * H * 2 + H * 8.0 + (qd + 2 * kvd) * 4.0);
-        TMG_HIP(launch_gemv(pro, EPI_QKV, qa, s));
-        if (rec) rec->end();
+        if (!rec || rec->want("gemv_qkv_rope", (double)m->qkv_rows * H * 2 + H * 8.0 + (qd + 2 * kvd) * 4.0)) TMG_HIP(launch_gemv(pro, EPI_QKV, qa, s));
 
         AttnArgs aa{};
         aa.q = m->q;
@@ -358,15 +346,11 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
         aa.part = m->attn_part;
         aa.part_ml = m->attn_ml;
         aa.out_f32 = c->attn_nsplit == 1 ? m->attn_out : nullptr;
-        if (rec) rec->begin("attn_decode", 2.0 * n_ctx_est * kvd * 4 + 2.0 * qd * 4);
-        TMG_HIP(launch_attn(aa, s));
-        if (rec) rec->end();
+        if (!rec || rec->want("attn_decode", 2.0 * n_ctx_est * kvd * 4 + 2.0 * qd * 4)) TMG_HIP(launch_attn(aa, s));
         const bool fused = c->attn_nsplit > 1 && c->attn_nsplit <= kFusedSplits;
         if (c->attn_nsplit > kFusedSplits) {
             aa.out_f32 = m->attn_out;
-            if (rec) rec->begin("attn_combine", 0.0);
-            TMG_HIP(launch_attn_combine(aa, s));
-            if (rec) rec->end();
+            if (!rec || rec->want("attn_combine", 0.0)) TMG_HIP(launch_attn_combine(aa, s));
         }
 
         GemvArgs oa{};
@@ -384,9 +368,7 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
             oa.hd = m->hd;
             oa.group = m->nq / m->nkv;
         }
-        if (rec) rec->begin("gemv_o_resid", (double)H * qd * 2 + qd * 4.0 + H * 8.0);
-        TMG_HIP(launch_gemv(fused ? PRO_ATTN_COMBINE : PRO_PLAIN, EPI_RESID, oa, s));
-        if (rec) rec->end();
+        if (!rec || rec->want("gemv_o_resid", (double)H * qd * 2 + qd * 4.0 + H * 8.0)) TMG_HIP(launch_gemv(fused ? PRO_ATTN_COMBINE : PRO_PLAIN, EPI_RESID, oa, s));
 
         GemvArgs ga{};
         ga.W = ly.gu;
@@ -396,9 +378,7 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
         ga.norm_w = ly.post_norm;
         ga.eps = m->cfg.rms_norm_eps;
         ga.y = m->h;
-        if (rec) rec->begin("gemv_gateup_swiglu", 2.0 * I * H * 2 + H * 8.0 + I * 4.0);
-        TMG_HIP(launch_gemv(PRO_NORM, EPI_SWIGLU, ga, s));
-        if (rec) rec->end();
+        if (!rec || rec->want("gemv_gateup_swiglu", 2.0 * I * H * 2 + H * 8.0 + I * 4.0)) TMG_HIP(launch_gemv(PRO_NORM, EPI_SWIGLU, ga, s));
 
         GemvArgs da{};
         da.W = ly.down;
@@ -406,9 +386,7 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
         da.in = I;
         da.x = m->h;
         da.y = m->x;
-        if (rec) rec->begin("gemv_down_resid", (double)H * I * 2 + I * 4.0 + H * 8.0);
-        TMG_HIP(launch_gemv(PRO_PLAIN, EPI_RESID, da, s));
-        if (rec) rec->end();
+        if (!rec || rec->want("gemv_down_resid", (double)H * I * 2 + I * 4.0 + H * 8.0)) TMG_HIP(launch_gemv(PRO_PLAIN, EPI_RESID, da, s));
     }
     GemvArgs la{};
     la.W = m->lm_head;
@@ -419,18 +397,15 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
     la.eps = m->cfg.rms_norm_eps;
     la.y = m->logits;
     la.argmax_part = mode == SEL_ARGMAX ? m->argmax_part : nullptr;
-    if (rec) rec->begin("gemv_lmhead_argmax", (double)m->V * H * 2 + H * 8.0 + m->V * 4.0);
-    TMG_HIP(launch_gemv(PRO_NORM, EPI_LOGITS, la, s));
-    if (rec) rec->end();
-    if (rec) rec->begin(mode == SEL_ARGMAX ? "finalize" : "sample", mode == SEL_ARGMAX ? 0.0 : m->V * 4.0);
-    int rc = enqueue_select(m, c, mode, 1);
-    if (rec) rec->end();
+    if (!rec || rec->want("gemv_lmhead_argmax", (double)m->V * H * 2 + H * 8.0 + m->V * 4.0)) TMG_HIP(launch_gemv(PRO_NORM, EPI_LOGITS, la, s));
+    int rc = TMG_OK;
+    if (!rec || rec->want(mode == SEL_ARGMAX ? "finalize" : "sample", mode == SEL_ARGMAX ? 0.0 : m->V * 4.0)) rc = enqueue_select(m, c, mode, 1);
     return rc;
 }
 
 int enqueue_select(tmg_model *m, tmg_cache *c, int mode, int advance_pos) {
     if (mode == SEL_ARGMAX) {
-        FinalizeArgs fa{c->st, c->history, advance_pos, m->V, m->argmax_part, m->argmax_nparts};
+        FinalizeArgs fa{c->st, c->history, advance_pos, m->V, m->argmax_part, m->argmax_nparts, (int)c->max_pos + 2};
         TMG_HIP(launch_finalize(fa, m->stream));
         return TMG_OK;
     }
@@ -442,6 +417,7 @@ int enqueue_select(tmg_model *m, tmg_cache *c, int mode, int advance_pos) {
     sa.seen_rw = c->seen;
     sa.cand = mode == SEL_FULL ? nullptr : c->cand;
     sa.history = c->history;
+    sa.hist_cap = (int)c->max_pos + 2;
     sa.greedy = mode == SEL_PENALTY_ARGMAX;
     sa.advance_pos = advance_pos;
     TMG_HIP(launch_sample(sa, m->stream));
@@ -559,6 +535,7 @@ int enqueue_persistent(tmg_model *m, tmg_cache *c, int steps, bool *used) {
     a.argmax_part = m->argmax_part;
     a.st = c->st;
     a.history = c->history;
+    a.hist_cap = (int)c->max_pos + 2;
     a.bar = c->bar;
     a.steps = steps;
     // TMG_PERSIST_TRACE=1: per-barrier timestamps of workgroup 0, summarized
@@ -1052,19 +1029,89 @@ extern "C" int tmg_profile_decode_step(tmg_model *m, tmg_cache *c, uint32_t toke
     if (c->len >= c->max_pos) return set_error(TMG_E_CAPACITY, "KV cache full");
     (void)hipSetDevice(m->device);
     int rc;
-    if ((rc = set_state(m, c, (int)token, true))) return rc;
-    LaunchRecorder rec{m->stream, {}, {}};
-    rc = enqueue_decode_step(m, c, &rec, SEL_ARGMAX);
-    TMG_HIP(hipStreamSynchronize(m->stream));
-    c->len += 1;
-    size_t n = rec.recs.size();
-    for (size_t i = 0; i < n && i < cap; i++) {
+    // the kernels of one step, in launch order
+    LaunchRecorder all;
+    all.none = true;
+    if ((rc = enqueue_decode_step(m, c, &all, SEL_ARGMAX))) return rc;
+    std::vector<std::string> kinds;
+    for (auto &n : all.names)
+        if (std::find(kinds.begin(), kinds.end(), n) == kinds.end()) kinds.push_back(n);
+    // each kind: its launches of one step captured as a graph, replayed back
+    // to back between two events (kernels abut as in the step graph)
+    constexpr int kReps = 8;
+    size_t nrec = 0;
+    hipEvent_t e0, e1;
+    TMG_HIP(hipEventCreate(&e0));
+    TMG_HIP(hipEventCreate(&e1));
+    // TMG_DECODE_GRAPH=0: the same launches enqueued one by one (profilers
+    // that do not follow graph launches)
+    const char *eg = getenv("TMG_DECODE_GRAPH");
+    const bool use_graph = !(eg && strcmp(eg, "0") == 0);
+    for (auto &kind : kinds) {
+        if ((rc = set_state(m, c, (int)token, true))) break;
+        int count = 0;  // launches of this kind in one step
+        double bytes = 0.0;
+        for (size_t i = 0; i < all.names.size(); i++)
+            if (all.names[i] == kind) {
+                count++;
+                bytes = all.bytes[i];
+            }
+        // kinds launched once or a few times per step are repeated so that one
+        // replay holds at least as many launches as a per-layer kind
+        const int inner = std::max(1, m->L / std::max(count, 1));
+        auto enqueue = [&]() -> int {
+            int r = TMG_OK;
+            for (int i = 0; i < inner && !r; i++) {
+                LaunchRecorder one;
+                one.only = kind.c_str();
+                r = enqueue_decode_step(m, c, &one, SEL_ARGMAX);
+            }
+            return r;
+        };
+        hipGraphExec_t ex = nullptr;
+        if (use_graph) {
+            TMG_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+            rc = enqueue();
+            hipGraph_t g = nullptr;
+            hipError_t e = hipStreamEndCapture(m->stream, &g);
+            if (rc) break;
+            TMG_HIP(e);
+            e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            TMG_HIP(e);
+        }
+        auto replay = [&]() -> int {
+            if (use_graph)
+                return hipGraphLaunch(ex, m->stream) == hipSuccess ? TMG_OK
+                                                                   : set_error(TMG_E_DEVICE, "graph launch failed");
+            return enqueue();
+        };
         float el = 0.f;
-        (void)hipEventElapsedTime(&el, rec.evs[2 * i], rec.evs[2 * i + 1]);
-        rec.recs[i].ms = el;
-        if (records) records[i] = rec.recs[i];
+        if (!(rc = replay())) {  // warm
+            TMG_HIP(hipEventRecord(e0, m->stream));
+            for (int r = 0; r < kReps && !rc; r++) rc = replay();
+            TMG_HIP(hipEventRecord(e1, m->stream));
+            TMG_HIP(hipEventSynchronize(e1));
+            TMG_HIP(hipEventElapsedTime(&el, e0, e1));
+        }
+        if (ex) (void)hipGraphExecDestroy(ex);
+        if (rc) break;
+        if (nrec < cap && records) {
+            tmg_kernel_record r{};
+            snprintf(r.name, sizeof(r.name), "%s", kind.c_str());
+            r.bytes = bytes;
+            r.ms = el / (float)(kReps * inner * count);
+            r.launches = count;
+            records[nrec] = r;
+        }
+        nrec++;
     }
-    for (auto e : rec.evs) (void)hipEventDestroy(e);
-    if (n_records) *n_records = std::min(n, cap);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    // the replays touched only scratch, the KV row at the current position
+    // (rewritten by the next step) and the step state, restored here
+    if (!rc) rc = set_state(m, c, (int)token, true);
+    if (!rc && hipStreamSynchronize(m->stream) != hipSuccess) rc = set_error(TMG_E_DEVICE, "stream sync failed");
+    if (n_records) *n_records = std::min(nrec, cap);
     return rc;
 }

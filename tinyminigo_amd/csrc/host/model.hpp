@@ -83,15 +83,16 @@ namespace tmg {
 // prologue; above that a combine kernel runs first.
 constexpr int kMinChunk = 64;
 constexpr int kMaxSplits = 64;
-constexpr int kFusedSplits = 8;
 
-// Per-launch timing hook used by tmg_profile_decode_step.
+// Launch filter used by tmg_profile_decode_step: every kernel of the step is
+// announced with its name and algorithmic bytes; when `only` is set, just the
+// kernels of that name are launched (to time them back to back in a graph).
 struct LaunchRecorder {
-    hipStream_t stream;
-    std::vector<tmg_kernel_record> recs;
-    std::vector<hipEvent_t> evs;
-    void begin(const char *name, double bytes);
-    void end();
+    const char *only = nullptr;
+    bool none = false;  // announce only, launch nothing
+    std::vector<std::string> names;
+    std::vector<double> bytes;
+    bool want(const char *name, double b);
 };
 
 // How a step turns logits into the next token.

@@ -24,12 +24,28 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(const GemvArgs a) {
     __shared__ float red[4][R];
     __shared__ float scratch[4];
     WeightRegs<KC, R> W;
-    gemv_load<KC, R>(a, blockIdx.x, W);  // weights first: independent of the prologue
-    const int pos = (EPI == EPI_QKV || PRO == PRO_ATTN_COMBINE) ? *a.pos : 0;
-    const int tok = PRO == PRO_EMBED_NORM ? *a.token : 0;
     float xv[KC][8];
-    gemv_prologue<KC, PRO, false>(a, tok, pos, xv, scratch, blockIdx.x == 0);
-    gemv_finish<KC, R, EPI, false>(a, blockIdx.x, pos, W, xv, red);
+    if constexpr (PRO == PRO_EMBED_NORM) {
+        // the gathered row depends on the token id: weights first
+        gemv_load<KC, R>(a, blockIdx.x, W);
+        const int pos = EPI == EPI_QKV ? *a.pos : 0;
+        gemv_prologue<KC, PRO, false>(a, *a.token, pos, xv, scratch, blockIdx.x == 0);
+        gemv_finish<KC, R, EPI, false>(a, blockIdx.x, pos, W, xv, red);
+    } else {
+        // activation-side loads, then the weights (see gemv.cuh)
+        ActIn<KC, PRO> in;
+        act_issue<KC, PRO>(a, in);
+        EpiIn pre{};
+        if constexpr (EPI == EPI_RESID) epi_issue_resid<R>(a, blockIdx.x, pre);
+        gemv_load<KC, R>(a, blockIdx.x, W);
+        // keep the scalar loads below after the weight loads: a wait for them
+        // would otherwise hold back the remaining weight loads
+        __builtin_amdgcn_sched_barrier(0);
+        const int pos = (EPI == EPI_QKV || PRO == PRO_ATTN_COMBINE) ? *a.pos : 0;
+        if constexpr (EPI == EPI_QKV) epi_load_rope<R>(a, blockIdx.x, pos, pre);
+        act_finish<KC, PRO>(a, pos, in, xv, scratch);
+        gemv_finish<KC, R, EPI, false, true>(a, blockIdx.x, pos, W, xv, red, pre);
+    }
 }
 
 template <int KC, int PRO, int EPI>
@@ -143,8 +159,9 @@ __global__ __launch_bounds__(1024) void finalize_kernel(const FinalizeArgs a) {
     int tok = (int)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
     if (tok < 0 || tok >= a.V) tok = 0;
     st->cur_token = tok;
-    a.history[st->step] = tok;
-    st->step = st->step + 1;
+    const int stp = st->step;
+    if (stp >= 0 && stp < a.hist_cap) a.history[stp] = tok;
+    st->step = stp + 1;
     if (a.advance_pos) st->pos = st->pos + 1;
     st->argmax_key = kArgmaxInit;
 }

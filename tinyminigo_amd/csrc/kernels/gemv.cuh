@@ -45,8 +45,10 @@ __device__ __forceinline__ void gemv_load(const GemvArgs &a, int blk, WeightRegs
         const u32x4 *wr = reinterpret_cast<const u32x4 *>(a.W + (size_t)row * a.in);
 #pragma unroll
         for (int c = 0; c < KC; c++) {
+            // clamped instead of branched, so all loads issue back to back;
+            // gemv_finish zeroes the chunks past the row end
             const int k = c * kChunk + t * 8;
-            W.w[r][c] = (k < a.in) ? __builtin_nontemporal_load(wr + (k >> 3)) : u32x4{0u, 0u, 0u, 0u};
+            W.w[r][c] = __builtin_nontemporal_load(wr + (min(k, a.in - 8) >> 3));
         }
     }
 }
@@ -132,6 +134,58 @@ __device__ __forceinline__ void load_attn(const GemvArgs &a, int pos, float (&xv
     }
 }
 
+template <int KC>
+__device__ __forceinline__ void load_norm_w(const GemvArgs &a, float (&wv)[KC][8]) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int c = 0; c < KC; c++) {
+        const int k = c * kChunk + t * 8;
+        float4 w0 = make_float4(0.f, 0.f, 0.f, 0.f), w1 = w0;
+        if (k < a.in) {
+            w0 = *reinterpret_cast<const float4 *>(a.norm_w + k);
+            w1 = *reinterpret_cast<const float4 *>(a.norm_w + k + 4);
+        }
+        wv[c][0] = w0.x;
+        wv[c][1] = w0.y;
+        wv[c][2] = w0.z;
+        wv[c][3] = w0.w;
+        wv[c][4] = w1.x;
+        wv[c][5] = w1.y;
+        wv[c][6] = w1.z;
+        wv[c][7] = w1.w;
+    }
+}
+
+// RMSNorm of the block's activation in registers (reference rms_norm_into,
+// src/tensor.rs:969-977; batch association src/tensor.rs:946-954).
+// `scratch` holds 4 floats of LDS.
+template <int KC, int PRO>
+__device__ __forceinline__ void rms_scale(const GemvArgs &a, float (&xv)[KC][8], const float (&wv)[KC][8],
+                                          float *scratch) {
+    const int t = threadIdx.x;
+    float ss[1] = {0.0f};
+#pragma unroll
+    for (int c = 0; c < KC; c++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) ss[0] += xv[c][j] * xv[c][j];
+    block_sum_n<1>(ss, scratch);
+    const float inv = 1.0f / sqrtf(ss[0] / (float)a.in + a.eps);
+#pragma unroll
+    for (int c = 0; c < KC; c++) {
+        const int k = c * kChunk + t * 8;
+        if (k < a.in) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                // decode (v*inv)*w; batch v*(inv*w) (src/tensor.rs:975 vs :951)
+                if constexpr (PRO == PRO_NORM_BATCH)
+                    xv[c][j] = __fmul_rn(xv[c][j], __fmul_rn(inv, wv[c][j]));
+                else
+                    xv[c][j] = __fmul_rn(__fmul_rn(xv[c][j], inv), wv[c][j]);
+            }
+        }
+    }
+}
+
 // Activation prologue: gather / load, then RMSNorm when PRO asks for it
 // (reference rms_norm_into, src/tensor.rs:969-977; batch association
 // src/tensor.rs:946-954).  `scratch` holds 4 floats of LDS.  `tok` and `pos`
@@ -162,39 +216,30 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs &a, int tok, int po
         load_act<KC, COH>(a.x, nullptr, in, xv);
     }
     if constexpr (PRO != PRO_PLAIN) {
-        float ss[1] = {0.0f};
-#pragma unroll
-        for (int c = 0; c < KC; c++)
-#pragma unroll
-            for (int j = 0; j < 8; j++) ss[0] += xv[c][j] * xv[c][j];
-        block_sum_n<1>(ss, scratch);
-        const float inv = 1.0f / sqrtf(ss[0] / (float)in + a.eps);
-#pragma unroll
-        for (int c = 0; c < KC; c++) {
-            const int k = c * kChunk + t * 8;
-            if (k < in) {
-                const float4 w0 = *reinterpret_cast<const float4 *>(a.norm_w + k);
-                const float4 w1 = *reinterpret_cast<const float4 *>(a.norm_w + k + 4);
-                const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    // decode (v*inv)*w; batch v*(inv*w) (src/tensor.rs:975 vs :951)
-                    if constexpr (PRO == PRO_NORM_BATCH)
-                        xv[c][j] = __fmul_rn(xv[c][j], __fmul_rn(inv, w[j]));
-                    else
-                        xv[c][j] = __fmul_rn(__fmul_rn(xv[c][j], inv), w[j]);
-                }
-            }
-        }
+        float wv[KC][8];
+        load_norm_w<KC>(a, wv);
+        rms_scale<KC, PRO>(a, xv, wv, scratch);
     }
+}
+
+// Epilogue inputs loaded ahead of the weights: the residual of row blk*R+t
+// (thread t < R) and the RoPE cos/sin of the block's R/2 rotation pairs.
+struct EpiIn {
+    float resid;
+    float rc[4], rs[4];
+};
+
+__device__ __forceinline__ float pick4(const float (&v)[4], int i) {
+    return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
 }
 
 // FMAs over a loaded block, the block reduction and the epilogue.
 // `red` is LDS of 4*R floats.  Returns after the epilogue; the caller
-// separates consecutive calls with a __syncthreads (red is reused).
-template <int KC, int R, int EPI, bool COH>
+// separates consecutive calls with a __syncthreads (red is reused).  With
+// PRE the residual / RoPE inputs come from `pre` instead of memory.
+template <int KC, int R, int EPI, bool COH, bool PRE = false>
 __device__ __forceinline__ void gemv_finish(const GemvArgs &a, int blk, int pos, const WeightRegs<KC, R> &W,
-                                            const float (&xv)[KC][8], float (*red)[R]) {
+                                            const float (&xv)[KC][8], float (*red)[R], const EpiIn &pre = EpiIn{}) {
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     float acc[R];
@@ -203,7 +248,7 @@ __device__ __forceinline__ void gemv_finish(const GemvArgs &a, int blk, int pos,
         float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
         for (int c = 0; c < KC; c++) {
-            const u32x4 u = W.w[r][c];
+            const u32x4 u = (c * kChunk + t * 8 < a.in) ? W.w[r][c] : u32x4{0u, 0u, 0u, 0u};
             s0 = fmaf(xv[c][0], bf16_lo(u.x), s0);
             s1 = fmaf(xv[c][1], bf16_hi(u.x), s1);
             s0 = fmaf(xv[c][2], bf16_lo(u.y), s0);
@@ -229,7 +274,7 @@ __device__ __forceinline__ void gemv_finish(const GemvArgs &a, int blk, int pos,
             const bool ok = row < a.out;
             if (ok) {
                 if constexpr (EPI == EPI_RESID)
-                    stf<COH>(a.y + row, ldf<COH>(a.y + row) + v);
+                    stf<COH>(a.y + row, (PRE ? pre.resid : ldf<COH>(a.y + row)) + v);
                 else
                     a.y[row] = v;  // logits / plain output: read after the launch
             }
@@ -259,8 +304,9 @@ __device__ __forceinline__ void gemv_finish(const GemvArgs &a, int blk, int pos,
                     const int kvd = a.nkv * a.hd;
                     if (head < a.nq + a.nkv) {
                         float oa, ob;
-                        rope_pair(va, vb, a.rope_cos[(size_t)pos * half + j], a.rope_sin[(size_t)pos * half + j], &oa,
-                                  &ob);
+                        const float rc = PRE ? pick4(pre.rc, t) : a.rope_cos[(size_t)pos * half + j];
+                        const float rs = PRE ? pick4(pre.rs, t) : a.rope_sin[(size_t)pos * half + j];
+                        rope_pair(va, vb, rc, rs, &oa, &ob);
                         if (head < a.nq) {
                             stf<COH>(a.q_out + head * a.hd + j, oa);
                             stf<COH>(a.q_out + head * a.hd + j + half, ob);
@@ -278,6 +324,136 @@ __device__ __forceinline__ void gemv_finish(const GemvArgs &a, int blk, int pos,
             }
         }
     }
+}
+
+// ---------------------------------------------------------------------------
+// Load order of the standalone decode GEMV.  Vector loads of a wavefront
+// complete in issue order, so an activation loaded after the weights could
+// only be used once every weight load had arrived.  The kernels therefore
+// issue the activation-side loads (x and the norm weights, or the split-K
+// attention partials, and the residual) first, then the weights, and run the
+// prologue (RMSNorm reduction, split merge) while the weights stream in.
+// ---------------------------------------------------------------------------
+
+template <int KC, int PRO>
+struct ActIn {
+    static constexpr bool kAttn = PRO == PRO_ATTN_COMBINE;
+    static constexpr bool kNorm = PRO == PRO_NORM || PRO == PRO_NORM_BATCH;
+    static constexpr int NS = kAttn ? kFusedSplits : 1;
+    float xv[KC][8];
+    float wv[kNorm ? KC : 1][8];
+    float2 ml[kAttn ? KC : 1][NS];
+    float4 o[kAttn ? KC : 1][NS][2];
+};
+
+// PRO in {PLAIN, NORM, NORM_BATCH, ATTN_COMBINE}; ATTN_COMBINE requires
+// a.nsplit <= kFusedSplits.
+template <int KC, int PRO>
+__device__ __forceinline__ void act_issue(const GemvArgs &a, ActIn<KC, PRO> &in) {
+    const int t = threadIdx.x;
+    if constexpr (PRO == PRO_ATTN_COMBINE) {
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            const int k = c * kChunk + t * 8;
+            const bool ok = k < a.in;
+            const int h = k / a.hd, d = k - h * a.hd;
+            const int g = h / a.group, hq = h - g * a.group;
+            const size_t base = (size_t)g * a.nsplit * a.group + hq;
+#pragma unroll
+            for (int sp = 0; sp < kFusedSplits; sp++) {
+                const size_t pi = base + (size_t)sp * a.group;
+                if (ok && sp < a.nsplit) {
+                    in.ml[c][sp] = *reinterpret_cast<const float2 *>(a.part_ml + pi * 2);
+                    in.o[c][sp][0] = *reinterpret_cast<const float4 *>(a.part + pi * a.hd + d);
+                    in.o[c][sp][1] = *reinterpret_cast<const float4 *>(a.part + pi * a.hd + d + 4);
+                } else {
+                    in.ml[c][sp] = make_float2(-INFINITY, 0.0f);
+                    in.o[c][sp][0] = in.o[c][sp][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+            }
+        }
+    } else {
+        load_act<KC, false>(a.x, nullptr, a.in, in.xv);
+        if constexpr (ActIn<KC, PRO>::kNorm) load_norm_w<KC>(a, in.wv);
+    }
+}
+
+// Same arithmetic, in the same order, as gemv_prologue / load_attn.
+template <int KC, int PRO>
+__device__ __forceinline__ void act_finish(const GemvArgs &a, int pos, ActIn<KC, PRO> &in, float (&xv)[KC][8],
+                                           float *scratch) {
+    const int t = threadIdx.x;
+    if constexpr (PRO == PRO_ATTN_COMBINE) {
+        const int active = active_splits(pos + 1, a.nsplit, a.min_chunk);
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            const int k = c * kChunk + t * 8;
+#pragma unroll
+            for (int j = 0; j < 8; j++) xv[c][j] = 0.0f;
+            if (k >= a.in) continue;
+            float M = -INFINITY;
+#pragma unroll
+            for (int sp = 0; sp < kFusedSplits; sp++)
+                if (sp < active) M = fmaxf(M, in.ml[c][sp].x);
+            float L = 0.0f;
+#pragma unroll
+            for (int sp = 0; sp < kFusedSplits; sp++) {
+                if (sp >= active) continue;
+                const float m = in.ml[c][sp].x;
+                const float w = (m == -INFINITY) ? 0.0f : expf(m - M);
+                L = fmaf(in.ml[c][sp].y, w, L);
+                const float4 o0 = in.o[c][sp][0], o1 = in.o[c][sp][1];
+                xv[c][0] = fmaf(o0.x, w, xv[c][0]);
+                xv[c][1] = fmaf(o0.y, w, xv[c][1]);
+                xv[c][2] = fmaf(o0.z, w, xv[c][2]);
+                xv[c][3] = fmaf(o0.w, w, xv[c][3]);
+                xv[c][4] = fmaf(o1.x, w, xv[c][4]);
+                xv[c][5] = fmaf(o1.y, w, xv[c][5]);
+                xv[c][6] = fmaf(o1.z, w, xv[c][6]);
+                xv[c][7] = fmaf(o1.w, w, xv[c][7]);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) xv[c][j] = xv[c][j] / L;
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < KC; c++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) xv[c][j] = in.xv[c][j];
+        if constexpr (ActIn<KC, PRO>::kNorm) rms_scale<KC, PRO>(a, xv, in.wv, scratch);
+    }
+}
+
+// Residual rows of block blk (issued before the weights).
+template <int R>
+__device__ __forceinline__ void epi_issue_resid(const GemvArgs &a, int blk, EpiIn &pre) {
+    const int t = threadIdx.x;
+    pre.resid = 0.0f;
+    if (t < R) {
+        const int row = blk * R + t;
+        if (row < a.out) pre.resid = a.y[row];
+    }
+}
+
+// RoPE cos/sin of the block's pairs at position pos: the R/2 pairs of a block
+// are consecutive frequencies of one head (hd/2 is a multiple of 4), so the
+// addresses are uniform over the workgroup.
+template <int R>
+__device__ __forceinline__ void epi_load_rope(const GemvArgs &a, int blk, int pos, EpiIn &pre) {
+    const int half = a.hd >> 1;
+    const int P0 = (blk * R) >> 1;
+    const int j0 = P0 - (P0 / half) * half;
+    const float *cb = a.rope_cos + (size_t)pos * half + j0;
+    const float *sb = a.rope_sin + (size_t)pos * half + j0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        pre.rc[i] = i < R / 2 ? cb[i] : 0.0f;
+        pre.rs[i] = i < R / 2 ? sb[i] : 0.0f;
+    }
+    // pin the (scalar) loads here rather than letting them sink into the
+    // epilogue, where their latency would add to the kernel's tail
+#pragma unroll
+    for (int i = 0; i < 4; i++) asm volatile("" ::"s"(pre.rc[i]), "s"(pre.rs[i]));
 }
 
 }  // namespace tmg

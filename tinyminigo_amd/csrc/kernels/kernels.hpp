@@ -92,6 +92,7 @@ struct FinalizeArgs {
     int V;            // ids outside [0, V) become 0 before they index anything
     const unsigned long long *argmax_part;  // per-workgroup keys of the lm_head GEMV
     int nparts;
+    int hist_cap;  // entries of history; ids at later steps are not recorded
 };
 
 hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t s);
@@ -131,6 +132,9 @@ hipError_t launch_copy_row(const float *x, int row, int H, float *dst, hipStream
 // ---- persistent decode ------------------------------------------------------
 
 constexpr int kBarGroups = 8;  // arrival groups of the grid barrier
+// Decode attention with at most this many splits is merged in the o_proj
+// GEMV prologue; with more, by attn_combine_kernel.
+constexpr int kFusedSplits = 8;
 
 // Grid-barrier counters, each on its own 128-byte line.  Zeroed once at cache
 // creation; the counters only grow and each launch records where the next
@@ -163,6 +167,7 @@ struct PersistArgs {
     const unsigned long long *argmax_part;
     DevState *st;
     int *history;
+    int hist_cap;
     GridBar *bar;
     int steps;  // decode steps run by this launch
     // optional: workgroup 0 records the 100 MHz realtime clock when it
@@ -189,6 +194,7 @@ struct SampleArgs {
     unsigned *seen_rw;     // same bitmap, updated with the chosen id
     unsigned long long *cand;  // [nslices][kSampleMaxK] packed (value, id) keys; null selects the full-vocabulary path
     int *history;
+    int hist_cap;
     int greedy;       // temperature <= 0: argmax of the penalized logits
     int advance_pos;  // 1 after a decode step, 0 after prefill
 };

@@ -215,7 +215,8 @@ __global__ __launch_bounds__(kBlock, 2) void decode_persistent(const PersistArgs
                 int t = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
                 if (t < 0 || t >= p.V) t = 0;
                 const int stp = (int)__hip_atomic_load(&p.st->step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(&p.history[stp], t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (stp >= 0 && stp < p.hist_cap)
+                    __hip_atomic_store(&p.history[stp], t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(&p.st->cur_token, t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(&p.st->step, stp + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(&p.st->pos, pos + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

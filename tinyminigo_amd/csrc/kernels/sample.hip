@@ -95,8 +95,9 @@ __device__ void emit_token(const SampleArgs &a, int tok) {
     if (tok < 0 || tok >= a.V) tok = 0;  // only reachable when every logit is NaN
     DevState *st = a.st;
     st->cur_token = tok;
-    a.history[st->step] = tok;
-    st->step = st->step + 1;
+    const int stp = st->step;
+    if (stp >= 0 && stp < a.hist_cap) a.history[stp] = tok;
+    st->step = stp + 1;
     if (a.advance_pos) st->pos = st->pos + 1;
     st->argmax_key = kArgmaxInit;
     a.seen_rw[tok >> 5] |= 1u << (tok & 31);

@@ -28,6 +28,16 @@ _hip.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
 _hip.hipEventSynchronize.argtypes = [C.c_void_p]
 _hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
 _hip.hipEventDestroy.argtypes = [C.c_void_p]
+_hip.hipStreamCreate.argtypes = [C.POINTER(C.c_void_p)]
+_hip.hipStreamDestroy.argtypes = [C.c_void_p]
+_hip.hipStreamSynchronize.argtypes = [C.c_void_p]
+_hip.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+_hip.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+_hip.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]
+_hip.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+_hip.hipGraphDestroy.argtypes = [C.c_void_p]
+_hip.hipGraphExecDestroy.argtypes = [C.c_void_p]
+_hip.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
 
 H2D, D2H, D2D = 1, 2, 3
 
@@ -79,19 +89,69 @@ class DeviceBuffer:
             self.ptr = C.c_void_p()
 
 
-class Timer:
-    """HIP events on the null stream around a region."""
+def copy_device(dst: "DeviceBuffer", src: "DeviceBuffer", nbytes: int) -> None:
+    _ok(_hip.hipMemcpy(dst.ptr, src.ptr, nbytes, D2D), "hipMemcpy D2D")
+
+
+class Stream:
+    """A HIP stream (default priority) of the runtime libtmg uses."""
 
     def __init__(self):
+        self.ptr = C.c_void_p()
+        _ok(_hip.hipStreamCreate(C.byref(self.ptr)), "hipStreamCreate")
+
+    @property
+    def addr(self) -> int:
+        return self.ptr.value
+
+    def synchronize(self) -> None:
+        _ok(_hip.hipStreamSynchronize(self.ptr), "hipStreamSynchronize")
+
+    def __del__(self):
+        if getattr(self, "ptr", None) is not None and self.ptr.value:
+            _hip.hipStreamDestroy(self.ptr)
+            self.ptr = C.c_void_p()
+
+
+class Graph:
+    """The launches `enqueue(stream)` makes, captured once and replayed."""
+
+    def __init__(self, stream: Stream, enqueue):
+        self.stream = stream
+        g = C.c_void_p()
+        _ok(_hip.hipStreamBeginCapture(stream.ptr, 0), "hipStreamBeginCapture")
+        try:
+            enqueue(stream)
+        finally:
+            _ok(_hip.hipStreamEndCapture(stream.ptr, C.byref(g)), "hipStreamEndCapture")
+        self.exec = C.c_void_p()
+        rc = _hip.hipGraphInstantiate(C.byref(self.exec), g, None, None, 0)
+        _hip.hipGraphDestroy(g)
+        _ok(rc, "hipGraphInstantiate")
+
+    def launch(self) -> None:
+        _ok(_hip.hipGraphLaunch(self.exec, self.stream.ptr), "hipGraphLaunch")
+
+    def __del__(self):
+        if getattr(self, "exec", None) is not None and self.exec.value:
+            _hip.hipGraphExecDestroy(self.exec)
+            self.exec = C.c_void_p()
+
+
+class Timer:
+    """HIP events around a region of one stream (the null stream by default)."""
+
+    def __init__(self, stream: "Stream | None" = None):
+        self.s = stream.ptr if stream is not None else None
         self.a, self.b = C.c_void_p(), C.c_void_p()
         _ok(_hip.hipEventCreate(C.byref(self.a)), "hipEventCreate")
         _ok(_hip.hipEventCreate(C.byref(self.b)), "hipEventCreate")
 
     def start(self):
-        _ok(_hip.hipEventRecord(self.a, None), "hipEventRecord")
+        _ok(_hip.hipEventRecord(self.a, self.s), "hipEventRecord")
 
     def stop(self) -> float:
-        _ok(_hip.hipEventRecord(self.b, None), "hipEventRecord")
+        _ok(_hip.hipEventRecord(self.b, self.s), "hipEventRecord")
         _ok(_hip.hipEventSynchronize(self.b), "hipEventSynchronize")
         ms = C.c_float()
         _ok(_hip.hipEventElapsedTime(C.byref(ms), self.a, self.b), "hipEventElapsedTime")

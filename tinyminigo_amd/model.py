@@ -129,12 +129,14 @@ class Model:
         return toks[:n_steps], ms.value
 
     def profile_decode_step(self, token: int, cache: "KvCache"):
-        """One decode step launched kernel by kernel with HIP events around each
-        launch: list of (name, algorithmic bytes, ms)."""
-        recs = (tmg_kernel_record * 4096)()
+        """Per-kernel timing of one decode step at the cache's position (each
+        kernel kind replayed back to back from a graph; the cache is left as it
+        was): list of (name, algorithmic bytes per launch, ms per launch,
+        launches per step)."""
+        recs = (tmg_kernel_record * 64)()
         n = C.c_size_t()
-        check(lib.tmg_profile_decode_step(self._h, cache._h, int(token), recs, 4096, C.byref(n)))
-        return [(recs[i].name.decode(), recs[i].bytes, recs[i].ms) for i in range(n.value)]
+        check(lib.tmg_profile_decode_step(self._h, cache._h, int(token), recs, 64, C.byref(n)))
+        return [(recs[i].name.decode(), recs[i].bytes, recs[i].ms, recs[i].launches) for i in range(n.value)]
 
 
 class KvCache:
