@@ -31,30 +31,70 @@ __device__ __forceinline__ void split_bf16(float x, uint16_t *hi, uint16_t *lo) 
     *lo = f32_to_bf16_rne(x - bf16_to_f32(h));
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+// Cross-lane moves without LDS: DPP within rows of 16 lanes and the gfx950
+// permlane swaps across rows.  For lane l:
+//   xor1 / xor2      -> value of lane l^1 / l^2       (DPP quad_perm)
+//   half_mirror      -> value of lane (l & ~7) | (7 - (l & 7))
+//   ror8             -> value of lane l^8             (DPP row_ror:8)
+//   permlane16_swap(a, b) -> {[a0-15, b0-15, a32-47, b32-47],
+//                             [a16-31, b16-31, a48-63, b48-63]}
+//   permlane32_swap(a, b) -> {[a0-31, b0-31], [a32-63, b32-63]}
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppRor8 = 0x128;       // row_ror:8
+
+// x + (x of lane l^16), and x + (x of lane l^32)
+__device__ __forceinline__ float add_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
-// Sum within aligned groups of W lanes (W a power of two <= 64).
+// Sum within aligned groups of W lanes (W a power of two <= 64); every lane
+// of a group receives the group's sum.
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "W must be a power of two");
+    if constexpr (W >= 2) v += dpp_mov<kDppXor1>(v);
+    if constexpr (W >= 4) v += dpp_mov<kDppXor2>(v);
+    if constexpr (W >= 8) v += dpp_mov<kDppHalfMirror>(v);  // quads hold equal values
+    if constexpr (W >= 16) v += dpp_mov<kDppRor8>(v);
+    if constexpr (W >= 32) v = add_xor16(v);
+    if constexpr (W >= 64) v = add_xor32(v);
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_mov<kDppXor1>(v));
+    v = fmaxf(v, dpp_mov<kDppXor2>(v));
+    v = fmaxf(v, dpp_mov<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_mov<kDppRor8>(v));
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
     return v;
 }
 
 // Reduce R values per lane across the 64-lane wavefront with a transposed
-// butterfly (log2(R) exchange steps that halve the live values, then a plain
-// butterfly): 10 shuffles for R = 8 instead of 48.  On return every lane
-// holds the wave sum of value (lane >> (6 - log2 R)).
+// butterfly: log2(R) exchange steps (lane halves 32 and 16 by permlane swaps,
+// 8 by DPP) that halve the live values, then a plain butterfly within the
+// remaining lane group.  On return every lane holds the wave sum of value
+// (lane >> (6 - log2 R)).
 template <int R>
 __device__ __forceinline__ float multi_wave_sum(float (&v)[R], int lane) {
     static_assert(R == 1 || R == 2 || R == 4 || R == 8, "R must be 1, 2, 4 or 8");
@@ -62,22 +102,29 @@ __device__ __forceinline__ float multi_wave_sum(float (&v)[R], int lane) {
     float cur[R];
 #pragma unroll
     for (int i = 0; i < R; i++) cur[i] = v[i];
+    if constexpr (LR >= 1) {  // lanes 32-63 keep values [R/2, R)
 #pragma unroll
-    for (int s = 0; s < LR; s++) {
-        const int off = 32 >> s;
-        const bool up = (lane & off) != 0;
-        const int n = R >> (s + 1);
-#pragma unroll
-        for (int i = 0; i < n; i++) {
-            float send = up ? cur[i] : cur[i + n];
-            float keep = up ? cur[i + n] : cur[i];
-            cur[i] = keep + __shfl_xor(send, off, 64);
+        for (int i = 0; i < R / 2; i++) {
+            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(cur[i]), __float_as_uint(cur[i + R / 2]),
+                                                            false, false);
+            cur[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
         }
     }
-    float x = cur[0];
+    if constexpr (LR >= 2) {  // lanes with bit 4 set keep the upper half
 #pragma unroll
-    for (int off = 32 >> LR; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
-    return x;
+        for (int i = 0; i < R / 4; i++) {
+            const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(cur[i]), __float_as_uint(cur[i + R / 4]),
+                                                            false, false);
+            cur[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+    }
+    if constexpr (LR >= 3) {  // lanes with bit 3 set keep cur[1]
+        const bool up = (lane & 8) != 0;
+        const float send = up ? cur[0] : cur[1];
+        const float keep = up ? cur[1] : cur[0];
+        cur[0] = keep + dpp_mov<kDppRor8>(send);
+    }
+    return group_sum<(64 >> LR)>(cur[0]);
 }
 
 // Block (256-thread) reductions of N values at once; every thread receives
