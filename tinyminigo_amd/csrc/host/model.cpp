@@ -343,6 +343,7 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
         aa.scale = 1.0f / sqrtf((float)m->hd);
         aa.nsplit = c->attn_nsplit;
         aa.min_chunk = kMinChunk;
+        aa.cap = (int)c->max_pos;
         aa.part = m->attn_part;
         aa.part_ml = m->attn_ml;
         aa.out_f32 = c->attn_nsplit == 1 ? m->attn_out : nullptr;

@@ -31,20 +31,46 @@ struct AttnShared {
     float l[NTEAM][GROUP];
 };
 
+// Lane geometry: TS lanes per position, NTEAM teams, J positions per team per
+// chunk of CH positions.
+template <int HD>
+struct AttnGeom {
+    static constexpr int TS = HD / 4;
+    static constexpr int NTEAM = kBlock / TS;
+    static constexpr int J = NTEAM >= 64 ? 1 : 64 / NTEAM;
+    static constexpr int CH = NTEAM * J;
+};
+
+// Split count of a decode attention row at context n_ctx: the same formula in
+// the attention kernel, its combine kernel and the fused combine prologue.
+__device__ __forceinline__ int active_splits(int n_ctx, int nsplit, int min_chunk) {
+    return min(nsplit, (n_ctx + min_chunk - 1) / min_chunk);
+}
+
+// Positions per split: at least min_chunk, and the context spread over the
+// nsplit splits once it is longer than nsplit * min_chunk.  Split s covers
+// [s * chunk, min(n_ctx, (s + 1) * chunk)); the active splits are
+// ceil(n_ctx / chunk) = min(nsplit, ceil(n_ctx / min_chunk)).
+__device__ __forceinline__ int attn_chunk(int n_ctx, int nsplit, int min_chunk) {
+    return max(min_chunk, (n_ctx + nsplit - 1) / nsplit);
+}
+
 // With out_f32/out_hi null, or more than one active split, writes (o, max,
 // sum) partials (a split without positions writes max = -inf, sum = 0);
 // otherwise writes the normalized row.
-template <int HD, int GROUP, bool COH, bool PREFETCH = true>
+// With SPEC (decode), the split's first chunk [split * min_chunk, + CH) is
+// loaded before the position is read from a.pos_dev (rows clamped to the
+// cache capacity a.cap), so the K/V loads do not wait for it; qpos and active
+// are then computed here and the arguments ignored.  Splits found inactive
+// return at once.
+template <int HD, int GROUP, bool COH, bool PREFETCH = true, bool SPEC = false>
 __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, int ti, int qpos, int active,
                                           AttnShared<HD, GROUP> &sm) {
     constexpr int TS = HD / 4;
     constexpr int NTEAM = kBlock / TS;
-    constexpr int J = NTEAM >= 64 ? 1 : 64 / NTEAM;  // positions per team per chunk
+    constexpr int J = AttnGeom<HD>::J;  // positions per team per chunk
     constexpr int CH = NTEAM * J;
     const int t = threadIdx.x, lt = t % TS, team = t / TS;
-    const int n_ctx = qpos + 1;
-    const int chunk = (n_ctx + active - 1) / active;
-    const int t0 = split * chunk, t1 = min(n_ctx, t0 + chunk);
     const int kvd = a.nkv * HD;
     const int qd = a.nq * HD;
     const float *kbase = a.k_cache + g * HD + lt * 4;
@@ -55,6 +81,27 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
 #pragma unroll
     for (int h = 0; h < GROUP; h++) qv[h] = ldf4<COH>(qrow + (g * GROUP + h) * HD + lt * 4);
 
+    float4 kr[J], vr[J];
+    const int spec_t0 = split * a.min_chunk;
+    if constexpr (SPEC) {
+        const int pos0 = *a.pos_dev;  // a scalar load, first used after the K/V loads are issued
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            const int p = min(spec_t0 + team + j * NTEAM, a.cap - 1);
+            kr[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
+            vr[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
+        }
+        // keep the loads above the position read: without this fence the
+        // compiler sinks them behind it (into the branch that uses them)
+        asm volatile("" ::: "memory");
+        qpos = pos0 + ti;
+        active = active_splits(qpos + 1, a.nsplit, a.min_chunk);
+        if (split >= active) return;
+    }
+    const int n_ctx = qpos + 1;
+    const int chunk = attn_chunk(n_ctx, a.nsplit, a.min_chunk);
+    const int t0 = split * chunk, t1 = min(n_ctx, t0 + chunk);
+
     float m_run[GROUP], l_run[GROUP];
     float4 o_acc[GROUP];
 #pragma unroll
@@ -64,13 +111,14 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
         o_acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
 
-    float4 kr[J], vr[J];
+    // Rows past t1 are loaded clamped (branch-free) and masked where used:
+    // their score is -inf and their V row is replaced by zeros (0 * garbage
+    // could be NaN).
+    const int last = max(t1 - 1, 0);
+    if (!SPEC || t0 != spec_t0) {
 #pragma unroll
-    for (int j = 0; j < J; j++) {
-        const int p = t0 + team + j * NTEAM;
-        // positions past t1 hold zeros: their weight is 0 and 0 * garbage could be NaN
-        kr[j] = vr[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (p < t1) {
+        for (int j = 0; j < J; j++) {
+            const int p = min(t0 + team + j * NTEAM, last);
             kr[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
             vr[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
         }
@@ -81,12 +129,9 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
         if (PREFETCH && more) {
 #pragma unroll
             for (int j = 0; j < J; j++) {
-                const int p = c0 + CH + team + j * NTEAM;
-                kn[j] = vn[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (p < t1) {
-                    kn[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
-                    vn[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
-                }
+                const int p = min(c0 + CH + team + j * NTEAM, last);
+                kn[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
+                vn[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
             }
         }
         // scores of this team's positions (every lane of the team gets them)
@@ -120,12 +165,14 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
             float4 o = make_float4(o_acc[h].x * corr, o_acc[h].y * corr, o_acc[h].z * corr, o_acc[h].w * corr);
 #pragma unroll
             for (int j = 0; j < J; j++) {
-                const float p = (s[j][h] == -INFINITY) ? 0.0f : expf(s[j][h] - m_new);
+                const bool ok = s[j][h] != -INFINITY;
+                const float p = ok ? expf(s[j][h] - m_new) : 0.0f;
+                const float4 v = ok ? vr[j] : make_float4(0.f, 0.f, 0.f, 0.f);
                 l += p;
-                o.x = fmaf(p, vr[j].x, o.x);
-                o.y = fmaf(p, vr[j].y, o.y);
-                o.z = fmaf(p, vr[j].z, o.z);
-                o.w = fmaf(p, vr[j].w, o.w);
+                o.x = fmaf(p, v.x, o.x);
+                o.y = fmaf(p, v.y, o.y);
+                o.z = fmaf(p, v.z, o.z);
+                o.w = fmaf(p, v.w, o.w);
             }
             m_run[h] = m_new;
             l_run[h] = l;
@@ -142,12 +189,9 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
                 // load the next chunk after this one is consumed (fewer registers)
 #pragma unroll
                 for (int j = 0; j < J; j++) {
-                    const int p = c0 + CH + team + j * NTEAM;
-                    kr[j] = vr[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (p < t1) {
-                        kr[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
-                        vr[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
-                    }
+                    const int p = min(c0 + CH + team + j * NTEAM, last);
+                    kr[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
+                    vr[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
                 }
             }
         }

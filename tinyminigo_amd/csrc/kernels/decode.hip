@@ -80,14 +80,20 @@ hipError_t launch_pe(const GemvArgs &a, hipStream_t s) {
 // them across the XCDs' L2s without any in-kernel fence.
 // ---------------------------------------------------------------------------
 
-template <int HD, int GROUP>
+// SPEC (decode): the split's first chunk is loaded before the position is
+// read (see attn_item).
+template <int HD, int GROUP, bool SPEC>
 __global__ __launch_bounds__(kBlock) void attn_kernel(const AttnArgs a) {
     __shared__ AttnShared<HD, GROUP> sm;
     const int split = blockIdx.x, g = blockIdx.y, ti = blockIdx.z;
-    const int qpos = (a.pos_dev ? *a.pos_dev : a.start) + ti;
-    const int active = active_splits(qpos + 1, a.nsplit, a.min_chunk);
-    if (split >= active) return;
-    attn_item<HD, GROUP, false>(a, split, g, ti, qpos, active, sm);
+    if constexpr (SPEC) {
+        attn_item<HD, GROUP, false, true, true>(a, split, g, ti, 0, 0, sm);
+    } else {
+        const int qpos = (a.pos_dev ? *a.pos_dev : a.start) + ti;
+        const int active = active_splits(qpos + 1, a.nsplit, a.min_chunk);
+        if (split >= active) return;
+        attn_item<HD, GROUP, false>(a, split, g, ti, qpos, active, sm);
+    }
 }
 
 // One thread per (query head, dim) of decode row 0.
@@ -113,14 +119,14 @@ __global__ __launch_bounds__(kBlock) void attn_combine_kernel(const AttnArgs a) 
     a.out_f32[idx] = O / L;
 }
 
-template <int HD>
+template <int HD, bool SPEC>
 hipError_t launch_attn_hd(const AttnArgs &a, hipStream_t s) {
     const dim3 grid(a.nsplit, a.nkv, a.T);
     switch (a.nq / a.nkv) {
-        case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, dim3(kBlock), 0, s, a); break;
-        case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, dim3(kBlock), 0, s, a); break;
-        case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, dim3(kBlock), 0, s, a); break;
-        case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, dim3(kBlock), 0, s, a); break;
+        case 1: hipLaunchKernelGGL((attn_kernel<HD, 1, SPEC>), grid, dim3(kBlock), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((attn_kernel<HD, 2, SPEC>), grid, dim3(kBlock), 0, s, a); break;
+        case 4: hipLaunchKernelGGL((attn_kernel<HD, 4, SPEC>), grid, dim3(kBlock), 0, s, a); break;
+        case 8: hipLaunchKernelGGL((attn_kernel<HD, 8, SPEC>), grid, dim3(kBlock), 0, s, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -184,12 +190,13 @@ hipError_t launch_gemv(int pro, int epi, const GemvArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {
+    const bool spec = a.pos_dev && a.cap > 0 && a.T == 1;
     switch (a.hd) {
-        case 16: return launch_attn_hd<16>(a, s);
-        case 32: return launch_attn_hd<32>(a, s);
-        case 64: return launch_attn_hd<64>(a, s);
-        case 128: return launch_attn_hd<128>(a, s);
-        case 256: return launch_attn_hd<256>(a, s);
+        case 16: return spec ? launch_attn_hd<16, true>(a, s) : launch_attn_hd<16, false>(a, s);
+        case 32: return spec ? launch_attn_hd<32, true>(a, s) : launch_attn_hd<32, false>(a, s);
+        case 64: return spec ? launch_attn_hd<64, true>(a, s) : launch_attn_hd<64, false>(a, s);
+        case 128: return spec ? launch_attn_hd<128, true>(a, s) : launch_attn_hd<128, false>(a, s);
+        case 256: return spec ? launch_attn_hd<256, true>(a, s) : launch_attn_hd<256, false>(a, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -14,6 +14,7 @@
 // persistent kernel where other workgroups wrote them in the same launch.
 #pragma once
 
+#include "attn.cuh"
 #include "coh.cuh"
 #include "common.cuh"
 #include "kernels.hpp"
@@ -87,12 +88,6 @@ __device__ __forceinline__ void load_act(const float *src, const uint16_t *src_b
             for (int j = 0; j < 8; j++) xv[c][j] = 0.0f;
         }
     }
-}
-
-// Split count of a decode attention row at context n_ctx: the same formula in
-// the attention kernel, its combine kernel and the fused combine prologue.
-__device__ __forceinline__ int active_splits(int n_ctx, int nsplit, int min_chunk) {
-    return min(nsplit, (n_ctx + min_chunk - 1) / min_chunk);
 }
 
 // The attention output for this thread's 8 consecutive dims (one head),

@@ -74,6 +74,7 @@ struct AttnArgs {
     float scale;      // 1/sqrt(hd)
     int nsplit;       // grid.x
     int min_chunk;    // minimum positions per active split
+    int cap;          // rows of k_cache / v_cache (bounds the speculative first-chunk loads; 0 disables them)
     float *part;      // [T][nkv][nsplit][group][hd] partial outputs
     float *part_ml;   // [T][nkv][nsplit][group][2] (max, sum)
     float *out_f32;   // [T][nq*hd] when one split covers the row, or null
