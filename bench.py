@@ -46,31 +46,56 @@ def cpu_model():
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(path, prompt, n_ctx0, seconds):
-    """The oracle decoding the same model on this host's cores: one prefill
-    of the prompt, then decode steps until about `seconds` have passed."""
+def cpu_baseline(path, prompt, seconds, long_wl=None, gpu_model=None, gpu_cache=None, sampled=None):
+    """The oracle (the C restatement of the reference CPU path) decoding the
+    same model on this host's cores: a prefill of the prompt, then decode
+    steps until about `seconds` have passed (at most 256).  For the 8k
+    workload the 8192-token CPU prefill (about ten minutes of single-threaded
+    attention) is replaced by the device's KV cache copied into the oracle's,
+    so the timed steps are CPU decode steps at that context.  With `sampled`
+    each step applies the penalty and the reference's sampler."""
     from oracle import oracle as O
     m = O.OracleModel.load(path)
     cache = m.new_cache()
-    t0 = time.perf_counter()
-    logits = m.prefill(prompt, cache)
-    prefill_s = time.perf_counter() - t0
+    if long_wl is not None:
+        n0 = gpu_cache.total_len()
+        for layer in range(long_wl.num_hidden_layers):
+            cache.push_rows(layer, gpu_cache.keys_flat(layer), gpu_cache.values_flat(layer))
+        logits = m.forward_token(int(prompt[-1]), cache)
+        prefill_s = None
+        what = f"decode at context {n0 + 1}+ (KV cache of the device prefill copied in)"
+    else:
+        t0 = time.perf_counter()
+        logits = m.prefill(prompt, cache)
+        prefill_s = time.perf_counter() - t0
+        what = f"after a {len(prompt)}-token prefill ({len(prompt) / prefill_s:.1f} prefill tok/s)"
+    generated = []
     n, t0 = 0, time.perf_counter()
-    tok = int(O.argmax(logits))
+
+    def pick(lg):
+        if sampled is None:
+            return int(O.argmax(lg))
+        if generated:
+            lg = O.apply_repetition_penalty(lg, generated, sampled["repetition_penalty"])
+        return O.sample(lg, sampled["temperature"], sampled["top_k"], sampled["top_p"], 0.5).token
+
+    tok = pick(logits)
     while True:
+        generated.append(tok)
         logits = m.forward_token(tok, cache)
-        tok = int(O.argmax(logits))
+        tok = pick(logits)
         n += 1
         el = time.perf_counter() - t0
         if el >= seconds or n >= 256:
             break
     threads = max(1, O.lib.om_num_threads() // 4)
+    mode = "sampled (penalty + top-k/top-p sampler)" if sampled else "greedy"
     return {
         "value": round(n / el, 3), "unit": "tok/s", "cores": threads, "kind": "port",
         "sample": (f"oracle (C restatement of the reference CPU path, GEMV on max(1,ncores/4)={threads} threads of "
-                   f"{os.cpu_count()} on '{cpu_model()}', AVX2={bool(O.lib.om_uses_avx2())}): {n} greedy decode "
-                   f"steps after a {len(prompt)}-token prefill ({len(prompt) / prefill_s:.1f} prefill tok/s)"),
-        "prefill_tok_s": round(len(prompt) / prefill_s, 2),
+                   f"{os.cpu_count()} on '{cpu_model()}', AVX2={bool(O.lib.om_uses_avx2())}): {n} {mode} decode "
+                   f"steps {what}"),
+        "prefill_tok_s": round(len(prompt) / prefill_s, 2) if prefill_s else None,
     }
 
 
@@ -123,10 +148,35 @@ def gemv_sweep(T):
     return res
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_1b_gemv_traffic.md")
+
+
+def pmc_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known size);
+    None when the summary has no line for it."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic-bytes-per-launch:"):
+                f = dict(kv.split("=", 1) for kv in line.split(":", 1)[1].split())
+                if f.get("kernel") == kernel:
+                    return int(f["bytes"])
+    except OSError:
+        pass
+    return None
+
+
+SAMPLED = dict(temperature=0.8, top_k=50, top_p=0.9, repetition_penalty=1.1, seed=42)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--workload", choices=["1b", "4b", "8k"], default="1b",
+                    help="1b: 64-token prompt + 256 greedy steps (default); 4b: 128-token prompt + 256 sampled "
+                         "tokens (T=0.8, top-k 50, top-p 0.9, penalty 1.1, seed 42); 8k: the 1b model after an "
+                         "8192-token prefill, 128 greedy steps")
+    ap.add_argument("--steps", type=int, default=None, help="decode steps (default: the workload's)")
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prefill-reps", type=int, default=5)
     ap.add_argument("--profile-steps", type=int, default=8)
@@ -145,48 +195,74 @@ def main():
 
     import tinyminigo_amd as T
     from tinyminigo_amd import workloads as W
+    # torch is not imported: a second HIP runtime in the process would leave
+    # one of the two without a device; synchronize through libtmg's runtime
+    from tinyminigo_amd.hip import synchronize as sync
 
-    wl = W.ONE_B
+    wl = {"1b": W.ONE_B, "4b": W.FOUR_B, "8k": W.LONG_CTX}[args.workload]
+    sampled = args.workload == "4b"
     t0 = time.perf_counter()
     path = W.ensure_model(wl, args.model_dir)
     log(f"model ready at {path} ({time.perf_counter() - t0:.1f}s)")
     prompt = [int(t) for t in wl.prompt()]
-    K, Wm = args.steps, args.warmup
+    K = args.steps if args.steps is not None else wl.gen_tokens
+    Wm = args.warmup
+    P = wl.prompt_len
     m = T.Model.load(path)
     log("model loaded")
 
-    # prefill tok/s: median over repetitions on fresh caches
+    # prefill tok/s: median over repetitions on fresh caches (one for 8k)
     pf = []
-    for _ in range(args.prefill_reps):
-        c = T.KvCache(m, wl.prompt_len + K + Wm + 8)
+    for _ in range(1 if args.workload == "8k" else args.prefill_reps):
+        c = T.KvCache(m, P + 8)
+        sync()
         t = time.perf_counter()
-        logits = m.forward_seq(prompt, c, want_logits=False)
+        m.forward_seq(prompt, c, want_logits=False)
+        sync()
         pf.append(time.perf_counter() - t)
         c.close()
     prefill_s = float(np.median(pf))
-    log(f"prefill {wl.prompt_len} tokens: {prefill_s * 1e3:.2f} ms")
+    log(f"prefill {P} tokens: {prefill_s * 1e3:.2f} ms")
 
-    # warmup on its own cache, then the timed steps on a fresh one
-    cache = T.KvCache(m, wl.prompt_len + max(K, Wm) + args.profile_steps + 8)
-    logits = m.forward_seq(prompt, cache)
-    first = int(np.argmax(logits))
-    if Wm:
-        wc = T.KvCache(m, wl.prompt_len + Wm + 8)
-        m.forward_seq(prompt, wc, want_logits=False)
-        m.decode_greedy(first, Wm, wc)
-        wc.close()
-    # torch is not imported: a second HIP runtime in the process would leave
-    # one of the two without a device; synchronize through libtmg's runtime
-    from tinyminigo_amd.hip import synchronize as sync
-    sync()
-    t = time.perf_counter()
-    toks, ev_ms = m.decode_greedy(first, K, cache)
-    sync()
-    wall = time.perf_counter() - t
-    ms_per_step = wall * 1e3 / K
-    n_ctx_avg = wl.prompt_len + (K + 1) / 2.0
+    cap = P + max(K, Wm) + args.profile_steps + 8
+    gen = None
+    if sampled:
+        # the product path: generate (prefill, device sampling, one id per
+        # step to the host); decode tok/s as the reference's main.rs reports
+        # it, (n - 1) / (elapsed - prefill)
+        T.generate(m, prompt, T.GenParams(max_tokens=Wm, **SAMPLED))
+        sync()
+        t = time.perf_counter()
+        gen = T.generate(m, prompt, T.GenParams(max_tokens=K, **SAMPLED))
+        wall_all = time.perf_counter() - t
+        wall = wall_all - gen.prefill_secs
+        K_timed = len(gen.tokens) - 1
+        ev_ms = None
+        log(f"generate {len(gen.tokens)} sampled tokens: {wall_all * 1e3:.1f} ms incl. prefill "
+            f"{gen.prefill_secs * 1e3:.1f} ms -> {K_timed / wall:.1f} tok/s")
+        cache = T.KvCache(m, cap)
+        logits = m.forward_seq(prompt, cache)
+        toks = [int(np.argmax(logits))]
+    else:
+        # warmup on its own cache, then the timed steps on a fresh one
+        cache = T.KvCache(m, cap)
+        logits = m.forward_seq(prompt, cache)
+        first = int(np.argmax(logits))
+        if Wm:
+            wc = T.KvCache(m, P + Wm + 8)
+            m.forward_seq(prompt, wc, want_logits=False)
+            m.decode_greedy(first, Wm, wc)
+            wc.close()
+        sync()
+        t = time.perf_counter()
+        toks, ev_ms = m.decode_greedy(first, K, cache)
+        sync()
+        wall = time.perf_counter() - t
+        K_timed = K
+        log(f"decode {K} steps: {wall * 1e3:.1f} ms wall, {ev_ms:.1f} ms events -> {K / wall:.1f} tok/s")
+    ms_per_step = wall * 1e3 / K_timed
+    n_ctx_avg = P + (K + 1) / 2.0
     step_bytes = wl.decode_bytes(int(round(n_ctx_avg)))
-    log(f"decode {K} steps: {wall * 1e3:.1f} ms wall, {ev_ms:.1f} ms events -> {K / wall:.1f} tok/s")
 
     # per-kernel timing: each kernel kind's launches of one step replayed back
     # to back from a graph between HIP events on the library's stream
@@ -205,20 +281,25 @@ def main():
     kernels = {k: {"launches": n, "avg_us": round(ms * 1e3, 2),
                    "GB_s": round(b / (ms * 1e-3) / 1e9, 1) if b else None,
                    "share": round(n * ms / step_kern_ms, 3)} for k, (n, b, ms) in per.items()}
+    traffic = pmc_traffic(name) if args.workload == "1b" else None
 
-    sweep = None if args.no_sweep else gemv_sweep(T)
+    sweep = None if (args.no_sweep or args.workload != "1b") else gemv_sweep(T)
 
     cpu = None
     if not args.no_cpu:
         log("timing the CPU baseline")
-        cpu = cpu_baseline(path, prompt, wl.prompt_len, args.cpu_seconds)
+        cpu = cpu_baseline(path, prompt, args.cpu_seconds, wl if args.workload == "8k" else None,
+                           m if args.workload == "8k" else None, cache if args.workload == "8k" else None,
+                           SAMPLED if sampled else None)
 
+    kind = (f"{K} sampled tokens (T=0.8, top-k 50, top-p 0.9, penalty 1.1, seed 42) through generate"
+            if sampled else f"{K} greedy decode steps")
     out = {
         "metric": METRIC,
-        "value": round(K / wall, 2),
+        "value": round(K_timed / wall, 2),
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": K,
+        "steps": K_timed,
         "warmup": Wm,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
@@ -227,20 +308,22 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": f"{wl.name}: {wl.prompt_len}-token prompt, batched prefill, {K} greedy decode steps",
+            "workload": f"{wl.name}: {P}-token prompt, batched prefill, {kind}",
             "model": "MiniCPM5-shaped Llama (random init)", "hidden": wl.hidden_size,
             "layers": wl.num_hidden_layers, "heads": wl.num_attention_heads, "kv_heads": wl.num_key_value_heads,
             "head_dim": wl.head_dim, "intermediate": wl.intermediate_size, "vocab": wl.vocab_size,
-            "global_batch": 1, "seq_len": wl.prompt_len + K, "parallelism": "none (1 GPU)",
+            "global_batch": 1, "seq_len": P + K, "parallelism": "none (1 GPU)",
             "arith": "BF16 weights, f32 activations/accumulation, f32 KV cache",
         },
-        "prefill_tok_s": round(wl.prompt_len / prefill_s, 1),
+        "prefill_tok_s": round(P / prefill_s, 1),
         "prefill_ms": round(prefill_s * 1e3, 3),
-        "decode_ms_events": round(ev_ms, 3),
-        "step_hbm": {"bytes_per_token": step_bytes, "n_ctx_avg": n_ctx_avg, "achieved_GB_s": round(step_gbs, 1),
+        "prefill_tflops": round(wl.prefill_flops(P) / prefill_s / 1e12, 2),
+        "decode_ms_events": round(ev_ms, 3) if ev_ms is not None else None,
+        "step_hbm": {"bytes_per_token": step_bytes, "kv_bytes_per_token": wl.kv_bytes(int(round(n_ctx_avg))),
+                     "n_ctx_avg": n_ctx_avg, "achieved_GB_s": round(step_gbs, 1),
                      "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "kernel": name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_per_launch": nbytes, "avg_launch_us": round(kern_ms * 1e3, 3),
                      "launches_per_step": n_launch},
         "kernels": kernels,

@@ -416,6 +416,17 @@ class OracleCache:
             raise OracleError("kv row width mismatch")
         lib.om_cache_push(self._h, layer, fp(k), fp(v))
 
+    def push_rows(self, layer: int, keys_flat, values_flat) -> None:
+        """push() of every row of flat [n, kv_dim] key/value arrays."""
+        k, v = f32(keys_flat), f32(values_flat)
+        if k.size != v.size or k.size % self.kv_dim:
+            raise OracleError("kv row width mismatch")
+        stride = self.kv_dim * 4
+        kb, vb = k.ctypes.data, v.ctypes.data
+        for i in range(k.size // self.kv_dim):
+            lib.om_cache_push(self._h, layer, C.cast(kb + i * stride, C.POINTER(C.c_float)),
+                              C.cast(vb + i * stride, C.POINTER(C.c_float)))
+
     def keys_flat(self, layer: int) -> np.ndarray:
         n = self.len(layer) * self.kv_dim
         return np.ctypeslib.as_array(lib.om_cache_keys(self._h, layer), (n,)).copy() if n else np.empty(0, np.float32)

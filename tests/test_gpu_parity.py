@@ -305,3 +305,52 @@ def test_persistent_matches_graph_bitwise(T, W, which, request):
     assert tp == tg
     assert np.array_equal(lp, lgr)
     assert np.array_equal(kp, kg)
+
+
+# --- C4: the 4B-class model, 128-token prompt + 256 sampled tokens ------------
+
+@pytest.fixture(scope="module")
+def four_b(T, O, W):
+    p = W.ensure_model(W.FOUR_B, model_root())
+    return T.Model.load(p), O.OracleModel.load(p)
+
+
+def test_four_b_sampled_generation(T, O, W, four_b):
+    """The 4B workload: T=0.8, top-k 50, top-p 0.9, repetition penalty 1.1,
+    seed 42.  All 256 ids are drawn on the device; the oracle replays the
+    first N of them (teacher forcing) and checks, at every replayed step, the
+    logits (tolerance), the top-50 candidate ids after penalty (identical up
+    to ties within the tolerance) and that the device's choice is the
+    oracle sampler's choice for the same uniform draw (or, at a CDF boundary,
+    at least a nucleus member)."""
+    g, o = four_b
+    wl = W.FOUR_B
+    prompt = [int(t) for t in wl.prompt()]
+    temp, k, p, pen, seed = 0.8, 50, 0.9, 1.1, 42
+    print("4B generate", flush=True)
+    out = T.generate(g, prompt, T.GenParams(max_tokens=wl.gen_tokens, temperature=temp, top_k=k, top_p=p,
+                                            repetition_penalty=pen, seed=seed))
+    assert len(out.tokens) == wl.gen_tokens
+    assert all(0 <= t < wl.vocab_size for t in out.tokens)
+    n = 16
+    print("4B oracle replay", flush=True)
+    ref = O.generate(o, prompt, n, forced=out.tokens[:n], repetition_penalty=pen, keep_logits=True)
+    close_logits(out.logits_first_step, ref.logits_first_step, "4B prefill")
+    # the device's own per-step logits, teacher forced through forward_token
+    gc = T.KvCache(g, len(prompt) + n + 1)
+    lg = g.forward_seq(prompt, gc)
+    mism = 0
+    for i in range(n):
+        gen = out.tokens[:i]
+        a = O.apply_repetition_penalty(lg, gen, pen) if gen else lg
+        b = ref.step_logits[i]
+        close_logits(a, b, f"4B step {i}")
+        ta, tb = np.argsort(-a, kind="stable")[:k], np.argsort(-b, kind="stable")[:k]
+        if set(ta) != set(tb):
+            assert np.min(np.abs(np.diff(np.sort(b)[::-1][:k + 1]))) < 2 * ABS_TOL, f"4B step {i}: top-{k} ids"
+        tr = O.sample(b, temp, k, p, device_draw(seed, i))
+        if tr.token != out.tokens[i]:
+            mism += 1
+            assert out.tokens[i] in set(int(c) for c, pr in zip(tr.cand_ids, tr.cand_probs) if pr > 0), f"step {i}"
+        lg = g.forward_token(out.tokens[i], gc)
+    assert mism <= 1, f"{mism} of {n} sampled ids differ"

@@ -89,3 +89,17 @@ def test_kv_cache_push_and_len():
     assert c.total_len() == 0
     with pytest.raises(O.OracleError, match="kv row width"):
         c.push(0, [0.1], [0.2])
+
+
+def test_kv_cache_push_rows_equals_row_pushes():
+    rng = np.random.default_rng(5)
+    k = rng.standard_normal(6 * 4).astype(np.float32)
+    v = rng.standard_normal(6 * 4).astype(np.float32)
+    a, b = O.OracleCache(2, 4), O.OracleCache(2, 4)
+    a.push_rows(1, k, v)
+    for i in range(6):
+        b.push(1, k[4 * i:4 * i + 4], v[4 * i:4 * i + 4])
+    assert a.len(1) == b.len(1) == 6
+    assert np.array_equal(a.keys_flat(1), b.keys_flat(1)) and np.array_equal(a.values_flat(1), b.values_flat(1))
+    with pytest.raises(O.OracleError, match="kv row width"):
+        a.push_rows(0, k[:5], v[:5])
