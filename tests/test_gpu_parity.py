@@ -354,3 +354,71 @@ def test_four_b_sampled_generation(T, O, W, four_b):
             assert out.tokens[i] in set(int(c) for c, pr in zip(tr.cand_ids, tr.cand_probs) if pr > 0), f"step {i}"
         lg = g.forward_token(out.tokens[i], gc)
     assert mism <= 1, f"{mism} of {n} sampled ids differ"
+
+
+# --- long prompts: the tiled MFMA GEMM and the MFMA prefill attention ---------
+
+def test_tiled_gemm_prefill_tiny(T, O, untied):
+    # 300 tokens >= the tiled-GEMM threshold: N not a multiple of the 128-token
+    # tile, M (hidden 64) smaller than the 128-row tile
+    g, o, wl = untied
+    ids = [int(t) for t in T.synth_tokens(51, 300, wl.vocab_size)]
+    gc, oc = T.KvCache(g, 320), o.new_cache()
+    close_logits(g.forward_seq(ids, gc), o.forward_seq(ids, oc), "prefill 300")
+    for layer in range(wl.num_hidden_layers):
+        assert np.abs(gc.keys_flat(layer) - oc.keys_flat(layer)).max() < 1e-4
+        assert np.abs(gc.values_flat(layer) - oc.values_flat(layer)).max() < 1e-4
+
+
+def test_long_prefill_chunks_vs_oracle(T, O, W, one_b):
+    # 1B model: a 700-token prefill, a second 333-token chunk starting at 700
+    # (MFMA attention with start > 0, partial query blocks), then decode steps
+    g, o = one_b
+    ids = [int(t) for t in W.LONG_CTX.prompt()[:1040]]
+    O.set_attn_threads(max(1, min(16, os.cpu_count() or 1)))
+    try:
+        gc, oc = T.KvCache(g, 1100), o.new_cache()
+        print("1B prefill 700", flush=True)
+        close_logits(g.forward_seq(ids[:700], gc), o.forward_seq(ids[:700], oc), "prefill 700")
+        print("1B prefill 333 at 700", flush=True)
+        close_logits(g.forward_seq(ids[700:1033], gc), o.forward_seq(ids[700:1033], oc), "prefill 333 at 700")
+        for layer in (0, 11, 23):
+            for a, b in ((gc.keys_flat(layer), oc.keys_flat(layer)), (gc.values_flat(layer), oc.values_flat(layer))):
+                d = np.abs(a - b)
+                assert np.all(d <= ABS_TOL + REL_TOL * np.abs(b)), f"layer {layer} kv: {d.max():.3e}"
+        for i in range(1033, 1040):
+            close_logits(g.forward_token(ids[i], gc), o.forward_token(ids[i], oc), f"decode at {i}")
+    finally:
+        O.set_attn_threads(1)
+
+
+def test_long_context_8k_prefill_matches_decode_path(T, W, one_b):
+    """The 8192-token prompt at full size, where the oracle would need about
+    ten minutes: the batched prefill (tiled GEMM, MFMA attention) against the
+    same ids fed one by one through the decode path (GEMV, split-K decode
+    attention) -- two independent device paths.  Last-token logits within the
+    logits tolerance (the reference bounds forward_seq vs forward_token by
+    1e-2, tests/diff_debug.rs:39), KV caches within it, and the greedy
+    continuations identical."""
+    g, _ = one_b
+    wl = W.LONG_CTX
+    ids = [int(t) for t in wl.prompt()]
+    n = len(ids)
+    pc = T.KvCache(g, n + 16)
+    print("8k prefill", flush=True)
+    a = g.forward_seq(ids, pc)
+    dc = T.KvCache(g, n + 16)
+    print("8k token by token", flush=True)
+    for t in ids[:-1]:
+        g.forward_token(t, dc, want_logits=False)
+    b = g.forward_token(ids[-1], dc)
+    close_logits(a, b, "8k prefill vs decode path")
+    for layer in (0, 23):
+        for x, y in ((pc.keys_flat(layer), dc.keys_flat(layer)), (pc.values_flat(layer), dc.values_flat(layer))):
+            d = np.abs(x - y)
+            assert np.all(d <= ABS_TOL + REL_TOL * np.abs(y)), f"layer {layer} kv: {d.max():.3e}"
+    first = int(np.argmax(a))
+    assert first == int(np.argmax(b))
+    ta, _ = g.decode_greedy(first, 16, pc)
+    tb, _ = g.decode_greedy(first, 16, dc)
+    assert list(ta) == list(tb)

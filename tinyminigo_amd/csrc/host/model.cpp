@@ -705,7 +705,10 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         aa.min_chunk = 1;
         aa.out_hi = m->pf_ahi;
         aa.out_lo = m->pf_alo;
-        TMG_HIP(launch_attn(aa, s));
+        if (attn_prefill_supported(aa))
+            TMG_HIP(launch_attn_prefill(aa, s));
+        else
+            TMG_HIP(launch_attn(aa, s));
 
         GemmArgs o{};
         o.W = ly.o;

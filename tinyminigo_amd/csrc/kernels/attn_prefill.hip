@@ -1,0 +1,277 @@
+// Causal GQA prefill attention on bf16 MFMA (reference attention_batch,
+// src/tensor.rs:1099-1139, used by forward_seq, src/model.rs:555-566).
+//
+// A workgroup owns 128 query columns -- 128/GROUP consecutive positions of
+// the GROUP query heads that share KV head g -- and walks the causal range of
+// the KV cache in blocks of 64 keys.  Each block of K and V is staged once in
+// LDS for all GROUP heads.  The f32 operands are carried as split-bf16 pairs
+// x = hi + lo (|x - hi - lo| <= 2^-18 |x|) and every product takes three MFMAs
+// (hi*hi + hi*lo + lo*hi), so the scores and the output keep close to f32
+// accuracy.
+//
+// Scores are computed transposed, S^T = K Q^T (v_mfma_f32_16x16x32_bf16: A =
+// 16 keys x 32 dims, B = 32 dims x 16 query columns), which leaves every lane
+// with the scores of one query column.  The online softmax (running max and
+// sum per column, exp2 of log2-scaled scores) therefore needs no transposes,
+// and the probabilities feed O^T += V^T P^T directly from registers: the
+// contraction over keys may visit the keys in any order as long as both
+// operands agree, so a lane's k-slots are the keys it already holds (4 from
+// each of two adjacent 16-key tiles), and V^T is read from an LDS copy
+// stored [dim][key] in the same order.
+#include "common.cuh"
+#include "kernels.hpp"
+
+namespace tmg {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPHD = 128;        // head dim
+constexpr int kPKB = 64;         // keys per block
+constexpr int kPCols = 128;      // query columns per workgroup (32 per wavefront)
+constexpr int kSKP = kPHD + 8;   // sK row pitch, bf16
+constexpr int kSVP = kPKB + 8;   // sV row pitch, bf16
+
+__device__ __forceinline__ void split2(float x, uint16_t &h, uint16_t &l) {
+    h = f32_to_bf16_rne(x);
+    l = f32_to_bf16_rne(x - bf16_to_f32(h));
+}
+
+// 8 floats -> (hi, lo) bf16x8 fragments
+__device__ __forceinline__ void split8(const float (&v)[8], bf16x8 &hi, bf16x8 &lo) {
+    u32x4 h, l;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint16_t h0, l0, h1, l1;
+        split2(v[2 * i], h0, l0);
+        split2(v[2 * i + 1], h1, l1);
+        h[i] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+        l[i] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+    }
+    hi = __builtin_bit_cast(bf16x8, h);
+    lo = __builtin_bit_cast(bf16x8, l);
+}
+
+__device__ __forceinline__ float max_xor16_32(float v) {
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    return v;
+}
+
+template <int GROUP>
+__global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) {
+    constexpr int QB = kPCols / GROUP;  // query positions per workgroup
+    __shared__ __attribute__((aligned(16))) uint16_t sK[2][kPKB][kSKP];  // [hi/lo][key][dim]
+    __shared__ __attribute__((aligned(16))) uint16_t sV[2][kPHD][kSVP];  // [hi/lo][dim][key]
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int r = lane & 15, q4 = lane >> 4;
+    const int nqb = (a.T + QB - 1) / QB;
+    const int qb = nqb - 1 - (int)blockIdx.x;  // longest causal ranges first
+    const int g = blockIdx.y;
+    const int kvd = a.nkv * kPHD, qd = a.nq * kPHD;
+    const int n_total = a.start + a.T;  // cache rows holding keys
+
+    // this lane's query column in each of its two 16-column tiles
+    int ti[2], qpos[2], qhead[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        const int c = wave * 32 + qt * 16 + r;
+        const int hh = c / QB, p = c - hh * QB;
+        ti[qt] = qb * QB + p;
+        qpos[qt] = a.start + ti[qt];
+        qhead[qt] = g * GROUP + hh;
+    }
+    // Q^T fragments (MFMA B operand): dims 32 ds + 8 q4 .. +7 of the column
+    bf16x8 qh[2][4], ql[2][4];
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        const float *src = a.q + (size_t)min(ti[qt], a.T - 1) * qd + qhead[qt] * kPHD + 8 * q4;
+#pragma unroll
+        for (int ds = 0; ds < 4; ds++) {
+            const float4 v0 = *reinterpret_cast<const float4 *>(src + 32 * ds);
+            const float4 v1 = *reinterpret_cast<const float4 *>(src + 32 * ds + 4);
+            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            split8(v, qh[qt][ds], ql[qt][ds]);
+        }
+    }
+    const float sl2 = a.scale * 1.4426950408889634f;  // scores in log2 units
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+    f32x4 o[2][8];
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) o[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int last_pos = a.start + min(a.T, (qb + 1) * QB) - 1;  // the workgroup's last query position
+    const int nkb = last_pos / kPKB + 1;
+    const float *kbase = a.k_cache + g * kPHD;
+    const float *vbase = a.v_cache + g * kPHD;
+    for (int kb = 0; kb < nkb; kb++) {
+        const int k0 = kb * kPKB;
+        __syncthreads();  // the previous block's fragments are read
+        // stage K [key][dim] (rows past the filled cache are zeros)
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int key = (t >> 5) + 8 * i, d = 4 * (t & 31);
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (k0 + key < n_total) v = *reinterpret_cast<const float4 *>(kbase + (size_t)(k0 + key) * kvd + d);
+            uint16_t h[4], lo[4];
+            split2(v.x, h[0], lo[0]);
+            split2(v.y, h[1], lo[1]);
+            split2(v.z, h[2], lo[2]);
+            split2(v.w, h[3], lo[3]);
+            *reinterpret_cast<u32x2 *>(&sK[0][key][d]) =
+                u32x2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+            *reinterpret_cast<u32x2 *>(&sK[1][key][d]) =
+                u32x2{(uint32_t)lo[0] | ((uint32_t)lo[1] << 16), (uint32_t)lo[2] | ((uint32_t)lo[3] << 16)};
+        }
+        // stage V transposed [dim][key], two keys per 32-bit store
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int key0 = 2 * ((t >> 5) + 8 * i), d = 4 * (t & 31);
+            float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+            if (k0 + key0 < n_total) v0 = *reinterpret_cast<const float4 *>(vbase + (size_t)(k0 + key0) * kvd + d);
+            if (k0 + key0 + 1 < n_total)
+                v1 = *reinterpret_cast<const float4 *>(vbase + (size_t)(k0 + key0 + 1) * kvd + d);
+            const float a0[4] = {v0.x, v0.y, v0.z, v0.w}, a1[4] = {v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                uint16_t h0, l0, h1, l1;
+                split2(a0[j], h0, l0);
+                split2(a1[j], h1, l1);
+                *reinterpret_cast<uint32_t *>(&sV[0][d + j][key0]) = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                *reinterpret_cast<uint32_t *>(&sV[1][d + j][key0]) = (uint32_t)l0 | ((uint32_t)l1 << 16);
+            }
+        }
+        __syncthreads();
+
+        // S^T = K Q^T: 4 key tiles x 2 query tiles
+        f32x4 s[4][2];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int qt = 0; qt < 2; qt++) s[kt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ds = 0; ds < 4; ds++) {
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++) {
+                const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(&sK[0][kt * 16 + r][32 * ds + 8 * q4]);
+                const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(&sK[1][kt * 16 + r][32 * ds + 8 * q4]);
+#pragma unroll
+                for (int qt = 0; qt < 2; qt++) {
+                    s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[qt][ds], s[kt][qt], 0, 0, 0);
+                    s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[qt][ds], s[kt][qt], 0, 0, 0);
+                    s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[qt][ds], s[kt][qt], 0, 0, 0);
+                }
+            }
+        }
+        // online softmax per query column; this lane holds keys k0 + 16 kt + 4 q4 + i
+#pragma unroll
+        for (int qt = 0; qt < 2; qt++) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int kp = k0 + 16 * kt + 4 * q4 + i;
+                    const float x = kp <= qpos[qt] ? s[kt][qt][i] * sl2 : -INFINITY;
+                    s[kt][qt][i] = x;
+                    mx = fmaxf(mx, x);
+                }
+            mx = max_xor16_32(mx);
+            const float m_new = fmaxf(m[qt], mx);  // finite: key 0 precedes every query
+            const float corr = exp2f(m[qt] - m_new);
+            m[qt] = m_new;
+            l[qt] *= corr;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) o[qt][dt] *= corr;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float p = exp2f(s[kt][qt][i] - m_new);
+                    s[kt][qt][i] = p;
+                    l[qt] += p;
+                }
+        }
+        // O^T += V^T P^T, 32 keys per step: tiles 2 ks and 2 ks + 1
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            bf16x8 ph[2], pl[2];
+#pragma unroll
+            for (int qt = 0; qt < 2; qt++) {
+                const float pv[8] = {s[2 * ks][qt][0],     s[2 * ks][qt][1],     s[2 * ks][qt][2],
+                                     s[2 * ks][qt][3],     s[2 * ks + 1][qt][0], s[2 * ks + 1][qt][1],
+                                     s[2 * ks + 1][qt][2], s[2 * ks + 1][qt][3]};
+                split8(pv, ph[qt], pl[qt]);
+            }
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                const int dim = dt * 16 + r;
+                const u32x2 h0 = *reinterpret_cast<const u32x2 *>(&sV[0][dim][32 * ks + 4 * q4]);
+                const u32x2 h1 = *reinterpret_cast<const u32x2 *>(&sV[0][dim][32 * ks + 16 + 4 * q4]);
+                const u32x2 l0 = *reinterpret_cast<const u32x2 *>(&sV[1][dim][32 * ks + 4 * q4]);
+                const u32x2 l1 = *reinterpret_cast<const u32x2 *>(&sV[1][dim][32 * ks + 16 + 4 * q4]);
+                const bf16x8 vh = __builtin_bit_cast(bf16x8, u32x4{h0[0], h0[1], h1[0], h1[1]});
+                const bf16x8 vl = __builtin_bit_cast(bf16x8, u32x4{l0[0], l0[1], l1[0], l1[1]});
+#pragma unroll
+                for (int qt = 0; qt < 2; qt++) {
+                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[qt], o[qt][dt], 0, 0, 0);
+                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl[qt], o[qt][dt], 0, 0, 0);
+                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph[qt], o[qt][dt], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // normalize and write the split-bf16 output: O^T rows dims 16 dt + 4 q4 + i
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+        const float L = add_xor32(add_xor16(l[qt]));  // the column's four lane groups
+        if (ti[qt] >= a.T) continue;
+        const float inv = 1.0f / L;
+        const size_t ob = (size_t)ti[qt] * qd + qhead[qt] * kPHD;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int d = dt * 16 + 4 * q4 + i;
+                split_bf16(o[qt][dt][i] * inv, a.out_hi + ob + d, a.out_lo + ob + d);
+            }
+        }
+    }
+}
+
+}  // namespace
+
+bool attn_prefill_supported(const AttnArgs &a) {
+    const int group = a.nkv > 0 ? a.nq / a.nkv : 0;
+    // short prompts keep the per-row kernel: a few query blocks cannot fill the chip
+    return a.hd == kPHD && a.out_hi && a.out_lo && a.nq == group * a.nkv && a.T >= kTiledMinTokens &&
+           (group == 1 || group == 2 || group == 4 || group == 8);
+}
+
+hipError_t launch_attn_prefill(const AttnArgs &a, hipStream_t s) {
+    if (!attn_prefill_supported(a) || a.T <= 0) return hipErrorInvalidValue;
+    const int group = a.nq / a.nkv;
+    const int QB = kPCols / group;
+    const dim3 grid((a.T + QB - 1) / QB, a.nkv);
+    switch (group) {
+        case 1: hipLaunchKernelGGL(attn_prefill_kernel<1>, grid, dim3(kBlock), 0, s, a); break;
+        case 2: hipLaunchKernelGGL(attn_prefill_kernel<2>, grid, dim3(kBlock), 0, s, a); break;
+        case 4: hipLaunchKernelGGL(attn_prefill_kernel<4>, grid, dim3(kBlock), 0, s, a); break;
+        case 8: hipLaunchKernelGGL(attn_prefill_kernel<8>, grid, dim3(kBlock), 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace tmg

@@ -82,6 +82,10 @@ struct AttnArgs {
 };
 
 hipError_t launch_attn(const AttnArgs &a, hipStream_t s);
+// Causal prefill attention on MFMA (head_dim 128, split-bf16 output): the
+// shapes it takes, and the launch.
+bool attn_prefill_supported(const AttnArgs &a);
+hipError_t launch_attn_prefill(const AttnArgs &a, hipStream_t s);
 // Merges the split-K partials of a decode attention launch into out_f32
 // (used when the merge is not fused into the o_proj GEMV prologue).
 hipError_t launch_attn_combine(const AttnArgs &a, hipStream_t s);
@@ -125,6 +129,9 @@ struct GemmArgs {
     float *k_cache, *v_cache;
 };
 
+// Prompts of at least kTiledMinTokens tokens (and K a multiple of 64) use the
+// LDS-tiled 128x128 kernel; shorter ones the 16x64 streaming kernel.
+constexpr int kTiledMinTokens = 256;
 hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s);
 
 // Copy row `row` of x[T,H] to dst[H] (last prefill row -> decode residual).

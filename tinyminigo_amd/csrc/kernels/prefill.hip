@@ -43,56 +43,10 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_split_kernel(const float *x, c
     }
 }
 
-// MFMA GEMM D[m][n] = sum_k W[m][k] * (Bhi[n][k] + Blo[n][k]).
-//
-// Workgroup tile: 16 weight rows x 64 tokens; the four wavefronts split K in
-// interleaved 32-wide steps and are summed through LDS.  MFMA
-// v_mfma_f32_16x16x32_bf16 operand layout: lane l supplies A row (l & 15),
-// k = 8*(l >> 4) .. +7, and B column (l & 15), the same k; it receives D rows
-// 4*(l >> 4) .. +3 of column (l & 15).  So every lane owns two adjacent
-// weight-row pairs of one token, which is what the pair epilogues need.
+// Epilogue of one MFMA output fragment: rows mb .. mb+3 (mb a multiple of 4)
+// of token column n.  Pair epilogues use rows (mb, mb+1) and (mb+2, mb+3).
 template <int EPI>
-__global__ __launch_bounds__(kBlock) void gemm_kernel(const GemmArgs a) {
-    constexpr int NB = 4;  // 16-token column blocks per workgroup
-    __shared__ f32x4 s_acc[4][NB][64];
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-    const int m0 = blockIdx.x * 16, n0 = blockIdx.y * 16 * NB;
-    const int K = a.K;
-    const int r = lane & 15, kq = (lane >> 4) * 8;
-    const uint16_t *Ap = a.W + (size_t)min(m0 + r, a.M - 1) * K + kq;
-    const uint16_t *Bh[NB], *Bl[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++) {
-        const int n = min(n0 + nb * 16 + r, a.N - 1);
-        Bh[nb] = a.Bhi + (size_t)n * K + kq;
-        Bl[nb] = a.Blo + (size_t)n * K + kq;
-    }
-    f32x4 acc[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int k = wave * 32; k < K; k += 128) {
-        const u32x4 av = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(Ap + k));
-        u32x4 bh[NB], bl[NB];
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++) {
-            bh[nb] = *reinterpret_cast<const u32x4 *>(Bh[nb] + k);
-            bl[nb] = *reinterpret_cast<const u32x4 *>(Bl[nb] + k);
-        }
-        const bf16x8 A = __builtin_bit_cast(bf16x8, av);
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++) {
-            acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8, bh[nb]), acc[nb], 0, 0, 0);
-            acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8, bl[nb]), acc[nb], 0, 0, 0);
-        }
-    }
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++) s_acc[wave][nb][lane] = acc[nb];
-    __syncthreads();
-    // wave w finishes column block nb = w
-    const int nb = wave;
-    const f32x4 v = (s_acc[0][nb][lane] + s_acc[1][nb][lane]) + (s_acc[2][nb][lane] + s_acc[3][nb][lane]);
-    const int n = n0 + nb * 16 + (lane & 15);
-    const int mb = m0 + (lane >> 4) * 4;  // rows mb .. mb+3
+__device__ __forceinline__ void gemm_store(const GemmArgs &a, int mb, int n, const f32x4 &v) {
     if (n >= a.N) return;
     if constexpr (EPI == GEPI_STORE || EPI == GEPI_RESID) {
         float *yr = a.y + (size_t)n * a.M;
@@ -144,6 +98,144 @@ __global__ __launch_bounds__(kBlock) void gemm_kernel(const GemmArgs a) {
     }
 }
 
+// MFMA GEMM D[m][n] = sum_k W[m][k] * (Bhi[n][k] + Blo[n][k]).
+//
+// Workgroup tile: 16 weight rows x 64 tokens; the four wavefronts split K in
+// interleaved 32-wide steps and are summed through LDS.  MFMA
+// v_mfma_f32_16x16x32_bf16 operand layout: lane l supplies A row (l & 15),
+// k = 8*(l >> 4) .. +7, and B column (l & 15), the same k; it receives D rows
+// 4*(l >> 4) .. +3 of column (l & 15).  So every lane owns two adjacent
+// weight-row pairs of one token, which is what the pair epilogues need.
+template <int EPI>
+__global__ __launch_bounds__(kBlock) void gemm_kernel(const GemmArgs a) {
+    constexpr int NB = 4;  // 16-token column blocks per workgroup
+    __shared__ f32x4 s_acc[4][NB][64];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int m0 = blockIdx.x * 16, n0 = blockIdx.y * 16 * NB;
+    const int K = a.K;
+    const int r = lane & 15, kq = (lane >> 4) * 8;
+    const uint16_t *Ap = a.W + (size_t)min(m0 + r, a.M - 1) * K + kq;
+    const uint16_t *Bh[NB], *Bl[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+        const int n = min(n0 + nb * 16 + r, a.N - 1);
+        Bh[nb] = a.Bhi + (size_t)n * K + kq;
+        Bl[nb] = a.Blo + (size_t)n * K + kq;
+    }
+    f32x4 acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k = wave * 32; k < K; k += 128) {
+        const u32x4 av = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(Ap + k));
+        u32x4 bh[NB], bl[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+            bh[nb] = *reinterpret_cast<const u32x4 *>(Bh[nb] + k);
+            bl[nb] = *reinterpret_cast<const u32x4 *>(Bl[nb] + k);
+        }
+        const bf16x8 A = __builtin_bit_cast(bf16x8, av);
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+            acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8, bh[nb]), acc[nb], 0, 0, 0);
+            acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, __builtin_bit_cast(bf16x8, bl[nb]), acc[nb], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) s_acc[wave][nb][lane] = acc[nb];
+    __syncthreads();
+    // wave w finishes column block nb = w
+    const int nb = wave;
+    const f32x4 v = (s_acc[0][nb][lane] + s_acc[1][nb][lane]) + (s_acc[2][nb][lane] + s_acc[3][nb][lane]);
+    const int n = n0 + nb * 16 + (lane & 15);
+    const int mb = m0 + (lane >> 4) * 4;  // rows mb .. mb+3
+    gemm_store<EPI>(a, mb, n, v);
+}
+
+// Tiled MFMA GEMM for long prompts: workgroup tile 128 weight rows x 128
+// tokens, K in steps of 64 staged through LDS (W, Bhi, Blo; rows padded to
+// 72 bf16 against bank conflicts).  The four wavefronts each own a 64 x 64
+// quarter (4 x 4 MFMA fragments).  The next K step's global loads are held
+// in registers while the current one is multiplied.
+constexpr int kTM = 128, kTN = 128, kTK = 64, kTKP = kTK + 8;
+
+template <int EPI>
+__global__ __launch_bounds__(kBlock) void gemm_tiled_kernel(const GemmArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t sA[kTM][kTKP];
+    __shared__ __attribute__((aligned(16))) uint16_t sH[kTN][kTKP];
+    __shared__ __attribute__((aligned(16))) uint16_t sL[kTN][kTKP];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int m0 = blockIdx.x * kTM, n0 = blockIdx.y * kTN;
+    const int K = a.K;
+    // global -> register staging: chunk c = t + 256 i (i < 4) is row c >> 3,
+    // 16-byte column c & 7 of each 128 x 64 tile
+    const uint16_t *gA[4], *gH[4], *gL[4];
+    int srow[4], scol[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = t + kBlock * i;
+        srow[i] = c >> 3;
+        scol[i] = (c & 7) * 8;
+        const int m = min(m0 + srow[i], a.M - 1), n = min(n0 + srow[i], a.N - 1);
+        gA[i] = a.W + (size_t)m * K + scol[i];
+        gH[i] = a.Bhi + (size_t)n * K + scol[i];
+        gL[i] = a.Blo + (size_t)n * K + scol[i];
+    }
+    u32x4 rA[4], rH[4], rL[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        rA[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gA[i]));
+        rH[i] = *reinterpret_cast<const u32x4 *>(gH[i]);
+        rL[i] = *reinterpret_cast<const u32x4 *>(gL[i]);
+    }
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int r = lane & 15, kq = (lane >> 4) * 8;
+    for (int k0 = 0; k0 < K; k0 += kTK) {
+        __syncthreads();  // the previous step's fragments are read
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            *reinterpret_cast<u32x4 *>(&sA[srow[i]][scol[i]]) = rA[i];
+            *reinterpret_cast<u32x4 *>(&sH[srow[i]][scol[i]]) = rH[i];
+            *reinterpret_cast<u32x4 *>(&sL[srow[i]][scol[i]]) = rL[i];
+        }
+        __syncthreads();
+        if (k0 + kTK < K) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                rA[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gA[i] + k0 + kTK));
+                rH[i] = *reinterpret_cast<const u32x4 *>(gH[i] + k0 + kTK);
+                rL[i] = *reinterpret_cast<const u32x4 *>(gL[i] + k0 + kTK);
+            }
+        }
+#pragma unroll
+        for (int kk = 0; kk < kTK; kk += 32) {
+            bf16x8 fa[4], fh[4], fl[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                fa[i] = *reinterpret_cast<const bf16x8 *>(&sA[wm * 64 + i * 16 + r][kk + kq]);
+                fh[i] = *reinterpret_cast<const bf16x8 *>(&sH[wn * 64 + i * 16 + r][kk + kq]);
+                fl[i] = *reinterpret_cast<const bf16x8 *>(&sL[wn * 64 + i * 16 + r][kk + kq]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fh[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fl[j], acc[i][j], 0, 0, 0);
+                }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            gemm_store<EPI>(a, m0 + wm * 64 + i * 16 + (lane >> 4) * 4, n0 + wn * 64 + j * 16 + r, acc[i][j]);
+}
+
 __global__ void copy_row_kernel(const float *x, int row, int H, float *dst) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < H; i += gridDim.x * blockDim.x)
         dst[i] = x[(size_t)row * H + i];
@@ -165,6 +257,17 @@ hipError_t launch_rmsnorm_split(const float *x, const float *w, float eps, int T
 
 hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
     if (a.K % 32 != 0 || a.M <= 0 || a.N <= 0) return hipErrorInvalidValue;
+    if (a.N >= kTiledMinTokens && a.K % kTK == 0) {
+        const dim3 grid((a.M + kTM - 1) / kTM, (a.N + kTN - 1) / kTN);
+        switch (epi) {
+            case GEPI_STORE: hipLaunchKernelGGL(gemm_tiled_kernel<GEPI_STORE>, grid, dim3(kBlock), 0, s, a); break;
+            case GEPI_RESID: hipLaunchKernelGGL(gemm_tiled_kernel<GEPI_RESID>, grid, dim3(kBlock), 0, s, a); break;
+            case GEPI_SWIGLU: hipLaunchKernelGGL(gemm_tiled_kernel<GEPI_SWIGLU>, grid, dim3(kBlock), 0, s, a); break;
+            case GEPI_QKV: hipLaunchKernelGGL(gemm_tiled_kernel<GEPI_QKV>, grid, dim3(kBlock), 0, s, a); break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     const dim3 grid((a.M + 15) / 16, (a.N + 63) / 64);
     switch (epi) {
         case GEPI_STORE: hipLaunchKernelGGL(gemm_kernel<GEPI_STORE>, grid, dim3(kBlock), 0, s, a); break;
