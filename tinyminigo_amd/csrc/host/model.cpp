@@ -342,7 +342,6 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
         aa.pos_dev = &c->st->pos;
         aa.scale = 1.0f / sqrtf((float)m->hd);
         aa.nsplit = c->attn_nsplit;
-        aa.min_chunk = kMinChunk;
         aa.cap = (int)c->max_pos;
         aa.part = m->attn_part;
         aa.part_ml = m->attn_ml;
@@ -365,7 +364,6 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
             oa.part_ml = m->attn_ml;
             oa.pos = &c->st->pos;
             oa.nsplit = c->attn_nsplit;
-            oa.min_chunk = kMinChunk;
             oa.hd = m->hd;
             oa.group = m->nq / m->nkv;
         }
@@ -467,7 +465,6 @@ int build_plan(tmg_model *m, tmg_cache *c) {
         o.part_ml = m->attn_ml;
         o.pos = &c->st->pos;
         o.nsplit = c->attn_nsplit;
-        o.min_chunk = kMinChunk;
         o.hd = m->hd;
         o.group = m->nq / m->nkv;
         GemvArgs &g = pl->gu[l];
@@ -495,7 +492,6 @@ int build_plan(tmg_model *m, tmg_cache *c) {
         a.pos_dev = &c->st->pos;
         a.scale = 1.0f / sqrtf((float)m->hd);
         a.nsplit = c->attn_nsplit;
-        a.min_chunk = kMinChunk;
         a.part = m->attn_part;
         a.part_ml = m->attn_ml;
     }
@@ -527,7 +523,6 @@ int enqueue_persistent(tmg_model *m, tmg_cache *c, int steps, bool *used) {
     a.nq = m->nq;
     a.nkv = m->nkv;
     a.nsplit = c->attn_nsplit;
-    a.min_chunk = kMinChunk;
     a.fused_merge = c->attn_nsplit <= kFusedSplits;
     a.nparts = m->argmax_nparts;
     a.attn_out = m->attn_out;
@@ -702,7 +697,6 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         aa.start = start;
         aa.scale = 1.0f / sqrtf((float)m->hd);
         aa.nsplit = 1;
-        aa.min_chunk = 1;
         aa.out_hi = m->pf_ahi;
         aa.out_lo = m->pf_alo;
         if (attn_prefill_supported(aa))
@@ -820,7 +814,7 @@ extern "C" int tmg_cache_new(tmg_model *m, uint32_t max_pos, tmg_cache **out) {
     tmg_cache *c = new tmg_cache();
     c->model = m;
     c->max_pos = max_pos;
-    c->attn_nsplit = (int)std::min<uint32_t>(kMaxSplits, (max_pos + kMinChunk - 1) / kMinChunk);
+    c->attn_nsplit = (int)std::min<uint32_t>(kMaxSplits, (max_pos + kAttnBlock - 1) / kAttnBlock);
     const size_t n = (size_t)m->L * max_pos * m->kvd;
     int rc = TMG_OK;
     void *k = nullptr, *v = nullptr, *st = nullptr, *hist = nullptr;

@@ -77,11 +77,10 @@ struct tmg_cache {
 
 namespace tmg {
 
-// Decode attention: each split covers at least kMinChunk positions; a cache
-// of max_pos rows uses up to ceil(max_pos / kMinChunk) splits (at most
-// kMaxSplits).  Up to kFusedSplits the merge runs in the o_proj GEMV
-// prologue; above that a combine kernel runs first.
-constexpr int kMinChunk = 64;
+// Decode attention: the context is dealt to the splits in kAttnBlock-position
+// blocks; a cache of max_pos rows uses up to ceil(max_pos / kAttnBlock)
+// splits (at most kMaxSplits).  Up to kFusedSplits the merge runs in the
+// o_proj GEMV prologue; above that a combine kernel runs first.
 constexpr int kMaxSplits = 64;
 
 // Launch filter used by tmg_profile_decode_step: every kernel of the step is

@@ -4,8 +4,8 @@
 // Reference: decode attention src/model.rs:434-459, attention_batch
 // src/tensor.rs:1099-1139, softmax src/tensor.rs:1055-1060.
 //
-// One call handles one (query row, KV head, split) item: positions
-// [t0, t1) of the row's context, for all GROUP query heads of the KV head, so
+// One call handles one (query row, KV head, split) item: the split's
+// 64-position blocks of the row's context, for all GROUP query heads of the KV head, so
 // every K/V load serves GROUP heads.  TS = HD/4 lanes own one position (a
 // float4 of K and of V each); the 256 threads form NTEAM such teams.  Each
 // team keeps its own online-softmax state (running max, sum, output) over the
@@ -43,25 +43,22 @@ struct AttnGeom {
 
 // Split count of a decode attention row at context n_ctx: the same formula in
 // the attention kernel, its combine kernel and the fused combine prologue.
-__device__ __forceinline__ int active_splits(int n_ctx, int nsplit, int min_chunk) {
-    return min(nsplit, (n_ctx + min_chunk - 1) / min_chunk);
+__device__ __forceinline__ int active_splits(int n_ctx, int nsplit) {
+    return min(nsplit, (n_ctx + kAttnBlock - 1) / kAttnBlock);
 }
 
-// Positions per split: at least min_chunk, and the context spread over the
-// nsplit splits once it is longer than nsplit * min_chunk.  Split s covers
-// [s * chunk, min(n_ctx, (s + 1) * chunk)); the active splits are
-// ceil(n_ctx / chunk) = min(nsplit, ceil(n_ctx / min_chunk)).
-__device__ __forceinline__ int attn_chunk(int n_ctx, int nsplit, int min_chunk) {
-    return max(min_chunk, (n_ctx + nsplit - 1) / nsplit);
-}
+// Partition of a row's context [0, n_ctx) over the splits: 64-position
+// blocks (one chunk of the lane geometry) dealt round robin, split s taking
+// blocks s, s + nsplit, s + 2 nsplit, ...  So split s always starts at
+// position 64 s, and the active splits are min(nsplit, ceil(n_ctx / 64)).
 
 // With out_f32/out_hi null, or more than one active split, writes (o, max,
 // sum) partials (a split without positions writes max = -inf, sum = 0);
 // otherwise writes the normalized row.
-// With SPEC (decode), the split's first chunk [split * min_chunk, + CH) is
-// loaded before the position is read from a.pos_dev (rows clamped to the
-// cache capacity a.cap), so the K/V loads do not wait for it; qpos and active
-// are then computed here and the arguments ignored.  Splits found inactive
+// With SPEC (decode), the split's first chunk [64 split, + 64) is loaded
+// before the position is read from a.pos_dev (rows clamped to the cache
+// capacity a.cap), so the K/V loads do not wait for it; qpos and active are
+// then computed here and the arguments ignored.  Splits found inactive
 // return at once.
 template <int HD, int GROUP, bool COH, bool PREFETCH = true, bool SPEC = false>
 __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, int ti, int qpos, int active,
@@ -81,13 +78,14 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
 #pragma unroll
     for (int h = 0; h < GROUP; h++) qv[h] = ldf4<COH>(qrow + (g * GROUP + h) * HD + lt * 4);
 
+    static_assert(CH == 64, "the split partition deals 64-position blocks");
     float4 kr[J], vr[J];
-    const int spec_t0 = split * a.min_chunk;
+    const int c_first = split * CH, c_step = a.nsplit * CH;
     if constexpr (SPEC) {
         const int pos0 = *a.pos_dev;  // a scalar load, first used after the K/V loads are issued
 #pragma unroll
         for (int j = 0; j < J; j++) {
-            const int p = min(spec_t0 + team + j * NTEAM, a.cap - 1);
+            const int p = min(c_first + team + j * NTEAM, a.cap - 1);
             kr[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
             vr[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
         }
@@ -95,12 +93,10 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
         // compiler sinks them behind it (into the branch that uses them)
         asm volatile("" ::: "memory");
         qpos = pos0 + ti;
-        active = active_splits(qpos + 1, a.nsplit, a.min_chunk);
+        active = active_splits(qpos + 1, a.nsplit);
         if (split >= active) return;
     }
     const int n_ctx = qpos + 1;
-    const int chunk = attn_chunk(n_ctx, a.nsplit, a.min_chunk);
-    const int t0 = split * chunk, t1 = min(n_ctx, t0 + chunk);
 
     float m_run[GROUP], l_run[GROUP];
     float4 o_acc[GROUP];
@@ -111,25 +107,25 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
         o_acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
 
-    // Rows past t1 are loaded clamped (branch-free) and masked where used:
-    // their score is -inf and their V row is replaced by zeros (0 * garbage
-    // could be NaN).
-    const int last = max(t1 - 1, 0);
-    if (!SPEC || t0 != spec_t0) {
+    // Rows past the context are loaded clamped (branch-free) and masked where
+    // used: their score is -inf and their V row is replaced by zeros (0 *
+    // garbage could be NaN).
+    const int last = n_ctx - 1;
+    if constexpr (!SPEC) {
 #pragma unroll
         for (int j = 0; j < J; j++) {
-            const int p = min(t0 + team + j * NTEAM, last);
+            const int p = min(c_first + team + j * NTEAM, last);
             kr[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
             vr[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
         }
     }
-    for (int c0 = t0; c0 < t1; c0 += CH) {
+    for (int c0 = c_first; c0 < n_ctx; c0 += c_step) {
         float4 kn[J], vn[J];
-        const bool more = c0 + CH < t1;
+        const bool more = c0 + c_step < n_ctx;
         if (PREFETCH && more) {
 #pragma unroll
             for (int j = 0; j < J; j++) {
-                const int p = min(c0 + CH + team + j * NTEAM, last);
+                const int p = min(c0 + c_step + team + j * NTEAM, last);
                 kn[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
                 vn[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
             }
@@ -138,7 +134,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
         float s[J][GROUP];
 #pragma unroll
         for (int j = 0; j < J; j++) {
-            const bool ok = c0 + team + j * NTEAM < t1;
+            const bool ok = c0 + team + j * NTEAM < n_ctx;
 #pragma unroll
             for (int h = 0; h < GROUP; h++) {
                 float d = 0.0f;
@@ -189,7 +185,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
                 // load the next chunk after this one is consumed (fewer registers)
 #pragma unroll
                 for (int j = 0; j < J; j++) {
-                    const int p = min(c0 + CH + team + j * NTEAM, last);
+                    const int p = min(c0 + c_step + team + j * NTEAM, last);
                     kr[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
                     vr[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
                 }

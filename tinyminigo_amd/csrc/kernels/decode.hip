@@ -90,33 +90,50 @@ __global__ __launch_bounds__(kBlock) void attn_kernel(const AttnArgs a) {
         attn_item<HD, GROUP, false, true, true>(a, split, g, ti, 0, 0, sm);
     } else {
         const int qpos = (a.pos_dev ? *a.pos_dev : a.start) + ti;
-        const int active = active_splits(qpos + 1, a.nsplit, a.min_chunk);
+        const int active = active_splits(qpos + 1, a.nsplit);
         if (split >= active) return;
         attn_item<HD, GROUP, false>(a, split, g, ti, qpos, active, sm);
     }
 }
 
-// One thread per (query head, dim) of decode row 0.
+// Merge of the split-K partials of decode row 0, one workgroup per query
+// head: the split statistics (max m_s, sum l_s) are reduced once per
+// workgroup, then 256 threads = (256 / hd) split lanes x hd dims accumulate
+// sum_s e^(m_s - M) o_s[d] with all their partial loads in flight, and the
+// split lanes are summed through LDS.  out = that / sum_s e^(m_s - M) l_s.
 __global__ __launch_bounds__(kBlock) void attn_combine_kernel(const AttnArgs a) {
-    const int idx = blockIdx.x * kBlock + threadIdx.x;
-    if (idx >= a.nq * a.hd) return;
+    __shared__ float s_w[kBlock];
+    __shared__ float s_o[kBlock];
+    __shared__ float scratch[4];
+    const int h = blockIdx.x, t = threadIdx.x;
     const int group = a.nq / a.nkv;
-    const int h = idx / a.hd, d = idx - h * a.hd;
     const int g = h / group, hq = h - g * group;
-    const int n_ctx = *a.pos_dev + 1;
-    const int active = active_splits(n_ctx, a.nsplit, a.min_chunk);
+    const int active = active_splits(*a.pos_dev + 1, a.nsplit);
     const size_t base = (size_t)g * a.nsplit * group + hq;
-    float M = -INFINITY;
-    for (int sp = 0; sp < active; sp++) M = fmaxf(M, a.part_ml[(base + (size_t)sp * group) * 2]);
-    float L = 0.0f, O = 0.0f;
-    for (int sp = 0; sp < active; sp++) {
-        const size_t pi = base + (size_t)sp * group;
-        const float m = a.part_ml[pi * 2];
-        const float w = (m == -INFINITY) ? 0.0f : expf(m - M);
-        L = fmaf(a.part_ml[pi * 2 + 1], w, L);
-        O = fmaf(a.part[pi * a.hd + d], w, O);
+    float m = -INFINITY, l = 0.0f;
+    if (t < active) {
+        const float2 ml = *reinterpret_cast<const float2 *>(a.part_ml + (base + (size_t)t * group) * 2);
+        m = ml.x;
+        l = ml.y;
     }
-    a.out_f32[idx] = O / L;
+    float M[1] = {m};
+    block_max_n<1>(M, scratch);
+    const float w = (m == -INFINITY) ? 0.0f : expf(m - M[0]);
+    float L[1] = {w * l};
+    block_sum_n<1>(L, scratch);
+    s_w[t] = w;
+    __syncthreads();
+    const int d = t % a.hd, j0 = t / a.hd, step = kBlock / a.hd;
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int sp = j0; sp < active; sp += step) acc = fmaf(a.part[(base + (size_t)sp * group) * a.hd + d], s_w[sp], acc);
+    s_o[t] = acc;
+    __syncthreads();
+    if (t < a.hd) {
+        float o = s_o[t];
+        for (int j = 1; j < step; j++) o += s_o[j * a.hd + t];
+        a.out_f32[h * a.hd + t] = o / L[0];
+    }
 }
 
 template <int HD, bool SPEC>
@@ -202,7 +219,8 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_attn_combine(const AttnArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((a.nq * a.hd + kBlock - 1) / kBlock), dim3(kBlock), 0, s, a);
+    if (a.nsplit > kBlock || a.hd > kBlock || kBlock % a.hd != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nq), dim3(kBlock), 0, s, a);
     return hipGetLastError();
 }
 

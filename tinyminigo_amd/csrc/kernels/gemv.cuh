@@ -95,7 +95,7 @@ __device__ __forceinline__ void load_act(const float *src, const uint16_t *src_b
 template <int KC, bool COH>
 __device__ __forceinline__ void load_attn(const GemvArgs &a, int pos, float (&xv)[KC][8]) {
     const int t = threadIdx.x;
-    const int active = active_splits(pos + 1, a.nsplit, a.min_chunk);
+    const int active = active_splits(pos + 1, a.nsplit);
 #pragma unroll
     for (int c = 0; c < KC; c++) {
         const int k = c * kChunk + t * 8;
@@ -379,7 +379,7 @@ __device__ __forceinline__ void act_finish(const GemvArgs &a, int pos, ActIn<KC,
                                            float *scratch) {
     const int t = threadIdx.x;
     if constexpr (PRO == PRO_ATTN_COMBINE) {
-        const int active = active_splits(pos + 1, a.nsplit, a.min_chunk);
+        const int active = active_splits(pos + 1, a.nsplit);
 #pragma unroll
         for (int c = 0; c < KC; c++) {
             const int k = c * kChunk + t * 8;

@@ -57,7 +57,7 @@ struct GemvArgs {
     // PRO_ATTN_COMBINE: the activation is the attention output, merged from
     // the split-K partials of the decode attention kernel (see AttnArgs)
     const float *part, *part_ml;
-    int nsplit, min_chunk, group;
+    int nsplit, group;
 };
 
 hipError_t launch_gemv(int pro, int epi, const GemvArgs &a, hipStream_t s);
@@ -73,7 +73,6 @@ struct AttnArgs {
     const int *pos_dev;
     float scale;      // 1/sqrt(hd)
     int nsplit;       // grid.x
-    int min_chunk;    // minimum positions per active split
     int cap;          // rows of k_cache / v_cache (bounds the speculative first-chunk loads; 0 disables them)
     float *part;      // [T][nkv][nsplit][group][hd] partial outputs
     float *part_ml;   // [T][nkv][nsplit][group][2] (max, sum)
@@ -143,6 +142,9 @@ constexpr int kBarGroups = 8;  // arrival groups of the grid barrier
 // Decode attention with at most this many splits is merged in the o_proj
 // GEMV prologue; with more, by attn_combine_kernel.
 constexpr int kFusedSplits = 8;
+// Decode attention deals the context to its splits in blocks of this many
+// positions (split s takes blocks s, s + nsplit, ...).
+constexpr int kAttnBlock = 64;
 
 // Grid-barrier counters, each on its own 128-byte line.  Zeroed once at cache
 // creation; the counters only grow and each launch records where the next
@@ -170,7 +172,7 @@ struct PersistPlan {
 
 struct PersistArgs {
     const PersistPlan *plan;
-    int L, V, nq, nkv, nsplit, min_chunk, fused_merge, nparts;
+    int L, V, nq, nkv, nsplit, fused_merge, nparts;
     float *attn_out, *part, *part_ml;  // split merge (when not fused)
     const unsigned long long *argmax_part;
     DevState *st;

@@ -144,7 +144,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_persistent(const PersistArgs
     for (int step = 0; step < p.steps; step++) {
         const int pos = (int)__hip_atomic_load(&p.st->pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int tok = (int)__hip_atomic_load(&p.st->cur_token, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int active = active_splits(pos + 1, p.nsplit, p.min_chunk);
+        const int active = active_splits(pos + 1, p.nsplit);
         for (int l = 0; l < p.L; l++) {
             // QKV (+ embedding gather on layer 0), RoPE, KV append
             if (l == 0)
