@@ -110,7 +110,7 @@ extern "C" int tmg_generate(tmg_model *m, const uint32_t *prompt, size_t n_promp
     st.penalty = p->repetition_penalty;
     st.seed = mix64((p->seed * 0x9E3779B97F4A7C15ull) ^ fnv1a64("sample"));
     TMG_HIPG(hipMemcpy(c->st, &st, sizeof(st), hipMemcpyHostToDevice));
-    if ((rc = get_step_graph(m, c, mode))) return rc;
+    if (step_graphs_enabled() && (rc = get_step_graph(m, c, mode))) return rc;
 
     // prefill (timed like the reference, src/model.rs:622-624)
     auto t0 = std::chrono::steady_clock::now();
@@ -148,7 +148,7 @@ extern "C" int tmg_generate(tmg_model *m, const uint32_t *prompt, size_t n_promp
     size_t produced = 0;
     for (size_t i = 0; i < max_tokens; i++) {
         while (enq < max_tokens && enq < i + kWindow) {
-            TMG_HIPG(hipGraphLaunch(c->graphs[mode], m->stream));
+            if ((rc = launch_step(m, c, mode))) return rc;
             TMG_HIPG(hipMemcpyAsync(host_tok + enq + 1, c->history + enq + 1, sizeof(int), hipMemcpyDeviceToHost,
                                     m->stream));
             TMG_HIPG(hipEventRecord(ring.ev[(enq + 1) % (kWindow + 1)], m->stream));

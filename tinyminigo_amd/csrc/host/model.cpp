@@ -610,6 +610,24 @@ int get_step_graph(tmg_model *m, tmg_cache *c, int mode) {
     return TMG_OK;
 }
 
+bool step_graphs_enabled() {
+    // TMG_DECODE_GRAPH=0 launches each step's kernels one by one instead of
+    // replaying the captured graph (for tools that cannot trace graph launches)
+    static const bool on = [] {
+        const char *e = getenv("TMG_DECODE_GRAPH");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+int launch_step(tmg_model *m, tmg_cache *c, int mode) {
+    if (!step_graphs_enabled()) return enqueue_decode_step(m, c, nullptr, mode);
+    int rc = get_step_graph(m, c, mode);
+    if (rc) return rc;
+    TMG_HIP(hipGraphLaunch(c->graphs[mode], m->stream));
+    return TMG_OK;
+}
+
 int set_state(tmg_model *m, tmg_cache *c, int token, bool reset_step) {
     // one small H2D write of the host-known fields; the step counter and the
     // argmax key are reset together with the position when asked
@@ -932,10 +950,7 @@ extern "C" int tmg_forward_token(tmg_model *m, tmg_cache *c, uint32_t token, flo
     if ((rc = set_state(m, c, (int)token, false))) return rc;
     bool used = false;
     if ((rc = enqueue_persistent(m, c, 1, &used))) return rc;
-    if (!used) {
-        if ((rc = get_step_graph(m, c, SEL_ARGMAX))) return rc;
-        TMG_HIP(hipGraphLaunch(c->graphs[SEL_ARGMAX], m->stream));
-    }
+    if (!used && (rc = launch_step(m, c, SEL_ARGMAX))) return rc;
     c->len += 1;
     if ((rc = fetch_logits(m, logits))) return rc;
     return used ? check_persistent(m, c) : TMG_OK;
@@ -981,10 +996,7 @@ extern "C" int tmg_decode_greedy(tmg_model *m, tmg_cache *c, uint32_t token, uin
     if ((uint64_t)c->len + n_steps > c->max_pos) return set_error(TMG_E_CAPACITY, "KV cache full");
     (void)hipSetDevice(m->device);
     int rc;
-    // TMG_DECODE_GRAPH=0 launches the same kernels one by one instead of
-    // replaying the captured graph (for tools that cannot trace graph launches)
-    const char *eg = getenv("TMG_DECODE_GRAPH");
-    const bool eager = eg && eg[0] == '0';
+    const bool eager = !step_graphs_enabled();
     if ((rc = set_state(m, c, (int)token, true))) return rc;
     hipEvent_t e0, e1;
     TMG_HIP(hipEventCreate(&e0));
@@ -993,14 +1005,8 @@ extern "C" int tmg_decode_greedy(tmg_model *m, tmg_cache *c, uint32_t token, uin
     bool used = false;
     if (!eager && (rc = enqueue_persistent(m, c, (int)n_steps, &used))) return rc;
     if (!used) {
-        if (!eager && (rc = get_step_graph(m, c, SEL_ARGMAX))) return rc;
-        for (uint32_t i = 0; i < n_steps; i++) {
-            if (eager) {
-                if ((rc = enqueue_decode_step(m, c, nullptr, SEL_ARGMAX))) return rc;
-            } else {
-                TMG_HIP(hipGraphLaunch(c->graphs[SEL_ARGMAX], m->stream));
-            }
-        }
+        for (uint32_t i = 0; i < n_steps; i++)
+            if ((rc = launch_step(m, c, SEL_ARGMAX))) return rc;
     }
     TMG_HIP(hipEventRecord(e1, m->stream));
     TMG_HIP(hipEventSynchronize(e1));
@@ -1043,8 +1049,7 @@ extern "C" int tmg_profile_decode_step(tmg_model *m, tmg_cache *c, uint32_t toke
     TMG_HIP(hipEventCreate(&e1));
     // TMG_DECODE_GRAPH=0: the same launches enqueued one by one (profilers
     // that do not follow graph launches)
-    const char *eg = getenv("TMG_DECODE_GRAPH");
-    const bool use_graph = !(eg && strcmp(eg, "0") == 0);
+    const bool use_graph = step_graphs_enabled();
     for (auto &kind : kinds) {
         if ((rc = set_state(m, c, (int)token, true))) break;
         int count = 0;  // launches of this kind in one step

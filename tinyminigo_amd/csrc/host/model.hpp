@@ -105,6 +105,10 @@ enum SelectMode {
 int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mode);
 int enqueue_select(tmg_model *m, tmg_cache *c, int mode, int advance_pos);
 int get_step_graph(tmg_model *m, tmg_cache *c, int mode);
+// One decode step on the model's stream: the cache's captured graph for
+// `mode`, or (TMG_DECODE_GRAPH=0) the same kernels launched one by one.
+bool step_graphs_enabled();
+int launch_step(tmg_model *m, tmg_cache *c, int mode);
 int set_state(tmg_model *m, tmg_cache *c, int token, bool reset_step);
 int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n);
 int ensure_rope(tmg_model *m, int npos);
