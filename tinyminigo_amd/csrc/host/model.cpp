@@ -667,6 +667,19 @@ static int ensure_prefill(tmg_model *m, int T) {
     return TMG_OK;
 }
 
+// Split-bf16 KV scratch for cache rows [0, n) (n rounded up to 64).
+static int ensure_kv_split(tmg_model *m, int n) {
+    const int cap = (n + 63) / 64 * 64;
+    if (cap <= m->kv_cap) return TMG_OK;
+    int rc;
+    const size_t sz = (size_t)cap * m->kvd;
+    if ((rc = dev_alloc(m, &m->pf_kh, sz)) || (rc = dev_alloc(m, &m->pf_kl, sz)) || (rc = dev_alloc(m, &m->pf_vth, sz)) ||
+        (rc = dev_alloc(m, &m->pf_vtl, sz)))
+        return rc;
+    m->kv_cap = cap;
+    return TMG_OK;
+}
+
 // Runs the batched prefill; leaves the last token's logits in m->logits and
 // the per-workgroup argmax keys in m->argmax_part.
 int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
@@ -717,10 +730,19 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         aa.nsplit = 1;
         aa.out_hi = m->pf_ahi;
         aa.out_lo = m->pf_alo;
-        if (attn_prefill_supported(aa))
+        if (attn_prefill_supported(aa)) {
+            if ((rc = ensure_kv_split(m, start + T))) return rc;
+            KVSplitArgs ka{kc, vc, start + T, m->nkv, m->hd, m->pf_kh, m->pf_kl, m->pf_vth, m->pf_vtl, m->kv_cap};
+            TMG_HIP(launch_kv_split(ka, s));
+            aa.kh = m->pf_kh;
+            aa.kl = m->pf_kl;
+            aa.vth = m->pf_vth;
+            aa.vtl = m->pf_vtl;
+            aa.vt_pitch = m->kv_cap;
             TMG_HIP(launch_attn_prefill(aa, s));
-        else
+        } else {
             TMG_HIP(launch_attn(aa, s));
+        }
 
         GemmArgs o{};
         o.W = ly.o;

@@ -18,6 +18,11 @@
 // operands agree, so a lane's k-slots are the keys it already holds (4 from
 // each of two adjacent 16-key tiles), and V^T is read from an LDS copy
 // stored [dim][key] in the same order.
+//
+// The K and V rows are split into bf16 pairs once per layer by
+// kv_split_kernel (V transposed per head), so the attention workgroups stage
+// ready-made MFMA operands: each block's 64 KB are plain 16-byte copies, and
+// the next block's copies are in flight while the current one is multiplied.
 #include "common.cuh"
 #include "kernels.hpp"
 
@@ -67,6 +72,52 @@ __device__ __forceinline__ float max_xor16_32(float v) {
     return v;
 }
 
+// One workgroup per (64 positions, KV head): f32 K/V rows -> split-bf16 K
+// [pos][kvd] and V^T [head][dim][pos] (through an LDS transpose); rows at or
+// past n are zeros.
+__global__ __launch_bounds__(kBlock) void kv_split_kernel(const KVSplitArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t sT[2][kPHD][kSVP];
+    const int t = threadIdx.x;
+    const int p0 = blockIdx.x * kPKB, g = blockIdx.y;
+    const int kvd = a.nkv * kPHD;
+    // K: 64 rows x 128 dims of head g, 4 floats per thread per step
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int row = (t >> 5) + 8 * i, d = 4 * (t & 31);
+        const int pos = p0 + row;
+        float4 k = make_float4(0.f, 0.f, 0.f, 0.f), v = k;
+        if (pos < a.n) {
+            k = *reinterpret_cast<const float4 *>(a.k_cache + (size_t)pos * kvd + g * kPHD + d);
+            v = *reinterpret_cast<const float4 *>(a.v_cache + (size_t)pos * kvd + g * kPHD + d);
+        }
+        const float kk[4] = {k.x, k.y, k.z, k.w}, vv[4] = {v.x, v.y, v.z, v.w};
+        uint16_t kh[4], kl[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            split2(kk[j], kh[j], kl[j]);
+            uint16_t vh, vl;
+            split2(vv[j], vh, vl);
+            sT[0][d + j][row] = vh;
+            sT[1][d + j][row] = vl;
+        }
+        const size_t o = (size_t)pos * kvd + g * kPHD + d;
+        *reinterpret_cast<u32x2 *>(a.kh + o) =
+            u32x2{(uint32_t)kh[0] | ((uint32_t)kh[1] << 16), (uint32_t)kh[2] | ((uint32_t)kh[3] << 16)};
+        *reinterpret_cast<u32x2 *>(a.kl + o) =
+            u32x2{(uint32_t)kl[0] | ((uint32_t)kl[1] << 16), (uint32_t)kl[2] | ((uint32_t)kl[3] << 16)};
+    }
+    __syncthreads();
+    // V^T: 128 dim rows x 64 positions, 16 bytes per thread per step
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = t + kBlock * i;
+        const int d = c >> 3, col = (c & 7) * 8;
+        const size_t o = ((size_t)g * kPHD + d) * a.vt_pitch + p0 + col;
+        *reinterpret_cast<u32x4 *>(a.vth + o) = *reinterpret_cast<const u32x4 *>(&sT[0][d][col]);
+        *reinterpret_cast<u32x4 *>(a.vtl + o) = *reinterpret_cast<const u32x4 *>(&sT[1][d][col]);
+    }
+}
+
 template <int GROUP>
 __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) {
     constexpr int QB = kPCols / GROUP;  // query positions per workgroup
@@ -78,7 +129,6 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
     const int qb = nqb - 1 - (int)blockIdx.x;  // longest causal ranges first
     const int g = blockIdx.y;
     const int kvd = a.nkv * kPHD, qd = a.nq * kPHD;
-    const int n_total = a.start + a.T;  // cache rows holding keys
 
     // this lane's query column in each of its two 16-column tiles
     int ti[2], qpos[2], qhead[2];
@@ -90,6 +140,30 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
         qpos[qt] = a.start + ti[qt];
         qhead[qt] = g * GROUP + hh;
     }
+    const int last_pos = a.start + min(a.T, (qb + 1) * QB) - 1;  // the workgroup's last query position
+    const int nkb = last_pos / kPKB + 1;
+
+    // staging map: copy c = t + 256 i (i < 4) of a block is K row c >> 4,
+    // 16-byte column c & 15, and V^T row c >> 3, 16-byte column c & 7
+    const uint16_t *gk[2], *gv[2];
+    gk[0] = a.kh + g * kPHD;
+    gk[1] = a.kl + g * kPHD;
+    gv[0] = a.vth + (size_t)g * kPHD * a.vt_pitch;
+    gv[1] = a.vtl + (size_t)g * kPHD * a.vt_pitch;
+    u32x4 rk[2][4], rv[2][4];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = t + kBlock * i;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                rk[h][i] = *reinterpret_cast<const u32x4 *>(gk[h] + (size_t)(k0 + (c >> 4)) * kvd + (c & 15) * 8);
+                rv[h][i] = *reinterpret_cast<const u32x4 *>(gv[h] + (size_t)(c >> 3) * a.vt_pitch + k0 + (c & 7) * 8);
+            }
+        }
+    };
+    fetch(0);
+
     // Q^T fragments (MFMA B operand): dims 32 ds + 8 q4 .. +7 of the column
     bf16x8 qh[2][4], ql[2][4];
 #pragma unroll
@@ -111,48 +185,20 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) o[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int last_pos = a.start + min(a.T, (qb + 1) * QB) - 1;  // the workgroup's last query position
-    const int nkb = last_pos / kPKB + 1;
-    const float *kbase = a.k_cache + g * kPHD;
-    const float *vbase = a.v_cache + g * kPHD;
     for (int kb = 0; kb < nkb; kb++) {
         const int k0 = kb * kPKB;
         __syncthreads();  // the previous block's fragments are read
-        // stage K [key][dim] (rows past the filled cache are zeros)
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int key = (t >> 5) + 8 * i, d = 4 * (t & 31);
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (k0 + key < n_total) v = *reinterpret_cast<const float4 *>(kbase + (size_t)(k0 + key) * kvd + d);
-            uint16_t h[4], lo[4];
-            split2(v.x, h[0], lo[0]);
-            split2(v.y, h[1], lo[1]);
-            split2(v.z, h[2], lo[2]);
-            split2(v.w, h[3], lo[3]);
-            *reinterpret_cast<u32x2 *>(&sK[0][key][d]) =
-                u32x2{(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
-            *reinterpret_cast<u32x2 *>(&sK[1][key][d]) =
-                u32x2{(uint32_t)lo[0] | ((uint32_t)lo[1] << 16), (uint32_t)lo[2] | ((uint32_t)lo[3] << 16)};
-        }
-        // stage V transposed [dim][key], two keys per 32-bit store
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int key0 = 2 * ((t >> 5) + 8 * i), d = 4 * (t & 31);
-            float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
-            if (k0 + key0 < n_total) v0 = *reinterpret_cast<const float4 *>(vbase + (size_t)(k0 + key0) * kvd + d);
-            if (k0 + key0 + 1 < n_total)
-                v1 = *reinterpret_cast<const float4 *>(vbase + (size_t)(k0 + key0 + 1) * kvd + d);
-            const float a0[4] = {v0.x, v0.y, v0.z, v0.w}, a1[4] = {v1.x, v1.y, v1.z, v1.w};
+            const int c = t + kBlock * i;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                uint16_t h0, l0, h1, l1;
-                split2(a0[j], h0, l0);
-                split2(a1[j], h1, l1);
-                *reinterpret_cast<uint32_t *>(&sV[0][d + j][key0]) = (uint32_t)h0 | ((uint32_t)h1 << 16);
-                *reinterpret_cast<uint32_t *>(&sV[1][d + j][key0]) = (uint32_t)l0 | ((uint32_t)l1 << 16);
+            for (int h = 0; h < 2; h++) {
+                *reinterpret_cast<u32x4 *>(&sK[h][c >> 4][(c & 15) * 8]) = rk[h][i];
+                *reinterpret_cast<u32x4 *>(&sV[h][c >> 3][(c & 7) * 8]) = rv[h][i];
             }
         }
         __syncthreads();
+        if (kb + 1 < nkb) fetch(k0 + kPKB);  // in flight during this block's MFMAs
 
         // S^T = K Q^T: 4 key tiles x 2 query tiles
         f32x4 s[4][2];
@@ -189,7 +235,7 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
                 }
             mx = max_xor16_32(mx);
             const float m_new = fmaxf(m[qt], mx);  // finite: key 0 precedes every query
-            const float corr = exp2f(m[qt] - m_new);
+            const float corr = __builtin_amdgcn_exp2f(m[qt] - m_new);
             m[qt] = m_new;
             l[qt] *= corr;
 #pragma unroll
@@ -198,7 +244,7 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
             for (int kt = 0; kt < 4; kt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const float p = exp2f(s[kt][qt][i] - m_new);
+                    const float p = __builtin_amdgcn_exp2f(s[kt][qt][i] - m_new);
                     s[kt][qt][i] = p;
                     l[qt] += p;
                 }
@@ -252,6 +298,13 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
 
 }  // namespace
 
+hipError_t launch_kv_split(const KVSplitArgs &a, hipStream_t s) {
+    if (a.hd != kPHD || a.n <= 0 || a.vt_pitch < (a.n + kPKB - 1) / kPKB * kPKB || a.vt_pitch % 8)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(kv_split_kernel, dim3((a.n + kPKB - 1) / kPKB, a.nkv), dim3(kBlock), 0, s, a);
+    return hipGetLastError();
+}
+
 bool attn_prefill_supported(const AttnArgs &a) {
     const int group = a.nkv > 0 ? a.nq / a.nkv : 0;
     // short prompts keep the per-row kernel: a few query blocks cannot fill the chip
@@ -260,7 +313,9 @@ bool attn_prefill_supported(const AttnArgs &a) {
 }
 
 hipError_t launch_attn_prefill(const AttnArgs &a, hipStream_t s) {
-    if (!attn_prefill_supported(a) || a.T <= 0) return hipErrorInvalidValue;
+    if (!attn_prefill_supported(a) || a.T <= 0 || !a.kh || !a.kl || !a.vth || !a.vtl ||
+        a.vt_pitch < (a.start + a.T + kPKB - 1) / kPKB * kPKB || a.vt_pitch % 8)
+        return hipErrorInvalidValue;
     const int group = a.nq / a.nkv;
     const int QB = kPCols / group;
     const dim3 grid((a.T + QB - 1) / QB, a.nkv);

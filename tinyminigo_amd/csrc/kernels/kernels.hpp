@@ -78,7 +78,22 @@ struct AttnArgs {
     float *part_ml;   // [T][nkv][nsplit][group][2] (max, sum)
     float *out_f32;   // [T][nq*hd] when one split covers the row, or null
     uint16_t *out_hi, *out_lo;  // [T][nq*hd] split-bf16 output (prefill), or null
+    // MFMA prefill attention: the cache rows [0, start+T) as split-bf16, keys
+    // [pos][nkv*hd] and values transposed [nkv][hd][vt_pitch]
+    const uint16_t *kh, *kl, *vth, *vtl;
+    int vt_pitch;
 };
+
+// Split-bf16 copies of one layer's KV cache rows [0, n) for the MFMA prefill
+// attention (rows up to the next multiple of 64 are zeros).
+struct KVSplitArgs {
+    const float *k_cache, *v_cache;  // [pos][nkv*hd]
+    int n, nkv, hd;
+    uint16_t *kh, *kl;               // [round64(n)][nkv*hd]
+    uint16_t *vth, *vtl;             // [nkv][hd][vt_pitch], vt_pitch >= round64(n)
+    int vt_pitch;
+};
+hipError_t launch_kv_split(const KVSplitArgs &a, hipStream_t s);
 
 hipError_t launch_attn(const AttnArgs &a, hipStream_t s);
 // Causal prefill attention on MFMA (head_dim 128, split-bf16 output): the
