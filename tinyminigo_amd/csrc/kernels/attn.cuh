@@ -97,6 +97,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
         if (split >= active) return;
     }
     const int n_ctx = qpos + 1;
+    const float sl2 = a.scale * 1.4426950408889634f;  // scores in log2 units: softmax by exp2
 
     float m_run[GROUP], l_run[GROUP];
     float4 o_acc[GROUP];
@@ -145,7 +146,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
                     d = fmaf(qv[h].w, kr[j].w, d);
                 }
                 d = group_sum<TS>(d);
-                s[j][h] = ok ? d * a.scale : -INFINITY;
+                s[j][h] = ok ? d * sl2 : -INFINITY;
             }
         }
         // online softmax update of the team's state
@@ -156,13 +157,13 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
             for (int j = 0; j < J; j++) mc = fmaxf(mc, s[j][h]);
             if (mc == -INFINITY) continue;  // no position of this team in the chunk
             const float m_new = fmaxf(m_run[h], mc);
-            const float corr = (m_run[h] == -INFINITY) ? 0.0f : expf(m_run[h] - m_new);
+            const float corr = (m_run[h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run[h] - m_new);
             float l = l_run[h] * corr;
             float4 o = make_float4(o_acc[h].x * corr, o_acc[h].y * corr, o_acc[h].z * corr, o_acc[h].w * corr);
 #pragma unroll
             for (int j = 0; j < J; j++) {
                 const bool ok = s[j][h] != -INFINITY;
-                const float p = ok ? expf(s[j][h] - m_new) : 0.0f;
+                const float p = ok ? __builtin_amdgcn_exp2f(s[j][h] - m_new) : 0.0f;
                 const float4 v = ok ? vr[j] : make_float4(0.f, 0.f, 0.f, 0.f);
                 l += p;
                 o.x = fmaf(p, v.x, o.x);
@@ -215,7 +216,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
 #pragma unroll 8
         for (int tm = 0; tm < NTEAM; tm++) {
             const float mt = sm.m[tm][h];
-            const float w = (mt == -INFINITY) ? 0.0f : expf(mt - M);
+            const float w = (mt == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mt - M);
             L = fmaf(sm.l[tm][h], w, L);
             O = fmaf(sm.o[tm][h][d], w, O);
         }

@@ -80,20 +80,22 @@ hipError_t launch_pe(const GemvArgs &a, hipStream_t s) {
 // them across the XCDs' L2s without any in-kernel fence.
 // ---------------------------------------------------------------------------
 
-// SPEC (decode): the split's first chunk is loaded before the position is
-// read (see attn_item).
+// SPEC (decode): splits below kSpecSplits load their first chunk before the
+// position is read (see attn_item).
 template <int HD, int GROUP, bool SPEC>
 __global__ __launch_bounds__(kBlock) void attn_kernel(const AttnArgs a) {
     __shared__ AttnShared<HD, GROUP> sm;
     const int split = blockIdx.x, g = blockIdx.y, ti = blockIdx.z;
     if constexpr (SPEC) {
-        attn_item<HD, GROUP, false, true, true>(a, split, g, ti, 0, 0, sm);
-    } else {
-        const int qpos = (a.pos_dev ? *a.pos_dev : a.start) + ti;
-        const int active = active_splits(qpos + 1, a.nsplit);
-        if (split >= active) return;
-        attn_item<HD, GROUP, false>(a, split, g, ti, qpos, active, sm);
+        if (split < kSpecSplits) {
+            attn_item<HD, GROUP, false, true, true>(a, split, g, ti, 0, 0, sm);
+            return;
+        }
     }
+    const int qpos = (a.pos_dev ? *a.pos_dev : a.start) + ti;
+    const int active = active_splits(qpos + 1, a.nsplit);
+    if (split >= active) return;
+    attn_item<HD, GROUP, false>(a, split, g, ti, qpos, active, sm);
 }
 
 // Merge of the split-K partials of decode row 0, one workgroup per query
@@ -118,7 +120,7 @@ __global__ __launch_bounds__(kBlock) void attn_combine_kernel(const AttnArgs a) 
     }
     float M[1] = {m};
     block_max_n<1>(M, scratch);
-    const float w = (m == -INFINITY) ? 0.0f : expf(m - M[0]);
+    const float w = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - M[0]);
     float L[1] = {w * l};
     block_sum_n<1>(L, scratch);
     s_w[t] = w;

@@ -111,7 +111,7 @@ __device__ __forceinline__ void load_attn(const GemvArgs &a, int pos, float (&xv
         for (int sp = 0; sp < active; sp++) {
             const size_t pi = base + (size_t)sp * a.group;
             const float m = ldf<COH>(a.part_ml + pi * 2);
-            const float w = (m == -INFINITY) ? 0.0f : expf(m - M);
+            const float w = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - M);
             L = fmaf(ldf<COH>(a.part_ml + pi * 2 + 1), w, L);
             const float4 o0 = ldf4<COH>(a.part + pi * a.hd + d);
             const float4 o1 = ldf4<COH>(a.part + pi * a.hd + d + 4);
@@ -395,7 +395,7 @@ __device__ __forceinline__ void act_finish(const GemvArgs &a, int pos, ActIn<KC,
             for (int sp = 0; sp < kFusedSplits; sp++) {
                 if (sp >= active) continue;
                 const float m = in.ml[c][sp].x;
-                const float w = (m == -INFINITY) ? 0.0f : expf(m - M);
+                const float w = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - M);
                 L = fmaf(in.ml[c][sp].y, w, L);
                 const float4 o0 = in.o[c][sp][0], o1 = in.o[c][sp][1];
                 xv[c][0] = fmaf(o0.x, w, xv[c][0]);

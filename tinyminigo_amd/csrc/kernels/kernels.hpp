@@ -75,7 +75,7 @@ struct AttnArgs {
     int nsplit;       // grid.x
     int cap;          // rows of k_cache / v_cache (bounds the speculative first-chunk loads; 0 disables them)
     float *part;      // [T][nkv][nsplit][group][hd] partial outputs
-    float *part_ml;   // [T][nkv][nsplit][group][2] (max, sum)
+    float *part_ml;   // [T][nkv][nsplit][group][2] (max of the log2-scaled scores, sum)
     float *out_f32;   // [T][nq*hd] when one split covers the row, or null
     uint16_t *out_hi, *out_lo;  // [T][nq*hd] split-bf16 output (prefill), or null
     // MFMA prefill attention: the cache rows [0, start+T) as split-bf16, keys
@@ -160,6 +160,11 @@ constexpr int kFusedSplits = 8;
 // Decode attention deals the context to its splits in blocks of this many
 // positions (split s takes blocks s, s + nsplit, ...).
 constexpr int kAttnBlock = 64;
+// Splits below this index load their first block before reading the
+// position (speculatively: most of them are active at any context); the
+// others read it first, so a long cache at a short context does not stream
+// the blocks of its inactive splits.
+constexpr int kSpecSplits = 8;
 
 // Grid-barrier counters, each on its own 128-byte line.  Zeroed once at cache
 // creation; the counters only grow and each launch records where the next

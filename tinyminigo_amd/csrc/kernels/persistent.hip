@@ -171,7 +171,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_persistent(const PersistArgs
                     for (int sp = 0; sp < active; sp++) {
                         const size_t pi = base + (size_t)sp * GROUP;
                         const float m = ldf<true>(p.part_ml + pi * 2);
-                        const float w = (m == -INFINITY) ? 0.0f : expf(m - M);
+                        const float w = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - M);
                         L = fmaf(ldf<true>(p.part_ml + pi * 2 + 1), w, L);
                         O = fmaf(ldf<true>(p.part + pi * HD + d), w, O);
                     }
