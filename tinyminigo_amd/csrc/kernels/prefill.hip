@@ -236,6 +236,96 @@ __global__ __launch_bounds__(kBlock) void gemm_tiled_kernel(const GemmArgs a) {
             gemm_store<EPI>(a, m0 + wm * 64 + i * 16 + (lane >> 4) * 4, n0 + wn * 64 + j * 16 + r, acc[i][j]);
 }
 
+// Tiled MFMA GEMM, LDS-DMA version: the same 128 x 128 workgroup tile and
+// 64 x 64 wavefront quarters, but the W / Bhi / Blo tiles go global -> LDS
+// directly (global_load_lds_dwordx4, no register staging) through a 3-stage
+// ring, so step s + 2 is in flight while step s is multiplied and each step
+// needs one barrier.  LDS rows are unpadded 128 B with the 16-byte chunks
+// XOR-swizzled by (row & 7) against bank conflicts: a DMA wave-instruction
+// fills 1 KB = 8 rows contiguously, so each lane fetches the global chunk that
+// belongs at its LDS slot.
+constexpr int kGStages = 3;
+constexpr int kGTile = kTM * kTK * 2;  // bytes of one 128 x 64 bf16 tile
+
+template <int EPI>
+__global__ __launch_bounds__(kBlock) void gemm_dma_kernel(const GemmArgs a) {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[kGStages * 3 * kGTile];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int m0 = blockIdx.x * kTM, n0 = blockIdx.y * kTN;
+    const int K = a.K;
+    const int nsteps = K / kTK;
+    // DMA: wave w's instruction i fills rows (4 w + i) * 8 .. +7 of a tile;
+    // lane l writes row (4 w + i) * 8 + (l >> 3), physical chunk l & 7, which
+    // holds logical chunk (l & 7) ^ (row & 7)
+    uint32_t off[3][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = (wave * 4 + i) * 8 + (lane >> 3);
+        const int lc = (lane & 7) ^ (row & 7);
+        off[0][i] = (uint32_t)min(m0 + row, a.M - 1) * (uint32_t)K + lc * 8;
+        off[1][i] = (uint32_t)min(n0 + row, a.N - 1) * (uint32_t)K + lc * 8;
+        off[2][i] = off[1][i];
+    }
+    auto issue = [&](int stage, int k0) {
+#pragma unroll
+        for (int x = 0; x < 3; x++) {
+            const uint16_t *base = x == 0 ? a.W : (x == 1 ? a.Bhi : a.Blo);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                __builtin_amdgcn_global_load_lds(base + off[x][i] + k0,
+                                                 smem + (stage * 3 + x) * kGTile + (wave * 4 + i) * 1024, 16, 0, 0);
+        }
+    };
+    issue(0, 0);
+    if (nsteps > 1) issue(1, kTK);
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int r = lane & 15, q4 = lane >> 4;
+    for (int st = 0; st < nsteps; st++) {
+        // this step's 12 DMAs are complete once at most the next step's 12
+        // are outstanding (vector memory counts complete in issue order)
+        if (st + 1 < nsteps)
+            __builtin_amdgcn_s_waitcnt(0xF7C);  // vmcnt(12)
+        else
+            __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+        __builtin_amdgcn_s_barrier();  // every wave's DMAs for this step landed; step - 1's reads are done
+        if (st + 2 < nsteps) issue((st + 2) % kGStages, (st + 2) * kTK);
+        const unsigned char *sa = smem + ((st % kGStages) * 3 + 0) * kGTile;
+        const unsigned char *sh = sa + kGTile, *sl = sa + 2 * kGTile;
+#pragma unroll
+        for (int kk = 0; kk < kTK; kk += 32) {
+            const int lc = kk / 8 + q4;
+            bf16x8 fa[4], fh[4], fl[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int ra = wm * 64 + i * 16 + r, rb = wn * 64 + i * 16 + r;
+                fa[i] = *reinterpret_cast<const bf16x8 *>(sa + ra * 128 + ((lc ^ (ra & 7)) * 16));
+                fh[i] = *reinterpret_cast<const bf16x8 *>(sh + rb * 128 + ((lc ^ (rb & 7)) * 16));
+                fl[i] = *reinterpret_cast<const bf16x8 *>(sl + rb * 128 + ((lc ^ (rb & 7)) * 16));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fh[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fl[j], acc[i][j], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            gemm_store<EPI>(a, m0 + wm * 64 + i * 16 + q4 * 4, n0 + wn * 64 + j * 16 + r, acc[i][j]);
+}
+
 __global__ void copy_row_kernel(const float *x, int row, int H, float *dst) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < H; i += gridDim.x * blockDim.x)
         dst[i] = x[(size_t)row * H + i];
@@ -260,10 +350,10 @@ hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
     if (a.N >= kTiledMinTokens && a.K % kTK == 0) {
         const dim3 grid((a.M + kTM - 1) / kTM, (a.N + kTN - 1) / kTN);
         switch (epi) {
-            case GEPI_STORE: hipLaunchKernelGGL(gemm_tiled_kernel<GEPI_STORE>, grid, dim3(kBlock), 0, s, a); break;
-            case GEPI_RESID: hipLaunchKernelGGL(gemm_tiled_kernel<GEPI_RESID>, grid, dim3(kBlock), 0, s, a); break;
-            case GEPI_SWIGLU: hipLaunchKernelGGL(gemm_tiled_kernel<GEPI_SWIGLU>, grid, dim3(kBlock), 0, s, a); break;
-            case GEPI_QKV: hipLaunchKernelGGL(gemm_tiled_kernel<GEPI_QKV>, grid, dim3(kBlock), 0, s, a); break;
+            case GEPI_STORE: hipLaunchKernelGGL(gemm_dma_kernel<GEPI_STORE>, grid, dim3(kBlock), 0, s, a); break;
+            case GEPI_RESID: hipLaunchKernelGGL(gemm_dma_kernel<GEPI_RESID>, grid, dim3(kBlock), 0, s, a); break;
+            case GEPI_SWIGLU: hipLaunchKernelGGL(gemm_dma_kernel<GEPI_SWIGLU>, grid, dim3(kBlock), 0, s, a); break;
+            case GEPI_QKV: hipLaunchKernelGGL(gemm_dma_kernel<GEPI_QKV>, grid, dim3(kBlock), 0, s, a); break;
             default: return hipErrorInvalidValue;
         }
         return hipGetLastError();
