@@ -296,6 +296,14 @@ bool LaunchRecorder::want(const char *name, double b) {
     return !none && (!only || strcmp(only, name) == 0);
 }
 
+// The split-K merge runs in the o_proj GEMV prologue when the splits are few
+// and the attention output fits one 2048-element chunk: every o_proj
+// workgroup re-reads all partials, which for a wider output costs more L2
+// traffic than a separate merge kernel.
+static bool fused_merge(const tmg_model *m, const tmg_cache *c) {
+    return c->attn_nsplit > 1 && c->attn_nsplit <= kFusedSplits && m->qd <= 2048;
+}
+
 int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mode) {
     hipStream_t s = m->stream;
     const int H = m->H, I = m->I, qd = m->qd, kvd = m->kvd;
@@ -347,8 +355,8 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
         aa.part_ml = m->attn_ml;
         aa.out_f32 = c->attn_nsplit == 1 ? m->attn_out : nullptr;
         if (!rec || rec->want("attn_decode", 2.0 * n_ctx_est * kvd * 4 + 2.0 * qd * 4)) TMG_HIP(launch_attn(aa, s));
-        const bool fused = c->attn_nsplit > 1 && c->attn_nsplit <= kFusedSplits;
-        if (c->attn_nsplit > kFusedSplits) {
+        const bool fused = fused_merge(m, c);
+        if (c->attn_nsplit > 1 && !fused) {
             aa.out_f32 = m->attn_out;
             if (!rec || rec->want("attn_combine", 0.0)) TMG_HIP(launch_attn_combine(aa, s));
         }
@@ -523,7 +531,7 @@ int enqueue_persistent(tmg_model *m, tmg_cache *c, int steps, bool *used) {
     a.nq = m->nq;
     a.nkv = m->nkv;
     a.nsplit = c->attn_nsplit;
-    a.fused_merge = c->attn_nsplit <= kFusedSplits;
+    a.fused_merge = c->attn_nsplit == 1 || fused_merge(m, c);
     a.nparts = m->argmax_nparts;
     a.attn_out = m->attn_out;
     a.part = m->attn_part;
