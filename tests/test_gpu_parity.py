@@ -392,6 +392,25 @@ def test_long_prefill_chunks_vs_oracle(T, O, W, one_b):
         O.set_attn_threads(1)
 
 
+def test_short_prompt_splitk_gemm_vs_oracle(T, O, W, one_b):
+    # prompts under 256 tokens run the split-K MFMA GEMM: 150 tokens = two
+    # full 64-token tiles + 22 (o_proj / down split 2 ways), then 100 more at
+    # position 150 (split 4 ways); the split reduction is order-independent,
+    # so a second run is bitwise identical
+    g, o = one_b
+    ids = [int(t) for t in W.LONG_CTX.prompt()[:250]]
+    gc, oc = T.KvCache(g, 300), o.new_cache()
+    a = g.forward_seq(ids[:150], gc)
+    close_logits(a, o.forward_seq(ids[:150], oc), "prefill 150")
+    close_logits(g.forward_seq(ids[150:], gc), o.forward_seq(ids[150:], oc), "prefill 100 at 150")
+    for layer in (0, 23):
+        for x, y in ((gc.keys_flat(layer), oc.keys_flat(layer)), (gc.values_flat(layer), oc.values_flat(layer))):
+            d = np.abs(x - y)
+            assert np.all(d <= ABS_TOL + REL_TOL * np.abs(y)), f"layer {layer} kv: {d.max():.3e}"
+    gc2 = T.KvCache(g, 300)
+    assert np.array_equal(a, g.forward_seq(ids[:150], gc2))
+
+
 def test_long_context_8k_prefill_matches_decode_path(T, W, one_b):
     """The 8192-token prompt at full size, where the oracle would need about
     ten minutes: the batched prefill (tiled GEMM, MFMA attention) against the

@@ -671,6 +671,12 @@ static int ensure_prefill(tmg_model *m, int T) {
         (rc = dev_alloc(m, &m->pf_alo, (size_t)cap * m->qd)) || (rc = dev_alloc(m, &m->pf_hhi, (size_t)cap * m->I)) ||
         (rc = dev_alloc(m, &m->pf_hlo, (size_t)cap * m->I)))
         return rc;
+    if (!m->pf_part) {
+        const size_t nc = skinny_counters(std::max(std::max(m->qkv_rows, m->H), 2 * m->I));
+        if ((rc = dev_alloc(m, &m->pf_part, kSkinnyPartFloats)) || (rc = dev_alloc(m, &m->pf_cnt, nc))) return rc;
+        hipError_t e = hipMemset(m->pf_cnt, 0, nc * sizeof(unsigned));
+        if (e != hipSuccess) return set_error(TMG_E_DEVICE, std::string("hipMemset: ") + hipGetErrorString(e));
+    }
     m->pf_cap = cap;
     return TMG_OK;
 }
@@ -723,6 +729,8 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         g.q_out = m->pf_q;
         g.k_cache = kc;
         g.v_cache = vc;
+        g.part = m->pf_part;
+        g.cnt = m->pf_cnt;
         TMG_HIP(launch_gemm(GEPI_QKV, g, s));
 
         AttnArgs aa{};
@@ -760,6 +768,8 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         o.N = T;
         o.K = qd;
         o.y = m->pf_x;
+        o.part = m->pf_part;
+        o.cnt = m->pf_cnt;
         TMG_HIP(launch_gemm(GEPI_RESID, o, s));
 
         TMG_HIP(launch_rmsnorm_split(m->pf_x, ly.post_norm, m->cfg.rms_norm_eps, T, H, m->pf_hi, m->pf_lo, s));
@@ -772,6 +782,8 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         gu.K = H;
         gu.h_hi = m->pf_hhi;
         gu.h_lo = m->pf_hlo;
+        gu.part = m->pf_part;
+        gu.cnt = m->pf_cnt;
         TMG_HIP(launch_gemm(GEPI_SWIGLU, gu, s));
 
         GemmArgs d{};
@@ -782,6 +794,8 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         d.N = T;
         d.K = I;
         d.y = m->pf_x;
+        d.part = m->pf_part;
+        d.cnt = m->pf_cnt;
         TMG_HIP(launch_gemm(GEPI_RESID, d, s));
     }
     // final norm of the last row (batch association) + lm_head + argmax

@@ -45,6 +45,9 @@ struct tmg_model {
     float *pf_x = nullptr, *pf_q = nullptr;
     uint16_t *pf_hi = nullptr, *pf_lo = nullptr, *pf_ahi = nullptr, *pf_alo = nullptr, *pf_hhi = nullptr,
              *pf_hlo = nullptr;
+    // split-K partial tiles and arrival counters of the short-prompt GEMM
+    float *pf_part = nullptr;
+    unsigned *pf_cnt = nullptr;
     // split-bf16 KV rows for the MFMA prefill attention (rows [0, kv_cap))
     int kv_cap = 0;
     uint16_t *pf_kh = nullptr, *pf_kl = nullptr, *pf_vth = nullptr, *pf_vtl = nullptr;

@@ -141,12 +141,22 @@ struct GemmArgs {
     int hd, nq, nkv;
     float *q_out;  // [N][nq*hd]
     float *k_cache, *v_cache;
+    // split-K workspace of the short-prompt kernel: partial tiles and one
+    // arrival counter per quarter tile (zero between launches; each launch
+    // leaves them zero).  Null disables split-K.
+    float *part;
+    unsigned *cnt;
 };
 
 // Prompts of at least kTiledMinTokens tokens (and K a multiple of 64) use the
-// LDS-tiled 128x128 kernel; shorter ones the 16x64 streaming kernel.
+// LDS-tiled 128x128 kernel; shorter ones the 64x64 split-K kernel (K a
+// multiple of 64) or the 16x64 streaming kernel.
 constexpr int kTiledMinTokens = 256;
 hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s);
+// Workspace the short-prompt kernel needs: floats of partials and counters
+// for any GEMM with at most `max_m` rows and fewer than kTiledMinTokens tokens.
+constexpr size_t kSkinnyPartFloats = (size_t)768 * 64 * 64;
+inline size_t skinny_counters(int max_m) { return (size_t)((max_m + 63) / 64) * ((kTiledMinTokens + 63) / 64) * 4; }
 
 // Copy row `row` of x[T,H] to dst[H] (last prefill row -> decode residual).
 hipError_t launch_copy_row(const float *x, int row, int H, float *dst, hipStream_t s);

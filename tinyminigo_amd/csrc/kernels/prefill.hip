@@ -9,6 +9,7 @@
 // BF16 and accumulation is f32.  Epilogues fuse RoPE + KV append, the
 // residual add and SwiGLU; the next GEMM's split operands are written
 // directly.
+#include "coh.cuh"
 #include "common.cuh"
 #include "kernels.hpp"
 
@@ -28,19 +29,51 @@ __global__ __launch_bounds__(kBlock) void embed_gather_kernel(const int *tokens,
 }
 
 // rms_norm_batch (src/tensor.rs:946-954): inv = 1/sqrt(ss/n + eps), v*(inv*w).
-__global__ __launch_bounds__(kBlock) void rmsnorm_split_kernel(const float *x, const float *w, float eps, int H,
+// One wavefront per row (four rows per workgroup), sum of squares reduced in
+// registers + DPP.  Rows of up to 4096 floats in 256-float blocks are held in
+// registers with the norm weights (every load issued up front); other widths
+// take a strided loop.
+__global__ __launch_bounds__(kBlock) void rmsnorm_split_kernel(const float *x, const float *w, float eps, int H, int T,
                                                               uint16_t *hi, uint16_t *lo) {
-    __shared__ float scratch[4];
-    const int row = blockIdx.x;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= T) return;
     const float *xr = x + (size_t)row * H;
-    float ss[1] = {0.0f};
-    for (int i = threadIdx.x; i < H; i += kBlock) ss[0] += xr[i] * xr[i];
-    block_sum_n<1>(ss, scratch);
-    const float inv = 1.0f / sqrtf(ss[0] / (float)H + eps);
-    for (int i = threadIdx.x; i < H; i += kBlock) {
-        const float v = __fmul_rn(xr[i], __fmul_rn(inv, w[i]));
-        split_bf16(v, hi + (size_t)row * H + i, lo + (size_t)row * H + i);
+    uint16_t *hr = hi + (size_t)row * H, *lr = lo + (size_t)row * H;
+    if (H % 256 == 0 && H <= 4096) {
+        const int nb = H / 256;
+        float4 v[16], wv[16];
+#pragma unroll
+        for (int b = 0; b < 16; b++)
+            if (b < nb) {
+                v[b] = *reinterpret_cast<const float4 *>(xr + b * 256 + lane * 4);
+                wv[b] = *reinterpret_cast<const float4 *>(w + b * 256 + lane * 4);
+            }
+        float ss = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 16; b++)
+            if (b < nb) ss += v[b].x * v[b].x + v[b].y * v[b].y + v[b].z * v[b].z + v[b].w * v[b].w;
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+#pragma unroll
+        for (int b = 0; b < 16; b++) {
+            if (b < nb) {
+                const int i = b * 256 + lane * 4;
+                const float e[4] = {__fmul_rn(v[b].x, __fmul_rn(inv, wv[b].x)), __fmul_rn(v[b].y, __fmul_rn(inv, wv[b].y)),
+                                    __fmul_rn(v[b].z, __fmul_rn(inv, wv[b].z)), __fmul_rn(v[b].w, __fmul_rn(inv, wv[b].w))};
+                uint16_t h[4], l[4];
+#pragma unroll
+                for (int c = 0; c < 4; c++) split_bf16(e[c], &h[c], &l[c]);
+                *reinterpret_cast<uint2 *>(hr + i) = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+                *reinterpret_cast<uint2 *>(lr + i) = make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+            }
+        }
+        return;
     }
+    float ss = 0.0f;
+    for (int i = lane; i < H; i += 64) ss += xr[i] * xr[i];
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+    for (int i = lane; i < H; i += 64) split_bf16(__fmul_rn(xr[i], __fmul_rn(inv, w[i])), hr + i, lr + i);
 }
 
 // Epilogue of one MFMA output fragment: rows mb .. mb+3 (mb a multiple of 4)
@@ -326,6 +359,169 @@ __global__ __launch_bounds__(kBlock) void gemm_dma_kernel(const GemmArgs a) {
             gemm_store<EPI>(a, m0 + wm * 64 + i * 16 + q4 * 4, n0 + wn * 64 + j * 16 + r, acc[i][j]);
 }
 
+// Split-K MFMA GEMM for short prompts (fewer than kTiledMinTokens tokens).
+//
+// Workgroup tile: 64 weight rows x 64 tokens over one contiguous range of K
+// (split ks of nsplit).  Each 64-wide K step's W, Bhi and Blo tiles go
+// global -> LDS by DMA (XOR-swizzled 128-byte rows, as in gemm_dma_kernel)
+// through a kSkStages-deep ring, so the next steps are in flight while one
+// is multiplied and each step needs one barrier.  Wavefront w owns tokens
+// 16 w .. 16 w + 15 against all 64 rows (4 MFMA row blocks).  The ring is
+// 72 KB, so two workgroups share a CU and one's MFMAs overlap the other's
+// LDS reads.
+//
+// With nsplit > 1 every wavefront stores its partial quarter tile, and the
+// last of the quarter's nsplit wavefronts to arrive (device-scope counter)
+// adds the partials in split order and runs the epilogue, so the result does
+// not depend on arrival order.  Token tiles of one (row tile, split) pair are
+// placed 8 blocks apart, i.e. on one XCD, so the W stream they share is read
+// from HBM once.
+constexpr int kSkStages = 3;
+constexpr int kSkTile = 64 * 128;  // bytes of one 64 x 64 bf16 tile
+constexpr int kSkOps = 6;          // DMA instructions per wave per step
+constexpr int kSkMaxSplit = 8;
+
+template <int EPI>
+__global__ __launch_bounds__(kBlock, 2) void gemm_skinny_kernel(const GemmArgs a, int nsplit, int n_tiles) {
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[kSkStages * 3 * kSkTile];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int r = lane & 15, q = lane >> 4;
+    const int m_tiles = (a.M + 63) >> 6;
+    const int rest = blockIdx.x >> 3;
+    const int nt = rest % n_tiles;
+    const int g = (rest / n_tiles) * 8 + (blockIdx.x & 7);
+    if (g >= m_tiles * nsplit) return;  // padding blocks of the XCD grouping
+    const int mt = g % m_tiles, ks = g / m_tiles;
+    const int K = a.K, nk = K >> 6;
+    const int s0 = ks * nk / nsplit, ns = (ks + 1) * nk / nsplit - s0;
+    const int m0 = mt * 64, n0 = nt * 64;
+    // DMA: wave w fills row groups 2w, 2w+1 (8 rows of 128 B) of each tile;
+    // lane l writes physical chunk l & 7 of row (l >> 3), i.e. logical chunk
+    // (l & 7) ^ (row & 7)
+    const uint16_t *src[3][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int row = (2 * wave + i) * 8 + (lane >> 3);
+        const int lc = (lane & 7) ^ (row & 7);
+        const size_t kofs = (size_t)s0 * 64 + lc * 8;
+        src[0][i] = a.W + (size_t)min(m0 + row, a.M - 1) * K + kofs;
+        src[1][i] = a.Bhi + (size_t)min(n0 + row, a.N - 1) * K + kofs;
+        src[2][i] = a.Blo + (size_t)min(n0 + row, a.N - 1) * K + kofs;
+    }
+    auto issue = [&](int j) {
+        unsigned char *dst = smem + (j % kSkStages) * 3 * kSkTile;
+#pragma unroll
+        for (int x = 0; x < 3; x++)
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                __builtin_amdgcn_global_load_lds(src[x][i] + j * 64, dst + x * kSkTile + (2 * wave + i) * 1024, 16, 0, 0);
+    };
+    for (int j = 0; j < kSkStages - 1 && j < ns; j++) issue(j);
+    f32x4 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int rb = wave * 16 + r;
+    for (int j = 0; j < ns; j++) {
+        // step j's DMAs are complete once at most the next step's are
+        // outstanding (vector memory completes in issue order)
+        static_assert(kSkStages == 3, "wait counts assume one step in flight behind the current one");
+        if (j + 1 < ns)
+            __builtin_amdgcn_s_waitcnt(0x0F70 | kSkOps);  // vmcnt(kSkOps)
+        else
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __builtin_amdgcn_s_barrier();  // every wave's DMAs of step j landed; step j-1's reads are done
+        if (j + kSkStages - 1 < ns) issue(j + kSkStages - 1);
+        const unsigned char *sa = smem + (j % kSkStages) * 3 * kSkTile;
+        const unsigned char *sh = sa + kSkTile, *sl = sa + 2 * kSkTile;
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+            const int lc = kk * 4 + q;
+            bf16x8 fa[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int ra = i * 16 + r;
+                fa[i] = *reinterpret_cast<const bf16x8 *>(sa + ra * 128 + ((lc ^ (ra & 7)) * 16));
+            }
+            const bf16x8 fh = *reinterpret_cast<const bf16x8 *>(sh + rb * 128 + ((lc ^ (rb & 7)) * 16));
+            const bf16x8 fl = *reinterpret_cast<const bf16x8 *>(sl + rb * 128 + ((lc ^ (rb & 7)) * 16));
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fh, acc[i], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fl, acc[i], 0, 0, 0);
+        }
+    }
+    const int col = n0 + rb;
+    if (nsplit > 1) {
+        // wave w's quarter of the tile (its 16 tokens) is reduced by the last
+        // of the tile's nsplit waves w to arrive.  Partials move through
+        // device-scope (sc1) stores and loads, which bypass the per-XCD L2s,
+        // and each wave's stores are complete before its counter increment,
+        // so no cache write-back or invalidation is needed; a per-wave
+        // counter needs no workgroup barrier.
+        const int slot = (nt * m_tiles + mt) * 4 + wave;
+        float *part = a.part + ((size_t)slot * nsplit + ks) * 1024 + lane;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) stf<true>(part + (i * 4 + e) * 64, acc[i][e]);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        unsigned old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(&a.cnt[slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = __builtin_amdgcn_readfirstlane(old);
+        if (old != (unsigned)(nsplit - 1)) return;
+        // all partials are loaded before any is added (one memory round trip)
+        const float *p0 = a.part + (size_t)slot * nsplit * 1024 + lane;
+        float pv[kSkMaxSplit][16];
+#pragma unroll
+        for (int sp = 0; sp < kSkMaxSplit; sp++)
+            if (sp < nsplit)
+#pragma unroll
+                for (int e = 0; e < 16; e++) pv[sp][e] = ldf<true>(p0 + (size_t)sp * 1024 + e * 64);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[i][e] = pv[0][i * 4 + e];
+#pragma unroll
+        for (int sp = 1; sp < kSkMaxSplit; sp++)
+            if (sp < nsplit)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[i][e] += pv[sp][i * 4 + e];
+        if (lane == 0) __hip_atomic_store(&a.cnt[slot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) gemm_store<EPI>(a, m0 + i * 16 + q * 4, col, acc[i]);
+}
+
+hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
+    // split K while the grid stays within one workgroup per CU, or while
+    // splits keep at least 20 K steps within three workgroups per CU; at most
+    // kSkMaxSplit ways, at least 2 steps per split
+    const int m_tiles = (a.M + 63) / 64, n_tiles = (a.N + 63) / 64, nk = a.K / 64;
+    int nsplit = 1;
+    if (a.part && a.cnt) {
+        for (;;) {
+            const int wg2 = m_tiles * n_tiles * nsplit * 2, ns2 = nk / (nsplit * 2);
+            if (nsplit * 2 > kSkMaxSplit || ns2 < 2) break;
+            if (wg2 <= 256 || (ns2 >= 20 && wg2 <= 768))
+                nsplit *= 2;
+            else
+                break;
+        }
+    }
+    if (nsplit > 1 && (size_t)m_tiles * n_tiles * nsplit * 4096 > kSkinnyPartFloats) return hipErrorInvalidValue;
+    const dim3 grid((m_tiles * nsplit + 7) / 8 * n_tiles * 8);
+    switch (epi) {
+        case GEPI_STORE: hipLaunchKernelGGL(gemm_skinny_kernel<GEPI_STORE>, grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
+        case GEPI_RESID: hipLaunchKernelGGL(gemm_skinny_kernel<GEPI_RESID>, grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
+        case GEPI_SWIGLU: hipLaunchKernelGGL(gemm_skinny_kernel<GEPI_SWIGLU>, grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
+        case GEPI_QKV: hipLaunchKernelGGL(gemm_skinny_kernel<GEPI_QKV>, grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 __global__ void copy_row_kernel(const float *x, int row, int H, float *dst) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < H; i += gridDim.x * blockDim.x)
         dst[i] = x[(size_t)row * H + i];
@@ -341,7 +537,7 @@ hipError_t launch_embed_gather(const int *tokens, int T, int H, const uint16_t *
 
 hipError_t launch_rmsnorm_split(const float *x, const float *w, float eps, int T, int H, uint16_t *hi, uint16_t *lo,
                                 hipStream_t s) {
-    hipLaunchKernelGGL(rmsnorm_split_kernel, dim3(T), dim3(kBlock), 0, s, x, w, eps, H, hi, lo);
+    hipLaunchKernelGGL(rmsnorm_split_kernel, dim3((T + 3) / 4), dim3(kBlock), 0, s, x, w, eps, H, T, hi, lo);
     return hipGetLastError();
 }
 
@@ -358,6 +554,7 @@ hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
         }
         return hipGetLastError();
     }
+    if (a.K % 64 == 0) return launch_skinny(epi, a, s);
     const dim3 grid((a.M + 15) / 16, (a.N + 63) / 64);
     switch (epi) {
         case GEPI_STORE: hipLaunchKernelGGL(gemm_kernel<GEPI_STORE>, grid, dim3(kBlock), 0, s, a); break;
