@@ -87,7 +87,7 @@ namespace tmg {
 // blocks; a cache of max_pos rows uses up to ceil(max_pos / kAttnBlock)
 // splits (at most kMaxSplits).  Up to kFusedSplits the merge runs in the
 // o_proj GEMV prologue; above that a combine kernel runs first.
-constexpr int kMaxSplits = 128;
+constexpr int kMaxSplits = 32;
 
 // Launch filter used by tmg_profile_decode_step: every kernel of the step is
 // announced with its name and algorithmic bytes; when `only` is set, just the

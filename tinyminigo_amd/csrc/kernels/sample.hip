@@ -3,19 +3,22 @@
 // sample, src/tensor.rs:1157-1213).
 //
 // Top-k path (0 < k <= kSampleMaxK, or greedy with a repetition penalty):
-//   pass 1, one workgroup per 2048-id slice: penalty, temperature, and a
-//   bitonic sort of packed (value, id) keys in LDS; the slice's best k keys
-//   are written out.
-//   pass 2, one workgroup: bitonic sort of all slice winners, then one lane
-//   runs the reference's sequential tail over the k candidates in order:
-//   softmax (max, exp, sequential sum, divide), nucleus cut at the first
-//   cumulative sum > top_p, renormalization, and the inverse-CDF walk.
+//   pass 1, one workgroup per 2048-id slice: penalty and temperature, then a
+//   radix select over the packed (value, id) keys held in registers (8-bit
+//   digits from the top, LDS histograms) finds the slice's k-th largest key;
+//   the slice's best k keys are written out unordered.
+//   pass 2, one workgroup: the same radix select over all slice winners, the
+//   k selected keys sorted by one wavefront (register bitonic sort), then one
+//   lane runs the reference's sequential tail over the k candidates in
+//   order: softmax (max, exp, sequential sum, divide), nucleus cut at the
+//   first cumulative sum > top_p, renormalization, and the inverse-CDF walk.
 // Full-vocabulary path (no top-k, top_p >= 1): one workgroup computes the
 // softmax and finds the draw with a block prefix sum in id order.
 //
 // Keys order by value descending, then id ascending, which is the reference
 // argmax tie rule; the reference's sort_unstable_by leaves equal-value order
 // unspecified, so any order among exact ties is as faithful as another.
+// Keys are unique (they contain the id), so the top k set is exact.
 #include "common.cuh"
 #include "kernels.hpp"
 
@@ -52,43 +55,104 @@ __device__ __forceinline__ float adjusted(const float *logits, const unsigned *s
     return v;
 }
 
-// Bitonic sort of n (power of two) keys in LDS, descending.
-__device__ void bitonic_desc(unsigned long long *k, int n) {
-    for (int size = 2; size <= n; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            __syncthreads();
-            for (int i = threadIdx.x; i < n / 2; i += blockDim.x) {
-                const int lo = 2 * i - (i & (stride - 1));
-                const int hi = lo + stride;
-                const bool desc = ((lo & size) == 0);
-                const unsigned long long a = k[lo], b = k[hi];
-                if (desc ? (a < b) : (a > b)) {
-                    k[lo] = b;
-                    k[hi] = a;
+// Radix select state shared by a workgroup.
+struct RadixSel {
+    unsigned hist[256];
+    int digit, above, count, n;
+};
+
+// Finds the k-th largest of the KPT keys each thread holds (k >= 1, at most
+// the number of keys): on return every thread has (prefix, mask) such that
+// the selected keys are exactly those with (key & mask) >= prefix, where mask
+// covers the top bits decided.  8-bit digits from the most significant;
+// stops as soon as the whole bin holding the k-th key is selected.
+template <int KPT>
+__device__ void radix_select(const unsigned long long (&key)[KPT], int k, RadixSel &rs, unsigned long long &prefix,
+                             unsigned long long &mask) {
+    const int t = threadIdx.x, nt = blockDim.x;
+    prefix = 0;
+    mask = 0;
+    int remaining = k;
+    for (int shift = 56; shift >= 0; shift -= 8) {
+        for (int i = t; i < 256; i += nt) rs.hist[i] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < KPT; j++)
+            if ((key[j] & mask) == prefix) atomicAdd(&rs.hist[(key[j] >> shift) & 255], 1u);
+        __syncthreads();
+        if (t < 64) {
+            // lane l holds digits 255 - 4l .. 252 - 4l, high digits first
+            unsigned c[4], sum = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                c[j] = rs.hist[255 - 4 * t - j];
+                sum += c[j];
+            }
+            // exclusive prefix over lanes by shuffles
+            unsigned incl = sum;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const unsigned o = __shfl_up(incl, off, 64);
+                if (t >= off) incl += o;
+            }
+            unsigned cum = incl - sum;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (cum < (unsigned)remaining && cum + c[j] >= (unsigned)remaining) {
+                    rs.digit = 255 - 4 * t - j;
+                    rs.above = (int)cum;
+                    rs.count = (int)c[j];
                 }
+                cum += c[j];
             }
         }
+        __syncthreads();
+        const int d = rs.digit;
+        remaining -= rs.above;
+        prefix |= (unsigned long long)d << shift;
+        mask |= 255ull << shift;
+        const bool done = rs.count == remaining;
+        __syncthreads();  // rs is rewritten by the next round
+        if (done) break;
     }
+}
+
+// Writes the selected keys (at most k; extra ties among padding keys are
+// dropped) to out[0 ..) in arbitrary order.
+template <int KPT>
+__device__ void radix_compact(const unsigned long long (&key)[KPT], int k, unsigned long long prefix,
+                              unsigned long long mask, RadixSel &rs, unsigned long long *out) {
+    if (threadIdx.x == 0) rs.n = 0;
     __syncthreads();
+#pragma unroll
+    for (int j = 0; j < KPT; j++) {
+        if ((key[j] & mask) >= prefix) {
+            const int pos = atomicAdd(&rs.n, 1);
+            if (pos < k) out[pos] = key[j];
+        }
+    }
 }
 
 __global__ __launch_bounds__(kBlock) void sample_partial_kernel(const SampleArgs a) {
-    __shared__ unsigned long long keys[kSampleSlice];
+    __shared__ RadixSel rs;
+    constexpr int KPT = kSampleSlice / kBlock;
     const DevState st = *a.st;
     const bool greedy = a.greedy != 0;
     const int K = greedy ? 1 : st.top_k;
     const int base = blockIdx.x * kSampleSlice;
-    for (int j = threadIdx.x; j < kSampleSlice; j += kBlock) {
-        const int i = base + j;
-        unsigned long long key = 0ull;
+    unsigned long long key[KPT];
+#pragma unroll
+    for (int j = 0; j < KPT; j++) {
+        const int i = base + j * kBlock + threadIdx.x;
+        key[j] = 0ull;
         if (i < a.V) {
             const float v = adjusted(a.logits, a.seen, st, i, greedy);
-            if (v == v) key = argmax_key(v, (uint32_t)i);
+            if (v == v) key[j] = argmax_key(v, (uint32_t)i);
         }
-        keys[j] = key;
     }
-    bitonic_desc(keys, kSampleSlice);
-    for (int j = threadIdx.x; j < K; j += kBlock) a.cand[(size_t)blockIdx.x * kSampleMaxK + j] = keys[j];
+    unsigned long long prefix, mask;
+    radix_select<KPT>(key, K, rs, prefix, mask);
+    radix_compact<KPT>(key, K, prefix, mask, rs, a.cand + (size_t)blockIdx.x * kSampleMaxK);
 }
 
 __device__ void emit_token(const SampleArgs &a, int tok) {
@@ -103,17 +167,45 @@ __device__ void emit_token(const SampleArgs &a, int tok) {
     a.seen_rw[tok >> 5] |= 1u << (tok & 31);
 }
 
-__global__ __launch_bounds__(1024) void sample_select_kernel(const SampleArgs a, int nslices, int npad) {
-    extern __shared__ unsigned long long cand[];
+__global__ __launch_bounds__(1024) void sample_select_kernel(const SampleArgs a, int nslices) {
+    __shared__ RadixSel rs;
+    __shared__ unsigned long long cand[kSampleMaxK];
     __shared__ float probs[kSampleMaxK];
+    constexpr int KPT = kSampleSelectKeys / 1024;
     const DevState st = *a.st;
     const bool greedy = a.greedy != 0;
     const int K = greedy ? 1 : st.top_k;
-    for (int i = threadIdx.x; i < npad; i += blockDim.x) {
-        const int sl = i / K, j = i - sl * K;
-        cand[i] = (sl < nslices) ? a.cand[(size_t)sl * kSampleMaxK + j] : 0ull;
+    const int n = nslices * K;
+    unsigned long long key[KPT];
+#pragma unroll
+    for (int j = 0; j < KPT; j++) {
+        const int i = j * 1024 + threadIdx.x;
+        const int sl = i / K, jj = i - sl * K;
+        key[j] = i < n ? a.cand[(size_t)sl * kSampleMaxK + jj] : 0ull;
     }
-    bitonic_desc(cand, npad);
+    unsigned long long prefix, mask;
+    radix_select<KPT>(key, K, rs, prefix, mask);
+    if (threadIdx.x < kSampleMaxK) cand[threadIdx.x] = 0ull;
+    __syncthreads();
+    radix_compact<KPT>(key, K, prefix, mask, rs, cand);
+    __syncthreads();
+    if (threadIdx.x >= 64) return;
+    // sort the (at most 64) winners descending: register bitonic sort in one wavefront
+    {
+        const int lane = threadIdx.x;
+        unsigned long long v = cand[lane];
+#pragma unroll
+        for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                const unsigned long long o = shfl_xor_u64(v, stride);
+                const bool lower = (lane & stride) == 0, desc = (lane & size) == 0;
+                const unsigned long long hi = v > o ? v : o, lo = v > o ? o : v;
+                v = (lower == desc) ? hi : lo;
+            }
+        }
+        cand[lane] = v;
+    }
     if (threadIdx.x != 0) return;
     if (greedy) {
         // all -inf/NaN logits leave key 0 on top: the reference returns 0
@@ -242,13 +334,11 @@ hipError_t launch_sample(const SampleArgs &a, hipStream_t s) {
     const int nslices = (a.V + kSampleSlice - 1) / kSampleSlice;
     if (a.greedy || a.cand) {
         // top-k (or greedy) path; the host only sets cand when top_k is usable
+        if (nslices * kSampleMaxK > kSampleSelectKeys) return hipErrorInvalidValue;
         hipLaunchKernelGGL(sample_partial_kernel, dim3(nslices), dim3(kBlock), 0, s, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        // npad: power of two covering nslices * kSampleMaxK (worst case k)
-        int npad = 1;
-        while (npad < nslices * kSampleMaxK) npad <<= 1;
-        hipLaunchKernelGGL(sample_select_kernel, dim3(1), dim3(1024), (size_t)npad * 8, s, a, nslices, npad);
+        hipLaunchKernelGGL(sample_select_kernel, dim3(1), dim3(1024), 0, s, a, nslices);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(sample_full_kernel, dim3(1), dim3(1024), 0, s, a);
