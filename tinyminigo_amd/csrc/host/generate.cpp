@@ -124,24 +124,14 @@ extern "C" int tmg_generate(tmg_model *m, const uint32_t *prompt, size_t n_promp
 
     const size_t max_tokens = p->max_tokens;
     if (max_tokens == 0) return TMG_OK;
-    // pinned slots for the generated ids, one per token
-    int *host_tok = nullptr;
-    TMG_HIPG(hipHostMalloc((void **)&host_tok, (max_tokens + 1) * sizeof(int), hipHostMallocDefault));
-    struct PinGuard {
-        int *p;
-        hipStream_t s;
-        ~PinGuard() {
-            (void)hipStreamSynchronize(s);  // no copy may still target the slots
-            (void)hipHostFree(p);
-        }
-    } pg{host_tok, m->stream};
+    // the kernels write each id into c->history (coherent pinned host memory)
+    const volatile int *host_tok = c->history;
     EventRing ring;
     ring.ev.resize(kWindow + 1);
     for (auto &e : ring.ev) TMG_HIPG(hipEventCreateWithFlags(&e, hipEventDisableTiming));
 
     // token 0 comes from the prefill logits (src/model.rs:623-646)
     if ((rc = enqueue_select(m, c, mode, 0))) return rc;
-    TMG_HIPG(hipMemcpyAsync(host_tok, c->history, sizeof(int), hipMemcpyDeviceToHost, m->stream));
     TMG_HIPG(hipEventRecord(ring.ev[0], m->stream));
 
     size_t enq = 0;  // forward steps enqueued; step j consumes token j and yields token j+1
@@ -149,8 +139,6 @@ extern "C" int tmg_generate(tmg_model *m, const uint32_t *prompt, size_t n_promp
     for (size_t i = 0; i < max_tokens; i++) {
         while (enq < max_tokens && enq < i + kWindow) {
             if ((rc = launch_step(m, c, mode))) return rc;
-            TMG_HIPG(hipMemcpyAsync(host_tok + enq + 1, c->history + enq + 1, sizeof(int), hipMemcpyDeviceToHost,
-                                    m->stream));
             TMG_HIPG(hipEventRecord(ring.ev[(enq + 1) % (kWindow + 1)], m->stream));
             enq++;
         }

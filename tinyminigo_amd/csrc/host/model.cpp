@@ -881,7 +881,8 @@ extern "C" int tmg_cache_new(tmg_model *m, uint32_t max_pos, tmg_cache **out) {
     int rc = TMG_OK;
     void *k = nullptr, *v = nullptr, *st = nullptr, *hist = nullptr;
     if (hipMalloc(&k, n * 4) != hipSuccess || hipMalloc(&v, n * 4) != hipSuccess ||
-        hipMalloc(&st, sizeof(DevState)) != hipSuccess || hipMalloc(&hist, ((size_t)max_pos + 2) * 4) != hipSuccess)
+        hipMalloc(&st, sizeof(DevState)) != hipSuccess ||
+        hipHostMalloc(&hist, ((size_t)max_pos + 2) * 4, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess)
         rc = set_error(TMG_E_NOMEM, "KV cache allocation of " + std::to_string(2 * n * 4) + " bytes failed");
     c->k = (float *)k;
     c->v = (float *)v;
@@ -940,7 +941,7 @@ extern "C" void tmg_cache_free(tmg_cache *c) {
     (void)hipFree(c->k);
     (void)hipFree(c->v);
     (void)hipFree(c->st);
-    (void)hipFree(c->history);
+    (void)hipHostFree(c->history);
     delete c;
 }
 
@@ -1062,9 +1063,7 @@ extern "C" int tmg_decode_greedy(tmg_model *m, tmg_cache *c, uint32_t token, uin
     if (ms) *ms = el;
     if (used && (rc = check_persistent(m, c))) return rc;
     if (tokens_out && n_steps) {
-        if ((rc = pinned(m, (size_t)n_steps * 4))) return rc;
-        TMG_HIP(hipMemcpy(m->pin, c->history, (size_t)n_steps * 4, hipMemcpyDeviceToHost));
-        memcpy(tokens_out, m->pin, (size_t)n_steps * 4);
+        memcpy(tokens_out, (const void *)c->history, (size_t)n_steps * 4);
     }
     return TMG_OK;
 }

@@ -68,7 +68,10 @@ struct tmg_cache {
     uint32_t max_pos = 0;
     float *k = nullptr, *v = nullptr;  // [L][max_pos][kvd]
     tmg::DevState *st = nullptr;       // device
-    int *history = nullptr;            // device, max_pos + 2 entries
+    // generated ids, max_pos + 2 entries, in coherent pinned host memory that
+    // the kernels write directly (the host reads a token as soon as the step
+    // that wrote it has completed; no copy per step)
+    int *history = nullptr;
     uint32_t len = 0;                  // host mirror of st->pos
     int attn_nsplit = 1;               // split-K width of decode attention for this cache
     unsigned *seen = nullptr;          // bitmap of generated ids (repetition penalty)

@@ -225,7 +225,7 @@ hipError_t launch_persistent(const void *kernel, int grid, const PersistArgs &a,
 // the vocabulary the first pass sorts.
 constexpr int kSampleMaxK = 64;
 constexpr int kSampleSlice = 2048;
-// Candidates the second sampling pass holds (8 per thread of 1024): slices x
+// Candidates the second sampling pass holds (16 per thread of 512): slices x
 // kSampleMaxK may not exceed it, i.e. vocabularies up to 262144 ids.
 constexpr int kSampleSelectKeys = 8192;
 

@@ -5,9 +5,9 @@
 // Top-k path (0 < k <= kSampleMaxK, or greedy with a repetition penalty):
 //   pass 1, one workgroup per 2048-id slice: penalty and temperature, then a
 //   radix select over the packed (value, id) keys held in registers (8-bit
-//   digits from the top, LDS histograms) finds the slice's k-th largest key;
-//   the slice's best k keys are written out unordered.
-//   pass 2, one workgroup: the same radix select over all slice winners, the
+//   digits from the top, LDS histograms; block_top_k) finds the slice's k-th
+//   largest key; the slice's best k keys are written out unordered.
+//   pass 2, one workgroup: the same selection over all slice winners, the
 //   k selected keys sorted by one wavefront (register bitonic sort), then one
 //   lane runs the reference's sequential tail over the k candidates in
 //   order: softmax (max, exp, sequential sum, divide), nucleus cut at the
@@ -57,18 +57,20 @@ __device__ __forceinline__ float adjusted(const float *logits, const unsigned *s
 
 // Radix select state shared by a workgroup.
 struct RadixSel {
+    unsigned long long kmin;
     unsigned hist[256];
     int digit, above, count, n;
 };
 
-// Finds the k-th largest of the KPT keys each thread holds (k >= 1, at most
-// the number of keys): on return every thread has (prefix, mask) such that
-// the selected keys are exactly those with (key & mask) >= prefix, where mask
-// covers the top bits decided.  8-bit digits from the most significant;
-// stops as soon as the whole bin holding the k-th key is selected.
+// Finds the k-th largest of the valid keys among the KPT each thread holds
+// (1 <= k <= number of valid keys): on return every thread has
+// (prefix, mask) such that the selected valid keys are exactly those with
+// (key & mask) >= prefix, where mask covers the top bits decided.  8-bit
+// digits from the most significant; stops as soon as the whole bin holding
+// the k-th key is selected.
 template <int KPT>
-__device__ void radix_select(const unsigned long long (&key)[KPT], int k, RadixSel &rs, unsigned long long &prefix,
-                             unsigned long long &mask) {
+__device__ void radix_select(const unsigned long long (&key)[KPT], const bool (&valid)[KPT], int k, RadixSel &rs,
+                             unsigned long long &prefix, unsigned long long &mask) {
     const int t = threadIdx.x, nt = blockDim.x;
     prefix = 0;
     mask = 0;
@@ -78,7 +80,7 @@ __device__ void radix_select(const unsigned long long (&key)[KPT], int k, RadixS
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < KPT; j++)
-            if ((key[j] & mask) == prefix) atomicAdd(&rs.hist[(key[j] >> shift) & 255], 1u);
+            if (valid[j] && (key[j] & mask) == prefix) atomicAdd(&rs.hist[(key[j] >> shift) & 255], 1u);
         __syncthreads();
         if (t < 64) {
             // lane l holds digits 255 - 4l .. 252 - 4l, high digits first
@@ -117,16 +119,69 @@ __device__ void radix_select(const unsigned long long (&key)[KPT], int k, RadixS
     }
 }
 
-// Writes the selected keys (at most k; extra ties among padding keys are
-// dropped) to out[0 ..) in arbitrary order.
-template <int KPT>
-__device__ void radix_compact(const unsigned long long (&key)[KPT], int k, unsigned long long prefix,
-                              unsigned long long mask, RadixSel &rs, unsigned long long *out) {
-    if (threadIdx.x == 0) rs.n = 0;
+// Selects the k largest valid keys of the block (all of them when there are
+// at most k) and writes them, unordered, to out[0 .. k); missing ones are
+// written as 0.  With PREFILTER, a first selection over the per-thread maxima
+// gives a lower bound T0 for the k-th largest key (the k largest maxima are k
+// distinct keys), and only keys >= T0 enter the exact selection: worth it
+// where most threads hold few real keys (the second pass), not where every
+// thread holds eight (the slices).
+template <int KPT, bool PREFILTER>
+__device__ void block_top_k(const unsigned long long (&key)[KPT], const bool (&valid)[KPT], int nvalid, int k,
+                            RadixSel &rs, unsigned long long *out) {
+    const int t = threadIdx.x;
+    for (int i = t; i < k; i += blockDim.x) out[i] = 0ull;
+    bool cv[KPT];
+#pragma unroll
+    for (int j = 0; j < KPT; j++) cv[j] = valid[j];
+    int ncand = nvalid;
+    if (PREFILTER && nvalid > k) {
+        unsigned long long tmax = 0;
+        bool any = false;
+#pragma unroll
+        for (int j = 0; j < KPT; j++)
+            if (valid[j]) {
+                tmax = key[j] > tmax ? key[j] : tmax;
+                any = true;
+            }
+        if (t == 0) rs.n = 0;
+        __syncthreads();
+        if (any) atomicAdd(&rs.n, 1);
+        __syncthreads();
+        const int nany = rs.n;
+        __syncthreads();
+        if (nany >= k) {
+            const unsigned long long km[1] = {tmax};
+            const bool kv[1] = {any};
+            unsigned long long p0, m0;
+            radix_select<1>(km, kv, k, rs, p0, m0);
+            // the k-th largest maximum: the smallest maximum inside the selection
+            if (t == 0) rs.kmin = ~0ull;
+            __syncthreads();
+            if (any && (tmax & m0) >= p0) atomicMin(&rs.kmin, tmax);
+            __syncthreads();
+            const unsigned long long t0 = rs.kmin;
+            int mine = 0;
+#pragma unroll
+            for (int j = 0; j < KPT; j++) {
+                cv[j] = valid[j] && key[j] >= t0;
+                mine += cv[j];
+            }
+            if (t == 0) rs.n = 0;
+            __syncthreads();
+            if (mine) atomicAdd(&rs.n, mine);
+            __syncthreads();
+            ncand = rs.n;
+            __syncthreads();
+        }
+    }
+    unsigned long long prefix = 0, mask = 0;  // (key & 0) >= 0: every candidate
+    if (ncand > k) radix_select<KPT>(key, cv, k, rs, prefix, mask);
+    if (t == 0) rs.n = 0;
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < KPT; j++) {
-        if ((key[j] & mask) >= prefix) {
+        if (cv[j] && (key[j] & mask) >= prefix) {
             const int pos = atomicAdd(&rs.n, 1);
             if (pos < k) out[pos] = key[j];
         }
@@ -141,18 +196,19 @@ __global__ __launch_bounds__(kBlock) void sample_partial_kernel(const SampleArgs
     const int K = greedy ? 1 : st.top_k;
     const int base = blockIdx.x * kSampleSlice;
     unsigned long long key[KPT];
+    bool valid[KPT];
 #pragma unroll
     for (int j = 0; j < KPT; j++) {
         const int i = base + j * kBlock + threadIdx.x;
         key[j] = 0ull;
-        if (i < a.V) {
+        valid[j] = i < a.V;
+        if (valid[j]) {
             const float v = adjusted(a.logits, a.seen, st, i, greedy);
             if (v == v) key[j] = argmax_key(v, (uint32_t)i);
         }
     }
-    unsigned long long prefix, mask;
-    radix_select<KPT>(key, K, rs, prefix, mask);
-    radix_compact<KPT>(key, K, prefix, mask, rs, a.cand + (size_t)blockIdx.x * kSampleMaxK);
+    block_top_k<KPT, false>(key, valid, min(kSampleSlice, a.V - base), K, rs,
+                            a.cand + (size_t)blockIdx.x * kSampleMaxK);
 }
 
 __device__ void emit_token(const SampleArgs &a, int tok) {
@@ -167,96 +223,97 @@ __device__ void emit_token(const SampleArgs &a, int tok) {
     a.seen_rw[tok >> 5] |= 1u << (tok & 31);
 }
 
-__global__ __launch_bounds__(1024) void sample_select_kernel(const SampleArgs a, int nslices) {
+// Lane l's float of wavefront-uniform lane i (a scalar read, no LDS).
+__device__ __forceinline__ float lane_f(float v, int i) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+}
+
+constexpr int kSelectThreads = 512;
+
+__global__ __launch_bounds__(kSelectThreads) void sample_select_kernel(const SampleArgs a, int nslices) {
     __shared__ RadixSel rs;
     __shared__ unsigned long long cand[kSampleMaxK];
-    __shared__ float probs[kSampleMaxK];
-    constexpr int KPT = kSampleSelectKeys / 1024;
+    constexpr int KPT = kSampleSelectKeys / kSelectThreads;
     const DevState st = *a.st;
     const bool greedy = a.greedy != 0;
     const int K = greedy ? 1 : st.top_k;
     const int n = nslices * K;
     unsigned long long key[KPT];
+    bool valid[KPT];
 #pragma unroll
     for (int j = 0; j < KPT; j++) {
-        const int i = j * 1024 + threadIdx.x;
+        const int i = j * kSelectThreads + threadIdx.x;
         const int sl = i / K, jj = i - sl * K;
-        key[j] = i < n ? a.cand[(size_t)sl * kSampleMaxK + jj] : 0ull;
+        valid[j] = i < n;
+        key[j] = valid[j] ? a.cand[(size_t)sl * kSampleMaxK + jj] : 0ull;
     }
-    unsigned long long prefix, mask;
-    radix_select<KPT>(key, K, rs, prefix, mask);
     if (threadIdx.x < kSampleMaxK) cand[threadIdx.x] = 0ull;
-    __syncthreads();
-    radix_compact<KPT>(key, K, prefix, mask, rs, cand);
+    block_top_k<KPT, true>(key, valid, n, K, rs, cand);
     __syncthreads();
     if (threadIdx.x >= 64) return;
-    // sort the (at most 64) winners descending: register bitonic sort in one wavefront
-    {
-        const int lane = threadIdx.x;
-        unsigned long long v = cand[lane];
+    // one wavefront from here: lane i holds candidate i.  Sort the (at most
+    // 64) winners descending with a register bitonic sort.
+    const int lane = threadIdx.x;
+    unsigned long long v = cand[lane];
 #pragma unroll
-        for (int size = 2; size <= 64; size <<= 1) {
+    for (int size = 2; size <= 64; size <<= 1) {
 #pragma unroll
-            for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                const unsigned long long o = shfl_xor_u64(v, stride);
-                const bool lower = (lane & stride) == 0, desc = (lane & size) == 0;
-                const unsigned long long hi = v > o ? v : o, lo = v > o ? o : v;
-                v = (lower == desc) ? hi : lo;
-            }
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const unsigned long long o = shfl_xor_u64(v, stride);
+            const bool lower = (lane & stride) == 0, desc = (lane & size) == 0;
+            const unsigned long long hi = v > o ? v : o, lo = v > o ? o : v;
+            v = (lower == desc) ? hi : lo;
         }
-        cand[lane] = v;
     }
-    if (threadIdx.x != 0) return;
     if (greedy) {
         // all -inf/NaN logits leave key 0 on top: the reference returns 0
-        const unsigned long long top = cand[0];
-        emit_token(a, top ? key_index(top) : 0);
+        if (lane == 0) emit_token(a, v ? key_index(v) : 0);
         return;
     }
-    // softmax over the k candidates in candidate order (src/tensor.rs:1177-1179)
-    const float mx = key_value(cand[0]);
+    // The reference's sequential tail, elementwise work across lanes and the
+    // running sums in candidate order through lane reads, so every float
+    // operation is the reference's, in its order.
+    // softmax over the k candidates (src/tensor.rs:1177-1179)
+    const float val = key_value(v);
+    const float mx = lane_f(val, 0);
+    float p = lane < K ? expf(val - mx) : 0.0f;
     float sum = 0.0f;
-    for (int i = 0; i < K; i++) {
-        probs[i] = expf(key_value(cand[i]) - mx);
-        sum += probs[i];
-    }
-    for (int i = 0; i < K; i++) probs[i] = probs[i] / sum;
+    for (int i = 0; i < K; i++) sum += lane_f(p, i);
+    p = p / sum;
     // nucleus (src/tensor.rs:1182-1201): candidates are already in descending
     // probability order
     if (st.top_p < 1.0f) {
         float cum = 0.0f;
         int cutoff = K;
         for (int r = 0; r < K; r++) {
-            cum += probs[r];
+            cum += lane_f(p, r);
             if (cum > st.top_p) {
                 cutoff = r + 1;
                 break;
             }
         }
         float s2 = 0.0f;
-        for (int r = 0; r < cutoff; r++) s2 += probs[r];
-        for (int r = 0; r < K; r++) probs[r] = r < cutoff ? probs[r] / s2 : 0.0f;
+        for (int r = 0; r < cutoff; r++) s2 += lane_f(p, r);
+        p = lane < cutoff ? p / s2 : 0.0f;
     }
     // inverse-CDF walk in candidate order (src/tensor.rs:1203-1212)
     const float r = uniform_f32(st.seed, (unsigned long long)st.step);
     float cum = 0.0f;
     int pick = -1;
     for (int i = 0; i < K; i++) {
-        cum += probs[i];
+        cum += lane_f(p, i);
         if (r < cum) {
             pick = i;
             break;
         }
     }
     if (pick < 0) {
-        pick = 0;
-        for (int i = 0; i < K; i++)
-            if (probs[i] > 0.0f) {
-                pick = i;
-                break;
-            }
+        const unsigned long long pos = __ballot(lane < K && p > 0.0f);
+        pick = pos ? __builtin_ctzll(pos) : 0;
     }
-    emit_token(a, key_index(cand[pick]));
+    const uint32_t klo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, pick);
+    const uint32_t khi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), pick);
+    if (lane == 0) emit_token(a, key_index(((unsigned long long)khi << 32) | klo));
 }
 
 // No top-k: candidates are all ids in id order (src/tensor.rs:1169-1179).
@@ -338,7 +395,7 @@ hipError_t launch_sample(const SampleArgs &a, hipStream_t s) {
         hipLaunchKernelGGL(sample_partial_kernel, dim3(nslices), dim3(kBlock), 0, s, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(sample_select_kernel, dim3(1), dim3(1024), 0, s, a, nslices);
+        hipLaunchKernelGGL(sample_select_kernel, dim3(1), dim3(kSelectThreads), 0, s, a, nslices);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(sample_full_kernel, dim3(1), dim3(1024), 0, s, a);
