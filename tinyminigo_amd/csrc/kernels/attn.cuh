@@ -6,8 +6,9 @@
 //
 // One call handles one (query row, KV head, split) item: the split's
 // 64-position blocks of the row's context, for all GROUP query heads of the KV head, so
-// every K/V load serves GROUP heads.  TS = HD/4 lanes own one position (a
-// float4 of K and of V each); the 256 threads form NTEAM such teams.  Each
+// every K/V load serves GROUP heads.  TS = HD/(4 VPL) lanes own one position
+// (VPL float4s of K and of V each, interleaved so one load instruction covers
+// TS x 16 contiguous bytes); the 256 threads form NTEAM such teams.  Each
 // team keeps its own online-softmax state (running max, sum, output) over the
 // positions it visits, so the chunk loop has no block-wide synchronization;
 // K and V of a 64-position chunk are loaded together and the next chunk is
@@ -22,23 +23,26 @@
 
 namespace tmg {
 
+// Lane geometry: VPL float4s per lane, TS lanes per position, NTEAM teams, J
+// positions per team per chunk of CH positions.  Two float4s per lane at
+// head_dim 128 halve the cross-lane reduction steps per score against one
+// (measured faster with two query heads per KV head, slower with four, where
+// the doubled accumulator registers cost more than the reductions saved).
 template <int HD, int GROUP>
-struct AttnShared {
-    static constexpr int TS = HD / 4;
-    static constexpr int NTEAM = kBlock / TS;
-    float o[NTEAM][GROUP][HD];
-    float m[NTEAM][GROUP];
-    float l[NTEAM][GROUP];
-};
-
-// Lane geometry: TS lanes per position, NTEAM teams, J positions per team per
-// chunk of CH positions.
-template <int HD>
 struct AttnGeom {
-    static constexpr int TS = HD / 4;
+    static constexpr int VPL = (HD >= 128 && GROUP <= 2) ? 2 : 1;
+    static constexpr int TS = HD / (4 * VPL);
     static constexpr int NTEAM = kBlock / TS;
     static constexpr int J = NTEAM >= 64 ? 1 : 64 / NTEAM;
     static constexpr int CH = NTEAM * J;
+};
+
+template <int HD, int GROUP>
+struct AttnShared {
+    static constexpr int NTEAM = AttnGeom<HD, GROUP>::NTEAM;
+    float o[NTEAM][GROUP][HD];
+    float m[NTEAM][GROUP];
+    float l[NTEAM][GROUP];
 };
 
 // Split count of a decode attention row at context n_ctx: the same formula in
@@ -63,32 +67,41 @@ __device__ __forceinline__ int active_splits(int n_ctx, int nsplit) {
 template <int HD, int GROUP, bool COH, bool PREFETCH = true, bool SPEC = false>
 __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, int ti, int qpos, int active,
                                           AttnShared<HD, GROUP> &sm) {
-    constexpr int TS = HD / 4;
-    constexpr int NTEAM = kBlock / TS;
-    constexpr int J = AttnGeom<HD>::J;  // positions per team per chunk
-    constexpr int CH = NTEAM * J;
+    using G = AttnGeom<HD, GROUP>;
+    constexpr int VPL = G::VPL, TS = G::TS, NTEAM = G::NTEAM;
+    constexpr int J = G::J;  // positions per team per chunk
+    constexpr int CH = G::CH;
     const int t = threadIdx.x, lt = t % TS, team = t / TS;
     const int kvd = a.nkv * HD;
     const int qd = a.nq * HD;
+    // lane lt owns dims (v TS + lt) 4 .. + 3 for v < VPL
     const float *kbase = a.k_cache + g * HD + lt * 4;
     const float *vbase = a.v_cache + g * HD + lt * 4;
 
-    float4 qv[GROUP];
+    float4 qv[GROUP][VPL];
     const float *qrow = a.q + (size_t)ti * qd;
 #pragma unroll
-    for (int h = 0; h < GROUP; h++) qv[h] = ldf4<COH>(qrow + (g * GROUP + h) * HD + lt * 4);
+    for (int h = 0; h < GROUP; h++)
+#pragma unroll
+        for (int v = 0; v < VPL; v++) qv[h][v] = ldf4<COH>(qrow + (g * GROUP + h) * HD + (v * TS + lt) * 4);
 
     static_assert(CH == 64, "the split partition deals 64-position blocks");
-    float4 kr[J], vr[J];
+    float4 kr[J][VPL], vr[J][VPL];
+    auto load_kv = [&](float4(&kd)[J][VPL], float4(&vd)[J][VPL], int c0, int lim) {
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            const int p = min(c0 + team + j * NTEAM, lim);
+#pragma unroll
+            for (int v = 0; v < VPL; v++) {
+                kd[j][v] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd + v * TS * 4);
+                vd[j][v] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd + v * TS * 4);
+            }
+        }
+    };
     const int c_first = split * CH, c_step = a.nsplit * CH;
     if constexpr (SPEC) {
         const int pos0 = *a.pos_dev;  // a scalar load, first used after the K/V loads are issued
-#pragma unroll
-        for (int j = 0; j < J; j++) {
-            const int p = min(c_first + team + j * NTEAM, a.cap - 1);
-            kr[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
-            vr[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
-        }
+        load_kv(kr, vr, c_first, a.cap - 1);
         // keep the loads above the position read: without this fence the
         // compiler sinks them behind it (into the branch that uses them)
         asm volatile("" ::: "memory");
@@ -100,37 +113,24 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
     const float sl2 = a.scale * 1.4426950408889634f;  // scores in log2 units: softmax by exp2
 
     float m_run[GROUP], l_run[GROUP];
-    float4 o_acc[GROUP];
+    float4 o_acc[GROUP][VPL];
 #pragma unroll
     for (int h = 0; h < GROUP; h++) {
         m_run[h] = -INFINITY;
         l_run[h] = 0.0f;
-        o_acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int v = 0; v < VPL; v++) o_acc[h][v] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
 
     // Rows past the context are loaded clamped (branch-free) and masked where
     // used: their score is -inf and their V row is replaced by zeros (0 *
     // garbage could be NaN).
     const int last = n_ctx - 1;
-    if constexpr (!SPEC) {
-#pragma unroll
-        for (int j = 0; j < J; j++) {
-            const int p = min(c_first + team + j * NTEAM, last);
-            kr[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
-            vr[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
-        }
-    }
+    if constexpr (!SPEC) load_kv(kr, vr, c_first, last);
     for (int c0 = c_first; c0 < n_ctx; c0 += c_step) {
-        float4 kn[J], vn[J];
+        float4 kn[J][VPL], vn[J][VPL];
         const bool more = c0 + c_step < n_ctx;
-        if (PREFETCH && more) {
-#pragma unroll
-            for (int j = 0; j < J; j++) {
-                const int p = min(c0 + c_step + team + j * NTEAM, last);
-                kn[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
-                vn[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
-            }
-        }
+        if (PREFETCH && more) load_kv(kn, vn, c0 + c_step, last);
         // scores of this team's positions (every lane of the team gets them)
         float s[J][GROUP];
 #pragma unroll
@@ -140,10 +140,17 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
             for (int h = 0; h < GROUP; h++) {
                 float d = 0.0f;
                 if (ok) {
-                    d = qv[h].x * kr[j].x;
-                    d = fmaf(qv[h].y, kr[j].y, d);
-                    d = fmaf(qv[h].z, kr[j].z, d);
-                    d = fmaf(qv[h].w, kr[j].w, d);
+                    d = qv[h][0].x * kr[j][0].x;
+                    d = fmaf(qv[h][0].y, kr[j][0].y, d);
+                    d = fmaf(qv[h][0].z, kr[j][0].z, d);
+                    d = fmaf(qv[h][0].w, kr[j][0].w, d);
+#pragma unroll
+                    for (int v = 1; v < VPL; v++) {
+                        d = fmaf(qv[h][v].x, kr[j][v].x, d);
+                        d = fmaf(qv[h][v].y, kr[j][v].y, d);
+                        d = fmaf(qv[h][v].z, kr[j][v].z, d);
+                        d = fmaf(qv[h][v].w, kr[j][v].w, d);
+                    }
                 }
                 d = group_sum<TS>(d);
                 s[j][h] = ok ? d * sl2 : -INFINITY;
@@ -159,37 +166,42 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
             const float m_new = fmaxf(m_run[h], mc);
             const float corr = (m_run[h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run[h] - m_new);
             float l = l_run[h] * corr;
-            float4 o = make_float4(o_acc[h].x * corr, o_acc[h].y * corr, o_acc[h].z * corr, o_acc[h].w * corr);
+            float4 o[VPL];
+#pragma unroll
+            for (int v = 0; v < VPL; v++)
+                o[v] = make_float4(o_acc[h][v].x * corr, o_acc[h][v].y * corr, o_acc[h][v].z * corr,
+                                   o_acc[h][v].w * corr);
 #pragma unroll
             for (int j = 0; j < J; j++) {
                 const bool ok = s[j][h] != -INFINITY;
                 const float p = ok ? __builtin_amdgcn_exp2f(s[j][h] - m_new) : 0.0f;
-                const float4 v = ok ? vr[j] : make_float4(0.f, 0.f, 0.f, 0.f);
                 l += p;
-                o.x = fmaf(p, v.x, o.x);
-                o.y = fmaf(p, v.y, o.y);
-                o.z = fmaf(p, v.z, o.z);
-                o.w = fmaf(p, v.w, o.w);
+#pragma unroll
+                for (int v = 0; v < VPL; v++) {
+                    const float4 x = ok ? vr[j][v] : make_float4(0.f, 0.f, 0.f, 0.f);
+                    o[v].x = fmaf(p, x.x, o[v].x);
+                    o[v].y = fmaf(p, x.y, o[v].y);
+                    o[v].z = fmaf(p, x.z, o[v].z);
+                    o[v].w = fmaf(p, x.w, o[v].w);
+                }
             }
             m_run[h] = m_new;
             l_run[h] = l;
-            o_acc[h] = o;
+#pragma unroll
+            for (int v = 0; v < VPL; v++) o_acc[h][v] = o[v];
         }
         if (more) {
             if constexpr (PREFETCH) {
 #pragma unroll
-                for (int j = 0; j < J; j++) {
-                    kr[j] = kn[j];
-                    vr[j] = vn[j];
-                }
+                for (int j = 0; j < J; j++)
+#pragma unroll
+                    for (int v = 0; v < VPL; v++) {
+                        kr[j][v] = kn[j][v];
+                        vr[j][v] = vn[j][v];
+                    }
             } else {
                 // load the next chunk after this one is consumed (fewer registers)
-#pragma unroll
-                for (int j = 0; j < J; j++) {
-                    const int p = min(c0 + c_step + team + j * NTEAM, last);
-                    kr[j] = *reinterpret_cast<const float4 *>(kbase + (size_t)p * kvd);
-                    vr[j] = *reinterpret_cast<const float4 *>(vbase + (size_t)p * kvd);
-                }
+                load_kv(kr, vr, c0 + c_step, last);
             }
         }
     }
@@ -197,7 +209,8 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
     // merge the NTEAM team states
 #pragma unroll
     for (int h = 0; h < GROUP; h++) {
-        *reinterpret_cast<float4 *>(&sm.o[team][h][lt * 4]) = o_acc[h];
+#pragma unroll
+        for (int v = 0; v < VPL; v++) *reinterpret_cast<float4 *>(&sm.o[team][h][(v * TS + lt) * 4]) = o_acc[h][v];
         if (lt == 0) {
             sm.m[team][h] = m_run[h];
             sm.l[team][h] = l_run[h];
