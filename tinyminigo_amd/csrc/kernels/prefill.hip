@@ -184,96 +184,14 @@ __global__ __launch_bounds__(kBlock) void gemm_kernel(const GemmArgs a) {
     gemm_store<EPI>(a, mb, n, v);
 }
 
-// Tiled MFMA GEMM for long prompts: workgroup tile 128 weight rows x 128
-// tokens, K in steps of 64 staged through LDS (W, Bhi, Blo; rows padded to
-// 72 bf16 against bank conflicts).  The four wavefronts each own a 64 x 64
-// quarter (4 x 4 MFMA fragments).  The next K step's global loads are held
-// in registers while the current one is multiplied.
-constexpr int kTM = 128, kTN = 128, kTK = 64, kTKP = kTK + 8;
+// Tiled MFMA GEMM for prompts of at least kTiledMinTokens tokens: workgroup
+// tile 128 weight rows x 128 tokens, K in steps of 64; each of the four
+// wavefronts owns a 64 x 64 quarter (4 x 4 MFMA fragments).
+constexpr int kTM = 128, kTN = 128, kTK = 64;
 
-template <int EPI>
-__global__ __launch_bounds__(kBlock) void gemm_tiled_kernel(const GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t sA[kTM][kTKP];
-    __shared__ __attribute__((aligned(16))) uint16_t sH[kTN][kTKP];
-    __shared__ __attribute__((aligned(16))) uint16_t sL[kTN][kTKP];
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-    const int wm = wave & 1, wn = wave >> 1;
-    const int m0 = blockIdx.x * kTM, n0 = blockIdx.y * kTN;
-    const int K = a.K;
-    // global -> register staging: chunk c = t + 256 i (i < 4) is row c >> 3,
-    // 16-byte column c & 7 of each 128 x 64 tile
-    const uint16_t *gA[4], *gH[4], *gL[4];
-    int srow[4], scol[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int c = t + kBlock * i;
-        srow[i] = c >> 3;
-        scol[i] = (c & 7) * 8;
-        const int m = min(m0 + srow[i], a.M - 1), n = min(n0 + srow[i], a.N - 1);
-        gA[i] = a.W + (size_t)m * K + scol[i];
-        gH[i] = a.Bhi + (size_t)n * K + scol[i];
-        gL[i] = a.Blo + (size_t)n * K + scol[i];
-    }
-    u32x4 rA[4], rH[4], rL[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        rA[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gA[i]));
-        rH[i] = *reinterpret_cast<const u32x4 *>(gH[i]);
-        rL[i] = *reinterpret_cast<const u32x4 *>(gL[i]);
-    }
-    f32x4 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int r = lane & 15, kq = (lane >> 4) * 8;
-    for (int k0 = 0; k0 < K; k0 += kTK) {
-        __syncthreads();  // the previous step's fragments are read
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            *reinterpret_cast<u32x4 *>(&sA[srow[i]][scol[i]]) = rA[i];
-            *reinterpret_cast<u32x4 *>(&sH[srow[i]][scol[i]]) = rH[i];
-            *reinterpret_cast<u32x4 *>(&sL[srow[i]][scol[i]]) = rL[i];
-        }
-        __syncthreads();
-        if (k0 + kTK < K) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                rA[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gA[i] + k0 + kTK));
-                rH[i] = *reinterpret_cast<const u32x4 *>(gH[i] + k0 + kTK);
-                rL[i] = *reinterpret_cast<const u32x4 *>(gL[i] + k0 + kTK);
-            }
-        }
-#pragma unroll
-        for (int kk = 0; kk < kTK; kk += 32) {
-            bf16x8 fa[4], fh[4], fl[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                fa[i] = *reinterpret_cast<const bf16x8 *>(&sA[wm * 64 + i * 16 + r][kk + kq]);
-                fh[i] = *reinterpret_cast<const bf16x8 *>(&sH[wn * 64 + i * 16 + r][kk + kq]);
-                fl[i] = *reinterpret_cast<const bf16x8 *>(&sL[wn * 64 + i * 16 + r][kk + kq]);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fh[j], acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fl[j], acc[i][j], 0, 0, 0);
-                }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            gemm_store<EPI>(a, m0 + wm * 64 + i * 16 + (lane >> 4) * 4, n0 + wn * 64 + j * 16 + r, acc[i][j]);
-}
-
-// Tiled MFMA GEMM, LDS-DMA version: the same 128 x 128 workgroup tile and
-// 64 x 64 wavefront quarters, but the W / Bhi / Blo tiles go global -> LDS
-// directly (global_load_lds_dwordx4, no register staging) through a 3-stage
-// ring, so step s + 2 is in flight while step s is multiplied and each step
-// needs one barrier.  LDS rows are unpadded 128 B with the 16-byte chunks
+// The W / Bhi / Blo tiles go global -> LDS directly (global_load_lds_dwordx4,
+// no register staging) through a 3-stage ring, so step s + 2 is in flight
+// while step s is multiplied and each step needs one barrier.  LDS rows are unpadded 128 B with the 16-byte chunks
 // XOR-swizzled by (row & 7) against bank conflicts: a DMA wave-instruction
 // fills 1 KB = 8 rows contiguously, so each lane fetches the global chunk that
 // belongs at its LDS slot.
