@@ -198,21 +198,29 @@ constexpr int kTM = 128, kTN = 128, kTK = 64;
 constexpr int kGStages = 3;
 constexpr int kGTile = kTM * kTK * 2;  // bytes of one 128 x 64 bf16 tile
 
+// NW = 8 wavefronts (two per SIMD, so one's MFMAs overlap the other's LDS
+// reads): wave w owns rows 64 (w & 1) .. +63 and tokens 32 (w >> 1) .. +31
+// (4 x 2 MFMA fragments) and issues two of each tile's 16 DMA instructions.
+constexpr int kGWaves = 8;
+
 template <int EPI>
-__global__ __launch_bounds__(kBlock) void gemm_dma_kernel(const GemmArgs a) {
+__global__ __launch_bounds__(kGWaves * 64) void gemm_dma_kernel(const GemmArgs a) {
+    constexpr int DPW = 16 / kGWaves;  // DMA instructions per wave per tile
+    constexpr int NJ = kTN / 16 / (kGWaves / 2);  // token fragments per wave
+    static_assert(3 * DPW <= 15, "vmcnt immediate");
     __shared__ __attribute__((aligned(1024))) unsigned char smem[kGStages * 3 * kGTile];
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int wm = wave & 1, wn = wave >> 1;
     const int m0 = blockIdx.x * kTM, n0 = blockIdx.y * kTN;
     const int K = a.K;
     const int nsteps = K / kTK;
-    // DMA: wave w's instruction i fills rows (4 w + i) * 8 .. +7 of a tile;
-    // lane l writes row (4 w + i) * 8 + (l >> 3), physical chunk l & 7, which
+    // DMA: wave w's instruction i fills rows (DPW w + i) * 8 .. +7 of a tile;
+    // lane l writes row (DPW w + i) * 8 + (l >> 3), physical chunk l & 7, which
     // holds logical chunk (l & 7) ^ (row & 7)
-    uint32_t off[3][4];
+    uint32_t off[3][DPW];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int row = (wave * 4 + i) * 8 + (lane >> 3);
+    for (int i = 0; i < DPW; i++) {
+        const int row = (wave * DPW + i) * 8 + (lane >> 3);
         const int lc = (lane & 7) ^ (row & 7);
         off[0][i] = (uint32_t)min(m0 + row, a.M - 1) * (uint32_t)K + lc * 8;
         off[1][i] = (uint32_t)min(n0 + row, a.N - 1) * (uint32_t)K + lc * 8;
@@ -223,24 +231,24 @@ __global__ __launch_bounds__(kBlock) void gemm_dma_kernel(const GemmArgs a) {
         for (int x = 0; x < 3; x++) {
             const uint16_t *base = x == 0 ? a.W : (x == 1 ? a.Bhi : a.Blo);
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < DPW; i++)
                 __builtin_amdgcn_global_load_lds(base + off[x][i] + k0,
-                                                 smem + (stage * 3 + x) * kGTile + (wave * 4 + i) * 1024, 16, 0, 0);
+                                                 smem + (stage * 3 + x) * kGTile + (wave * DPW + i) * 1024, 16, 0, 0);
         }
     };
     issue(0, 0);
     if (nsteps > 1) issue(1, kTK);
-    f32x4 acc[4][4];
+    f32x4 acc[4][NJ];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < NJ; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int r = lane & 15, q4 = lane >> 4;
     for (int st = 0; st < nsteps; st++) {
-        // this step's 12 DMAs are complete once at most the next step's 12
-        // are outstanding (vector memory counts complete in issue order)
+        // this step's 3 DPW DMAs are complete once at most the next step's are
+        // outstanding (vector memory counts complete in issue order)
         if (st + 1 < nsteps)
-            __builtin_amdgcn_s_waitcnt(0xF7C);  // vmcnt(12)
+            __builtin_amdgcn_s_waitcnt(0xF70 | (3 * DPW));  // vmcnt(3 DPW)
         else
             __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
         __builtin_amdgcn_s_barrier();  // every wave's DMAs for this step landed; step - 1's reads are done
@@ -250,31 +258,35 @@ __global__ __launch_bounds__(kBlock) void gemm_dma_kernel(const GemmArgs a) {
 #pragma unroll
         for (int kk = 0; kk < kTK; kk += 32) {
             const int lc = kk / 8 + q4;
-            bf16x8 fa[4], fh[4], fl[4];
+            bf16x8 fa[4], fh[NJ], fl[NJ];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int ra = wm * 64 + i * 16 + r, rb = wn * 64 + i * 16 + r;
+                const int ra = wm * 64 + i * 16 + r;
                 fa[i] = *reinterpret_cast<const bf16x8 *>(sa + ra * 128 + ((lc ^ (ra & 7)) * 16));
-                fh[i] = *reinterpret_cast<const bf16x8 *>(sh + rb * 128 + ((lc ^ (rb & 7)) * 16));
-                fl[i] = *reinterpret_cast<const bf16x8 *>(sl + rb * 128 + ((lc ^ (rb & 7)) * 16));
+            }
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const int rb = wn * NJ * 16 + j * 16 + r;
+                fh[j] = *reinterpret_cast<const bf16x8 *>(sh + rb * 128 + ((lc ^ (rb & 7)) * 16));
+                fl[j] = *reinterpret_cast<const bf16x8 *>(sl + rb * 128 + ((lc ^ (rb & 7)) * 16));
             }
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++)
+                for (int j = 0; j < NJ; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fh[j], acc[i][j], 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++)
+                for (int j = 0; j < NJ; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fl[j], acc[i][j], 0, 0, 0);
         }
     }
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            gemm_store<EPI>(a, m0 + wm * 64 + i * 16 + q4 * 4, n0 + wn * 64 + j * 16 + r, acc[i][j]);
+        for (int j = 0; j < NJ; j++)
+            gemm_store<EPI>(a, m0 + wm * 64 + i * 16 + q4 * 4, n0 + wn * NJ * 16 + j * 16 + r, acc[i][j]);
 }
 
 // Split-K MFMA GEMM for short prompts (fewer than kTiledMinTokens tokens).
@@ -464,10 +476,10 @@ hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
     if (a.N >= kTiledMinTokens && a.K % kTK == 0) {
         const dim3 grid((a.M + kTM - 1) / kTM, (a.N + kTN - 1) / kTN);
         switch (epi) {
-            case GEPI_STORE: hipLaunchKernelGGL(gemm_dma_kernel<GEPI_STORE>, grid, dim3(kBlock), 0, s, a); break;
-            case GEPI_RESID: hipLaunchKernelGGL(gemm_dma_kernel<GEPI_RESID>, grid, dim3(kBlock), 0, s, a); break;
-            case GEPI_SWIGLU: hipLaunchKernelGGL(gemm_dma_kernel<GEPI_SWIGLU>, grid, dim3(kBlock), 0, s, a); break;
-            case GEPI_QKV: hipLaunchKernelGGL(gemm_dma_kernel<GEPI_QKV>, grid, dim3(kBlock), 0, s, a); break;
+            case GEPI_STORE: hipLaunchKernelGGL(gemm_dma_kernel<GEPI_STORE>, grid, dim3(kGWaves * 64), 0, s, a); break;
+            case GEPI_RESID: hipLaunchKernelGGL(gemm_dma_kernel<GEPI_RESID>, grid, dim3(kGWaves * 64), 0, s, a); break;
+            case GEPI_SWIGLU: hipLaunchKernelGGL(gemm_dma_kernel<GEPI_SWIGLU>, grid, dim3(kGWaves * 64), 0, s, a); break;
+            case GEPI_QKV: hipLaunchKernelGGL(gemm_dma_kernel<GEPI_QKV>, grid, dim3(kGWaves * 64), 0, s, a); break;
             default: return hipErrorInvalidValue;
         }
         return hipGetLastError();
