@@ -36,7 +36,10 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPHD = 128;        // head dim
 constexpr int kPKB = 64;         // keys per block
-constexpr int kPCols = 128;      // query columns per workgroup (32 per wavefront)
+constexpr int kPCols = 128;      // query columns per workgroup
+constexpr int kPWaves = 8;       // wavefronts per workgroup (two per SIMD)
+constexpr int kPQT = kPCols / (16 * kPWaves);  // 16-column query tiles per wavefront
+constexpr int kPCopies = kPKB * kPHD / 8 / (kPWaves * 64);  // 16-byte staging copies per thread per K (or V) half
 constexpr int kSKP = kPHD + 8;   // sK row pitch, bf16
 constexpr int kSVP = kPKB + 8;   // sV row pitch, bf16
 
@@ -119,8 +122,9 @@ __global__ __launch_bounds__(kBlock) void kv_split_kernel(const KVSplitArgs a) {
 }
 
 template <int GROUP>
-__global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(kPWaves * 64) void attn_prefill_kernel(const AttnArgs a) {
     constexpr int QB = kPCols / GROUP;  // query positions per workgroup
+    constexpr int NT = kPWaves * 64;    // threads
     __shared__ __attribute__((aligned(16))) uint16_t sK[2][kPKB][kSKP];  // [hi/lo][key][dim]
     __shared__ __attribute__((aligned(16))) uint16_t sV[2][kPHD][kSVP];  // [hi/lo][dim][key]
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
@@ -131,10 +135,10 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
     const int kvd = a.nkv * kPHD, qd = a.nq * kPHD;
 
     // this lane's query column in each of its two 16-column tiles
-    int ti[2], qpos[2], qhead[2];
+    int ti[kPQT], qpos[kPQT], qhead[kPQT];
 #pragma unroll
-    for (int qt = 0; qt < 2; qt++) {
-        const int c = wave * 32 + qt * 16 + r;
+    for (int qt = 0; qt < kPQT; qt++) {
+        const int c = wave * kPQT * 16 + qt * 16 + r;
         const int hh = c / QB, p = c - hh * QB;
         ti[qt] = qb * QB + p;
         qpos[qt] = a.start + ti[qt];
@@ -143,18 +147,18 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
     const int last_pos = a.start + min(a.T, (qb + 1) * QB) - 1;  // the workgroup's last query position
     const int nkb = last_pos / kPKB + 1;
 
-    // staging map: copy c = t + 256 i (i < 4) of a block is K row c >> 4,
+    // staging map: copy c = t + NT i (i < kPCopies) of a block is K row c >> 4,
     // 16-byte column c & 15, and V^T row c >> 3, 16-byte column c & 7
     const uint16_t *gk[2], *gv[2];
     gk[0] = a.kh + g * kPHD;
     gk[1] = a.kl + g * kPHD;
     gv[0] = a.vth + (size_t)g * kPHD * a.vt_pitch;
     gv[1] = a.vtl + (size_t)g * kPHD * a.vt_pitch;
-    u32x4 rk[2][4], rv[2][4];
+    u32x4 rk[2][kPCopies], rv[2][kPCopies];
     auto fetch = [&](int k0) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = t + kBlock * i;
+        for (int i = 0; i < kPCopies; i++) {
+            const int c = t + NT * i;
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 rk[h][i] = *reinterpret_cast<const u32x4 *>(gk[h] + (size_t)(k0 + (c >> 4)) * kvd + (c & 15) * 8);
@@ -165,9 +169,9 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
     fetch(0);
 
     // Q^T fragments (MFMA B operand): dims 32 ds + 8 q4 .. +7 of the column
-    bf16x8 qh[2][4], ql[2][4];
+    bf16x8 qh[kPQT][4], ql[kPQT][4];
 #pragma unroll
-    for (int qt = 0; qt < 2; qt++) {
+    for (int qt = 0; qt < kPQT; qt++) {
         const float *src = a.q + (size_t)min(ti[qt], a.T - 1) * qd + qhead[qt] * kPHD + 8 * q4;
 #pragma unroll
         for (int ds = 0; ds < 4; ds++) {
@@ -178,19 +182,22 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
         }
     }
     const float sl2 = a.scale * 1.4426950408889634f;  // scores in log2 units
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
-    f32x4 o[2][8];
+    float m[kPQT], l[kPQT];
+    f32x4 o[kPQT][8];
 #pragma unroll
-    for (int qt = 0; qt < 2; qt++)
+    for (int qt = 0; qt < kPQT; qt++) {
+        m[qt] = -INFINITY;
+        l[qt] = 0.0f;
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) o[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 
     for (int kb = 0; kb < nkb; kb++) {
         const int k0 = kb * kPKB;
         __syncthreads();  // the previous block's fragments are read
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = t + kBlock * i;
+        for (int i = 0; i < kPCopies; i++) {
+            const int c = t + NT * i;
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 *reinterpret_cast<u32x4 *>(&sK[h][c >> 4][(c & 15) * 8]) = rk[h][i];
@@ -201,11 +208,11 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
         if (kb + 1 < nkb) fetch(k0 + kPKB);  // in flight during this block's MFMAs
 
         // S^T = K Q^T: 4 key tiles x 2 query tiles
-        f32x4 s[4][2];
+        f32x4 s[4][kPQT];
 #pragma unroll
         for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-            for (int qt = 0; qt < 2; qt++) s[kt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int qt = 0; qt < kPQT; qt++) s[kt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ds = 0; ds < 4; ds++) {
 #pragma unroll
@@ -213,7 +220,7 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
                 const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(&sK[0][kt * 16 + r][32 * ds + 8 * q4]);
                 const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(&sK[1][kt * 16 + r][32 * ds + 8 * q4]);
 #pragma unroll
-                for (int qt = 0; qt < 2; qt++) {
+                for (int qt = 0; qt < kPQT; qt++) {
                     s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[qt][ds], s[kt][qt], 0, 0, 0);
                     s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[qt][ds], s[kt][qt], 0, 0, 0);
                     s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[qt][ds], s[kt][qt], 0, 0, 0);
@@ -222,7 +229,7 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
         }
         // online softmax per query column; this lane holds keys k0 + 16 kt + 4 q4 + i
 #pragma unroll
-        for (int qt = 0; qt < 2; qt++) {
+        for (int qt = 0; qt < kPQT; qt++) {
             float mx = -INFINITY;
 #pragma unroll
             for (int kt = 0; kt < 4; kt++)
@@ -252,9 +259,9 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
         // O^T += V^T P^T, 32 keys per step: tiles 2 ks and 2 ks + 1
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
-            bf16x8 ph[2], pl[2];
+            bf16x8 ph[kPQT], pl[kPQT];
 #pragma unroll
-            for (int qt = 0; qt < 2; qt++) {
+            for (int qt = 0; qt < kPQT; qt++) {
                 const float pv[8] = {s[2 * ks][qt][0],     s[2 * ks][qt][1],     s[2 * ks][qt][2],
                                      s[2 * ks][qt][3],     s[2 * ks + 1][qt][0], s[2 * ks + 1][qt][1],
                                      s[2 * ks + 1][qt][2], s[2 * ks + 1][qt][3]};
@@ -270,7 +277,7 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
                 const bf16x8 vh = __builtin_bit_cast(bf16x8, u32x4{h0[0], h0[1], h1[0], h1[1]});
                 const bf16x8 vl = __builtin_bit_cast(bf16x8, u32x4{l0[0], l0[1], l1[0], l1[1]});
 #pragma unroll
-                for (int qt = 0; qt < 2; qt++) {
+                for (int qt = 0; qt < kPQT; qt++) {
                     o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[qt], o[qt][dt], 0, 0, 0);
                     o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl[qt], o[qt][dt], 0, 0, 0);
                     o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph[qt], o[qt][dt], 0, 0, 0);
@@ -280,7 +287,7 @@ __global__ __launch_bounds__(kBlock) void attn_prefill_kernel(const AttnArgs a) 
     }
     // normalize and write the split-bf16 output: O^T rows dims 16 dt + 4 q4 + i
 #pragma unroll
-    for (int qt = 0; qt < 2; qt++) {
+    for (int qt = 0; qt < kPQT; qt++) {
         const float L = add_xor32(add_xor16(l[qt]));  // the column's four lane groups
         if (ti[qt] >= a.T) continue;
         const float inv = 1.0f / L;
@@ -320,10 +327,10 @@ hipError_t launch_attn_prefill(const AttnArgs &a, hipStream_t s) {
     const int QB = kPCols / group;
     const dim3 grid((a.T + QB - 1) / QB, a.nkv);
     switch (group) {
-        case 1: hipLaunchKernelGGL(attn_prefill_kernel<1>, grid, dim3(kBlock), 0, s, a); break;
-        case 2: hipLaunchKernelGGL(attn_prefill_kernel<2>, grid, dim3(kBlock), 0, s, a); break;
-        case 4: hipLaunchKernelGGL(attn_prefill_kernel<4>, grid, dim3(kBlock), 0, s, a); break;
-        case 8: hipLaunchKernelGGL(attn_prefill_kernel<8>, grid, dim3(kBlock), 0, s, a); break;
+        case 1: hipLaunchKernelGGL(attn_prefill_kernel<1>, grid, dim3(kPWaves * 64), 0, s, a); break;
+        case 2: hipLaunchKernelGGL(attn_prefill_kernel<2>, grid, dim3(kPWaves * 64), 0, s, a); break;
+        case 4: hipLaunchKernelGGL(attn_prefill_kernel<4>, grid, dim3(kPWaves * 64), 0, s, a); break;
+        case 8: hipLaunchKernelGGL(attn_prefill_kernel<8>, grid, dim3(kPWaves * 64), 0, s, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
