@@ -370,6 +370,23 @@ def test_tiled_gemm_prefill_tiny(T, O, untied):
         assert np.abs(gc.values_flat(layer) - oc.values_flat(layer)).max() < 1e-4
 
 
+def test_prefill_k_not_multiple_of_64(T, O, W):
+    # hidden 96 and intermediate 160: every projection's K is a multiple of 32
+    # but not of 64, so prefill takes the 16x64 streaming MFMA kernel (40 and
+    # 300 tokens), decode the masked GEMV tail
+    import dataclasses
+    wl = dataclasses.replace(W.TINY, name="tiny-llama-h96-kv3-i160-s13", hidden_size=96, num_attention_heads=6,
+                             num_key_value_heads=3, intermediate_size=160, weight_seed=13)
+    p = W.ensure_model(wl, model_root())
+    g, o = T.Model.load(p), O.OracleModel.load(p)
+    ids = [int(t) for t in T.synth_tokens(61, 346, wl.vocab_size)]
+    for n in (40, 300):
+        gc, oc = T.KvCache(g, 360), o.new_cache()
+        close_logits(g.forward_seq(ids[:n], gc), o.forward_seq(ids[:n], oc), f"prefill {n}")
+        for i in range(n, n + 6):
+            close_logits(g.forward_token(ids[i], gc), o.forward_token(ids[i], oc), f"decode at {i}")
+
+
 def test_long_prefill_chunks_vs_oracle(T, O, W, one_b):
     # 1B model: a 700-token prefill, a second 333-token chunk starting at 700
     # (MFMA attention with start > 0, partial query blocks), then decode steps
