@@ -228,7 +228,7 @@ hipError_t launch_attn_combine(const AttnArgs &a, hipStream_t s) {
 
 int gemv_blocks(int out, int in) {
     const int kc = (in + kChunk - 1) / kChunk;
-    const int R = kc <= 2 ? 8 : 4;  // gemv_rows<KC>()
+    const int R = kc <= 3 ? 8 : 4;  // gemv_rows<KC>()
     return (out + R - 1) / R;
 }
 

@@ -27,7 +27,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 template <int KC>
 __host__ __device__ constexpr int gemv_rows() {
-    return KC <= 2 ? 8 : 4;
+    return KC <= 3 ? 8 : 4;
 }
 
 template <int KC, int R>
