@@ -46,16 +46,17 @@ def cpu_model():
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(path, prompt, seconds, long_wl=None, gpu_model=None, gpu_cache=None, sampled=None):
+def cpu_baseline(path, prompt, seconds, long_wl=None, gpu_model=None, gpu_cache=None, sampled=None, i8=False):
     """The oracle (the C restatement of the reference CPU path) decoding the
     same model on this host's cores: a prefill of the prompt, then decode
     steps until about `seconds` have passed (at most 256).  For the 8k
     workload the 8192-token CPU prefill (about ten minutes of single-threaded
     attention) is replaced by the device's KV cache copied into the oracle's,
     so the timed steps are CPU decode steps at that context.  With `sampled`
-    each step applies the penalty and the reference's sampler."""
+    each step applies the penalty and the reference's sampler; with `i8` the
+    oracle runs the reference's int8 weight-only path (TMG_I8=1)."""
     from oracle import oracle as O
-    m = O.OracleModel.load(path)
+    m = O.OracleModel.load(path, i8=i8)
     cache = m.new_cache()
     if long_wl is not None:
         n0 = gpu_cache.total_len()
@@ -92,7 +93,8 @@ def cpu_baseline(path, prompt, seconds, long_wl=None, gpu_model=None, gpu_cache=
     mode = "sampled (penalty + top-k/top-p sampler)" if sampled else "greedy"
     return {
         "value": round(n / el, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-        "sample": (f"oracle (C restatement of the reference CPU path, GEMV on max(1,ncores/4)={threads} threads of "
+        "sample": (f"oracle (C restatement of the reference CPU path{', int8 weights' if i8 else ''}, GEMV on "
+                   f"max(1,ncores/4)={threads} threads of "
                    f"{os.cpu_count()} on '{cpu_model()}', AVX2={bool(O.lib.om_uses_avx2())}): {n} {mode} decode "
                    f"steps {what}"),
         "prefill_tok_s": round(len(prompt) / prefill_s, 2) if prefill_s else None,
@@ -183,6 +185,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true", help="skip the GEMV shape sweep")
+    ap.add_argument("--weights", choices=["bf16", "i8"], default="bf16",
+                    help="i8: load with TMG_I8=1, the reference's int8 weight-only mode (per-row int8 q/k/v/o/"
+                         "gate/up/down, BF16 lm_head); the CPU baseline then times the oracle's int8 path")
     ap.add_argument("--model-dir", default=os.environ.get("TMG_MODEL_DIR",
                                                            os.path.join(tempfile.gettempdir(), "tmg_models")))
     args = ap.parse_args()
@@ -208,8 +213,13 @@ def main():
     K = args.steps if args.steps is not None else wl.gen_tokens
     Wm = args.warmup
     P = wl.prompt_len
+    i8 = args.weights == "i8"
+    if i8:
+        os.environ["TMG_I8"] = "1"  # read by tmg_model_load, as the reference reads it at load
+    else:
+        os.environ.pop("TMG_I8", None)
     m = T.Model.load(path)
-    log("model loaded")
+    log(f"model loaded ({args.weights} weights)")
 
     # prefill tok/s: median over repetitions on fresh caches (one for 8k)
     pf = []
@@ -262,7 +272,7 @@ def main():
         log(f"decode {K} steps: {wall * 1e3:.1f} ms wall, {ev_ms:.1f} ms events -> {K / wall:.1f} tok/s")
     ms_per_step = wall * 1e3 / K_timed
     n_ctx_avg = P + (K + 1) / 2.0
-    step_bytes = wl.decode_bytes(int(round(n_ctx_avg)))
+    step_bytes = wl.decode_bytes(int(round(n_ctx_avg)), i8)
 
     # per-kernel timing: each kernel kind's launches of one step replayed back
     # to back from a graph between HIP events on the library's stream
@@ -281,16 +291,16 @@ def main():
     kernels = {k: {"launches": n, "avg_us": round(ms * 1e3, 2),
                    "GB_s": round(b / (ms * 1e-3) / 1e9, 1) if b else None,
                    "share": round(n * ms / step_kern_ms, 3)} for k, (n, b, ms) in per.items()}
-    traffic = pmc_traffic(name) if args.workload == "1b" else None
+    traffic = pmc_traffic(name) if (args.workload == "1b" and not i8) else None
 
-    sweep = None if (args.no_sweep or args.workload != "1b") else gemv_sweep(T)
+    sweep = None if (args.no_sweep or args.workload != "1b" or i8) else gemv_sweep(T)
 
     cpu = None
     if not args.no_cpu:
         log("timing the CPU baseline")
         cpu = cpu_baseline(path, prompt, args.cpu_seconds, wl if args.workload == "8k" else None,
                            m if args.workload == "8k" else None, cache if args.workload == "8k" else None,
-                           SAMPLED if sampled else None)
+                           SAMPLED if sampled else None, i8)
 
     kind = (f"{K} sampled tokens (T=0.8, top-k 50, top-p 0.9, penalty 1.1, seed 42) through generate"
             if sampled else f"{K} greedy decode steps")
@@ -305,7 +315,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "i8" if i8 else "bf16",
         "data": "synthetic",
         "config": {
             "workload": f"{wl.name}: {P}-token prompt, batched prefill, {kind}",
@@ -313,7 +323,9 @@ def main():
             "layers": wl.num_hidden_layers, "heads": wl.num_attention_heads, "kv_heads": wl.num_key_value_heads,
             "head_dim": wl.head_dim, "intermediate": wl.intermediate_size, "vocab": wl.vocab_size,
             "global_batch": 1, "seq_len": P + K, "parallelism": "none (1 GPU)",
-            "arith": "BF16 weights, f32 activations/accumulation, f32 KV cache",
+            "arith": ("int8 layer weights with f32 row scales (TMG_I8=1), activations quantized per GEMV to int8, "
+                      "exact int32 dots; BF16 lm_head; f32 KV cache" if i8 else
+                      "BF16 weights, f32 activations/accumulation, f32 KV cache"),
         },
         "prefill_tok_s": round(P / prefill_s, 1),
         "prefill_ms": round(prefill_s * 1e3, 3),

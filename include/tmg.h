@@ -82,7 +82,12 @@ int tmg_config_load(const char *config_json_path, tmg_config *out);
  * src/model.rs:181-244): config.json must sit next to the .safetensors file
  * (src/config.rs:174-184).  Weight matrices must be BF16; they are uploaded
  * raw to HBM on `device`.  Norm weights and the embedding may be BF16, F16 or
- * F32 (converted as in src/safetensors_loader.rs:103-147). */
+ * F32 (converted as in src/safetensors_loader.rs:103-147).  With TMG_I8=1 in
+ * the environment (the reference's gate, src/model.rs:57-76) the q, k, v, o,
+ * gate, up and down projections are quantized to per-row int8 at load
+ * (tmg_quantize_i8): decode steps stream the int8 rows (tmg_gemv_i8's
+ * arithmetic), prefill multiplies by the same codes, dequantized, in f32
+ * (src/tensor.rs:795-858); lm_head stays BF16. */
 int tmg_model_load(const char *safetensors_path, int device, tmg_model **out);
 void tmg_model_free(tmg_model *model);
 int tmg_model_config(const tmg_model *model, tmg_config *out);
@@ -127,6 +132,27 @@ int tmg_generate(tmg_model *model, const uint32_t *prompt, size_t n_prompt, cons
  * default stream).  in must be a multiple of 8 and W 16-byte aligned. */
 int tmg_gemv_bf16(const uint16_t *w_dev, const float *x_dev, float *y_dev, uint32_t out, uint32_t in,
                   void *stream);
+
+/* Kernel level, int8 weight-only mode (TMG_I8=1): y[out] = the reference's
+ * matmul_w_into over WMat::I8 (src/tensor.rs:341-364): x is quantized with
+ * one symmetric scale (quantize_row_i8, src/tensor.rs:125-139), each row dot
+ * is exact in int32 (dot_i8, src/tensor.rs:144-170) and
+ * y[o] = (dot as f32) * xs * scale[o].  q [out, in] int8 codes, scale [out]
+ * f32, x [in] f32, y [out] f32, all DEVICE pointers.  in must be a multiple
+ * of 8 and <= 16384; q 8-byte, x 16-byte aligned. */
+int tmg_gemv_i8(const int8_t *q_dev, const float *scale_dev, const float *x_dev, float *y_dev, uint32_t out,
+                uint32_t in, void *stream);
+
+/* WMat::quantize_i8 (src/tensor.rs:275-293) of BF16 rows widened to f32, as
+ * wmat_maybe_i8 loads them (src/model.rs:60-68): scale[r] = max|w|/127 (1.0
+ * for a zero row), q = round(w/scale) (halves away from zero) clamped to
+ * [-127, 127].  w [rows, in] BF16 (read only), q [rows, in], scale [rows],
+ * DEVICE pointers; in a multiple of 8; w 16-byte, q 8-byte aligned.  Models
+ * loaded with TMG_I8=1 in the environment quantize their q/k/v/o/gate/up/
+ * down projections this way; lm_head, norms and the embedding stay as they
+ * are (src/model.rs:227-233). */
+int tmg_quantize_i8(const uint16_t *w_dev, uint32_t rows, uint32_t in, int8_t *q_dev, float *scale_dev,
+                    void *stream);
 
 /* ---------------------------------------------------------------------- */
 /* Measurement entry points.  No counterpart in the reference: they expose  */

@@ -37,6 +37,7 @@ def _load_lib():
         build()
     lib = C.CDLL(LIB_PATH)
     F, PF, PU16, PU32, S = C.c_float, C.POINTER(C.c_float), C.POINTER(C.c_uint16), C.POINTER(C.c_uint32), C.c_size_t
+    PI8 = C.POINTER(C.c_int8)
     sig = {
         "om_set_num_threads": (None, [C.c_int]),
         "om_set_attn_threads": (None, [C.c_int]),
@@ -68,6 +69,11 @@ def _load_lib():
         "om_cache_push": (None, [C.c_void_p, C.c_int, PF, PF]),
         "om_forward_token": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, PF]),
         "om_forward_seq": (C.c_int, [C.c_void_p, C.c_void_p, PU32, S, PF]),
+        "om_quantize_i8": (None, [PF, S, S, PI8, PF]),
+        "om_quantize_row_i8": (F, [PF, S, PI8]),
+        "om_dot_i8": (C.c_int32, [PI8, PI8, S]),
+        "om_matmul_w_i8": (None, [PF, PI8, PF, S, S, PF]),
+        "om_matmul_batch_w_i8": (None, [PF, PI8, PF, S, S, S, PF]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -92,6 +98,11 @@ def u16p(a: np.ndarray):
 def u32p(a: np.ndarray):
     assert a.dtype == np.uint32 and a.flags.c_contiguous
     return a.ctypes.data_as(C.POINTER(C.c_uint32))
+
+
+def i8p(a: np.ndarray):
+    assert a.dtype == np.int8 and a.flags.c_contiguous
+    return a.ctypes.data_as(C.POINTER(C.c_int8))
 
 
 def f32(a) -> np.ndarray:
@@ -127,6 +138,51 @@ def matmul_batch_w(x, w_bf16: np.ndarray, out: int, inp: int, T: int) -> np.ndar
     x, w = f32(x), np.ascontiguousarray(w_bf16, dtype=np.uint16)
     y = np.empty(T * out, np.float32)
     lib.om_matmul_batch_w(fp(x), u16p(w), out, inp, T, fp(y))
+    return y
+
+
+# int8 weight-only mode (TMG_I8=1; src/tensor.rs:125-170, 275-293, 341-386)
+
+def quantize_i8(w, out: int, inp: int):
+    """WMat::quantize_i8 of an f32 [out, in] matrix -> (int8 rows, f32 scales)."""
+    w = f32(w)
+    assert w.size == out * inp
+    q = np.empty(out * inp, np.int8)
+    s = np.empty(out, np.float32)
+    lib.om_quantize_i8(fp(w), out, inp, i8p(q), fp(s))
+    return q, s
+
+
+def quantize_i8_bf16(w_bf16: np.ndarray, out: int, inp: int):
+    """wmat_maybe_i8 of a BF16 tensor (src/model.rs:60-68): widen, then quantize."""
+    return quantize_i8(bf16_to_f32(np.ascontiguousarray(w_bf16, dtype=np.uint16)), out, inp)
+
+
+def quantize_row_i8(x):
+    """quantize_row_i8 -> (int8 vector, scale)."""
+    x = f32(x)
+    q = np.empty(x.size, np.int8)
+    s = float(lib.om_quantize_row_i8(fp(x), x.size, i8p(q)))
+    return q, s
+
+
+def dot_i8(a, b) -> int:
+    a, b = np.ascontiguousarray(a, dtype=np.int8), np.ascontiguousarray(b, dtype=np.int8)
+    assert a.size == b.size
+    return int(lib.om_dot_i8(i8p(a), i8p(b), a.size))
+
+
+def matmul_w_i8(x, q: np.ndarray, s: np.ndarray, out: int, inp: int) -> np.ndarray:
+    x, q, s = f32(x), np.ascontiguousarray(q, dtype=np.int8), f32(s)
+    y = np.empty(out, np.float32)
+    lib.om_matmul_w_i8(fp(x), i8p(q), fp(s), out, inp, fp(y))
+    return y
+
+
+def matmul_batch_w_i8(x, q: np.ndarray, s: np.ndarray, out: int, inp: int, T: int) -> np.ndarray:
+    x, q, s = f32(x), np.ascontiguousarray(q, dtype=np.int8), f32(s)
+    y = np.empty(T * out, np.float32)
+    lib.om_matmul_batch_w_i8(fp(x), i8p(q), fp(s), out, inp, T, fp(y))
     return y
 
 
@@ -380,6 +436,7 @@ class _Weights(C.Structure):
         ("wo", C.POINTER(C.c_void_p)), ("wg", C.POINTER(C.c_void_p)), ("wu", C.POINTER(C.c_void_p)),
         ("wd", C.POINTER(C.c_void_p)), ("in_norm", C.POINTER(C.c_void_p)), ("post_norm", C.POINTER(C.c_void_p)),
         ("final_norm", C.c_void_p), ("embed", C.c_void_p), ("lm_bf16", C.c_void_p),
+        ("q8", C.POINTER(C.c_void_p) * 7), ("s8", C.POINTER(C.c_void_p) * 7),
     ]
 
 
@@ -439,8 +496,11 @@ class OracleCache:
 class OracleModel:
     """Model (src/model.rs:338-591) over the C restatement."""
 
-    def __init__(self, config: Config, tensors: Dict[str, Tensor]):
+    def __init__(self, config: Config, tensors: Dict[str, Tensor], i8: bool = False):
+        """i8: the TMG_I8=1 load (src/model.rs:57-76): q, k, v, o, gate, up and
+        down quantized per row to int8; lm_head, norms and embedding unchanged."""
         self.config = c = config
+        self.i8 = i8
         H, I, V = c.hidden_size, c.intermediate_size, c.vocab_size
         qd, kvd = c.num_attention_heads * c.head_dim, c.num_key_value_heads * c.head_dim
 
@@ -461,6 +521,11 @@ class OracleModel:
         self._keep.append(embed)
         L = c.num_hidden_layers
         arrs = {k: (C.c_void_p * L)() for k in ("wq", "wk", "wv", "wo", "wg", "wu", "wd", "in_norm", "post_norm")}
+        wkeys = ("wq", "wk", "wv", "wo", "wg", "wu", "wd")
+        q8 = {k: (C.c_void_p * L)() for k in wkeys}
+        s8 = {k: (C.c_void_p * L)() for k in wkeys}
+        shapes = {"wq": (qd, H), "wk": (kvd, H), "wv": (kvd, H), "wo": (H, qd), "wg": (I, H), "wu": (I, H),
+                  "wd": (H, I)}
         for l in range(L):
             p = f"model.layers.{l}."
             spec = [("wq", "self_attn.q_proj.weight", qd * H), ("wk", "self_attn.k_proj.weight", kvd * H),
@@ -471,6 +536,11 @@ class OracleModel:
                 a = np.ascontiguousarray(need(p + name, numel, bf16=True).data)
                 self._keep.append(a)
                 arrs[key][l] = a.ctypes.data
+                if i8:
+                    qa, sa = quantize_i8_bf16(a, *shapes[key])
+                    self._keep += [qa, sa]
+                    q8[key][l] = qa.ctypes.data
+                    s8[key][l] = sa.ctypes.data
             for key, name in (("in_norm", "input_layernorm.weight"), ("post_norm", "post_attention_layernorm.weight")):
                 a = _f32vec(need(p + name, H))
                 self._keep.append(a)
@@ -487,6 +557,11 @@ class OracleModel:
                      c.rope_theta, arrs["wq"], arrs["wk"], arrs["wv"], arrs["wo"], arrs["wg"], arrs["wu"],
                      arrs["wd"], arrs["in_norm"], arrs["post_norm"], fnorm.ctypes.data, embed.ctypes.data,
                      None if lm_arr is None else lm_arr.ctypes.data)
+        if i8:
+            for f, key in enumerate(wkeys):
+                w.q8[f] = C.cast(q8[key], C.POINTER(C.c_void_p))
+                w.s8[f] = C.cast(s8[key], C.POINTER(C.c_void_p))
+            self._keep += [q8, s8]
         self._h = lib.om_model_new(C.byref(w))
 
     def __del__(self):
@@ -495,12 +570,12 @@ class OracleModel:
             self._h = None
 
     @classmethod
-    def load(cls, model_path: str) -> "OracleModel":
+    def load(cls, model_path: str, i8: bool = False) -> "OracleModel":
         """Model::load -> load_model_safetensors (src/model.rs:181-244)."""
         cpath = os.path.join(os.path.dirname(os.path.abspath(model_path)), "config.json")
         if not os.path.exists(cpath):
             raise OracleError(f"config.json not found next to {model_path}")
-        return cls(load_config(cpath), load_safetensors(model_path))
+        return cls(load_config(cpath), load_safetensors(model_path), i8=i8)
 
     def new_cache(self) -> OracleCache:
         c = self.config

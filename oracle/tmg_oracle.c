@@ -295,6 +295,203 @@ OM_API void om_matmul_batch_w(const float *x, const uint16_t *w, size_t out, siz
 }
 
 /* ------------------------------------------------------------------------ */
+/* int8 weight-only mode, TMG_I8=1 (src/model.rs:57-76; src/tensor.rs:125-170, */
+/* 275-293, 341-386, 795-945)                                                */
+/* ------------------------------------------------------------------------ */
+
+/* `v as i8` of a value already clamped to [-127, 127]: Rust's float-to-int
+ * cast maps NaN to 0. */
+static inline int8_t i8_of(float r) {
+    if (r != r) return 0;
+    return (int8_t)fminf(fmaxf(r, -127.0f), 127.0f);
+}
+
+/* WMat::quantize_i8 (src/tensor.rs:275-293): per row, scale = max|w| / 127
+ * (1.0 for an all-zero row) and q = round(w / scale) clamped to [-127, 127].
+ * f32::round rounds half away from zero, as roundf does; the max folds from
+ * 0 with f32::max, which skips NaN like fmaxf. */
+OM_API void om_quantize_i8(const float *w, size_t out, size_t in, int8_t *q, float *s) {
+    for (size_t o = 0; o < out; o++) {
+        const float *row = w + o * in;
+        float maxabs = 0.0f;
+        for (size_t i = 0; i < in; i++) maxabs = fmaxf(fabsf(row[i]), maxabs);
+        const float scale = maxabs > 0.0f ? maxabs / 127.0f : 1.0f;
+        s[o] = scale;
+        for (size_t i = 0; i < in; i++) q[o * in + i] = i8_of(roundf(row[i] / scale));
+    }
+}
+
+/* quantize_row_i8 (src/tensor.rs:125-139): one symmetric scale for the
+ * activation vector; an all-zero vector gives zeros and scale 0.  Returns the
+ * scale. */
+OM_API float om_quantize_row_i8(const float *x, size_t n, int8_t *q) {
+    float maxabs = 0.0f;
+    for (size_t i = 0; i < n; i++) maxabs = fmaxf(fabsf(x[i]), maxabs);
+    if (maxabs == 0.0f) {
+        memset(q, 0, n);
+        return 0.0f;
+    }
+    const float s = maxabs / 127.0f;
+    const float inv = 1.0f / s;
+    for (size_t i = 0; i < n; i++) q[i] = i8_of(roundf(x[i] * inv));
+    return s;
+}
+
+/* dot_i8 (src/tensor.rs:144-170): exact integer dot; the AVX2 kernel's i16
+ * pairwise madd and i32 lane sums only reorder integer additions, which wrap
+ * modulo 2^32 in a release build. */
+OM_API int32_t om_dot_i8(const int8_t *a, const int8_t *b, size_t n) {
+    uint32_t acc = 0;
+    for (size_t i = 0; i < n; i++) acc += (uint32_t)((int32_t)a[i] * (int32_t)b[i]);
+    return (int32_t)acc;
+}
+
+typedef struct {
+    const int8_t *xq, *q;
+    const float *s;
+    float xs, *y;
+    size_t in, start, end;
+} gemv_i8_job;
+
+static void *gemv_i8_worker(void *p) {
+    gemv_i8_job *j = (gemv_i8_job *)p;
+    for (size_t o = j->start; o < j->end; o++)
+        j->y[o] = (float)om_dot_i8(j->xq, j->q + o * j->in, j->in) * j->xs * j->s[o];
+    return NULL;
+}
+
+/* matmul_w_into for WMat::I8 on an AVX2 host (src/tensor.rs:341-374): the
+ * activation is quantized once, then y[o] = (dot as f32) * xs * scale[o],
+ * multiplied left to right, rows split over max(1, ncores/4) threads in
+ * ceil(out/nthreads) chunks (one thread below 64 rows).  (A host without AVX2
+ * takes a dequantizing scalar loop instead, src/tensor.rs:376-385; the
+ * reference's benchmarks and this restatement use the AVX2 path.) */
+OM_API void om_matmul_w_i8(const float *x, const int8_t *q, const float *s, size_t out, size_t in, float *y) {
+    int8_t *xq = (int8_t *)malloc(in ? in : 1);
+    const float xs = om_quantize_row_i8(x, in, xq);
+    size_t nthreads = (size_t)num_threads() / 4;
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > out) nthreads = out;
+    if (nthreads <= 1 || out < 64) {
+        gemv_i8_job j = {xq, q, s, xs, y, in, 0, out};
+        gemv_i8_worker(&j);
+    } else {
+        size_t chunk = (out + nthreads - 1) / nthreads;
+        pthread_t th[256];
+        gemv_i8_job jobs[256];
+        size_t nt = 0;
+        for (size_t st = 0; st < out && nt < 256; st += chunk, nt++) {
+            jobs[nt] = (gemv_i8_job){xq, q, s, xs, y, in, st, st + chunk < out ? st + chunk : out};
+            pthread_create(&th[nt], NULL, gemv_i8_worker, &jobs[nt]);
+        }
+        for (size_t i = 0; i < nt; i++) pthread_join(th[i], NULL);
+    }
+    free(xq);
+}
+
+/* Dequantizing dot of the scalar paths (dot_w_row_avx2's I8 arm,
+ * src/tensor.rs:876-883, and the T == 1 loop, src/tensor.rs:622-633):
+ * acc += x * (q as f32) in sequence, no FMA; then acc * scale. */
+static float dot_deq_i8(const float *x, const int8_t *q, float scale, size_t in) {
+    float acc = 0.0f;
+    for (size_t k = 0; k < in; k++) acc += x[k] * (float)q[k];
+    return acc * scale;
+}
+
+/* gemm_tile_avx2 over WMat::I8 (src/tensor.rs:799-858): the BF16 tile with
+ * the weight lanes widened from int8 (load_w_m256, src/tensor.rs:916-921),
+ * written as eight explicit FMA lanes (identical to the AVX2 FMAs), the row
+ * scale applied at write-back.  In the k tail (in % 8 != 0) the reference
+ * adds x * wf_elem = x * (q * scale) and then multiplies by the scale again
+ * (src/tensor.rs:833-840, 940); that is restated as is.  Token tails and an
+ * odd last row use the dequantizing scalar dot. */
+static void gemm_tile_i8(const float *x, const int8_t *q, const float *s, size_t out, size_t in, size_t T, float *y,
+                         size_t r0, size_t r1) {
+    const size_t kchunks = in / 8, ktail = in % 8;
+    size_t o = r0;
+    while (o + 1 < r1) {
+        const size_t tblock = T - (T % 4);
+        for (size_t tb = 0; tb < tblock; tb += 4) {
+            float acc[4][2][8];
+            memset(acc, 0, sizeof(acc));
+            for (size_t kc = 0; kc < kchunks; kc++) {
+                const size_t ki = kc * 8;
+                for (int t = 0; t < 4; t++)
+                    for (int l = 0; l < 8; l++) {
+                        const float xv = x[(tb + t) * in + ki + l];
+                        acc[t][0][l] = fmaf(xv, (float)q[o * in + ki + l], acc[t][0][l]);
+                        acc[t][1][l] = fmaf(xv, (float)q[(o + 1) * in + ki + l], acc[t][1][l]);
+                    }
+            }
+            for (int t = 0; t < 4; t++) {
+                float s0 = reduce8(acc[t][0]), s1 = reduce8(acc[t][1]);
+                for (size_t k = kchunks * 8; k < kchunks * 8 + ktail; k++) {
+                    const float xk = x[(tb + t) * in + k];
+                    s0 += xk * ((float)q[o * in + k] * s[o]);
+                    s1 += xk * ((float)q[(o + 1) * in + k] * s[o + 1]);
+                }
+                y[(tb + t) * out + o] = s0 * s[o];
+                y[(tb + t) * out + o + 1] = s1 * s[o + 1];
+            }
+        }
+        for (size_t t = tblock; t < T; t++) {
+            y[t * out + o] = dot_deq_i8(x + t * in, q + o * in, s[o], in);
+            y[t * out + o + 1] = dot_deq_i8(x + t * in, q + (o + 1) * in, s[o + 1], in);
+        }
+        o += 2;
+    }
+    if (o < r1)
+        for (size_t t = 0; t < T; t++) y[t * out + o] = dot_deq_i8(x + t * in, q + o * in, s[o], in);
+}
+
+typedef struct {
+    const float *x;
+    const int8_t *q;
+    const float *s;
+    float *y;
+    size_t out, in, T, r0, r1;
+} gemm_i8_job;
+
+static void *gemm_i8_worker(void *p) {
+    gemm_i8_job *j = (gemm_i8_job *)p;
+    gemm_tile_i8(j->x, j->q, j->s, j->out, j->in, j->T, j->y, j->r0, j->r1);
+    return NULL;
+}
+
+/* matmul_batch_w_into for WMat::I8: T >= 2 takes the tile above in 8-row
+ * jobs over all cores (src/tensor.rs:741-792); T == 1 the dequantizing loop
+ * (src/tensor.rs:622-633; with several threads and out >= 64 the reference
+ * reaches unreachable!() at src/tensor.rs:641 instead -- a one-token prompt
+ * in int8 mode -- and this restates the single-thread result). */
+OM_API void om_matmul_batch_w_i8(const float *x, const int8_t *q, const float *s, size_t out, size_t in, size_t T,
+                                 float *y) {
+    if (T < 2) {
+        for (size_t o = 0; o < out; o++)
+            for (size_t t = 0; t < T; t++) y[t * out + o] = dot_deq_i8(x + t * in, q + o * in, s[o], in);
+        return;
+    }
+    size_t rowblock = 8, njobs = (out + rowblock - 1) / rowblock;
+    size_t nthreads = (size_t)num_threads();
+    if (nthreads > njobs) nthreads = njobs;
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    size_t base = njobs / nthreads, extra = njobs % nthreads, js = 0, nt = 0;
+    pthread_t th[256];
+    gemm_i8_job jobs[256];
+    for (size_t ti = 0; ti < nthreads; ti++) {
+        size_t nj = base + (ti < extra ? 1 : 0);
+        if (nj == 0) break;
+        size_t r0 = js * rowblock, r1 = (js + nj) * rowblock;
+        if (r1 > out) r1 = out;
+        js += nj;
+        jobs[nt] = (gemm_i8_job){x, q, s, y, out, in, T, r0, r1};
+        pthread_create(&th[nt], NULL, gemm_i8_worker, &jobs[nt]);
+        nt++;
+    }
+    for (size_t i = 0; i < nt; i++) pthread_join(th[i], NULL);
+}
+
+/* ------------------------------------------------------------------------ */
 /* A8: RMSNorm (src/tensor.rs:946-977)                                       */
 /* ------------------------------------------------------------------------ */
 
@@ -643,7 +840,35 @@ typedef struct {
     const float *final_norm;
     const float *embed;    /* [V,H] f32, the reference converts at load */
     const uint16_t *lm_bf16; /* [V,H] BF16, or NULL when tied */
+    /* int8 mode (TMG_I8=1, src/model.rs:57-76, 212-218): per-layer int8 rows
+     * and row scales of q, k, v, o, gate, up, down, in that order; all NULL in
+     * BF16 mode.  lm_head, norms and the embedding stay as above. */
+    const int8_t **q8[7];
+    const float **s8[7];
 } om_weights;
+
+enum { W_Q, W_K, W_V, W_O, W_G, W_U, W_D };
+
+static const uint16_t *w_bf16(const om_weights *w, int which, int l) {
+    const uint16_t **t[7] = {w->wq, w->wk, w->wv, w->wo, w->wg, w->wu, w->wd};
+    return t[which][l];
+}
+
+/* matmul_w_into / matmul_batch_w_into dispatch on the WMat variant. */
+static void lin(const om_weights *w, int which, int l, const float *x, size_t out, size_t in, float *y) {
+    if (w->q8[which])
+        om_matmul_w_i8(x, w->q8[which][l], w->s8[which][l], out, in, y);
+    else
+        om_matmul_w(x, w_bf16(w, which, l), out, in, y);
+}
+
+static void lin_batch(const om_weights *w, int which, int l, const float *x, size_t out, size_t in, size_t T,
+                      float *y) {
+    if (w->q8[which])
+        om_matmul_batch_w_i8(x, w->q8[which][l], w->s8[which][l], out, in, T, y);
+    else
+        om_matmul_batch_w(x, w_bf16(w, which, l), out, in, T, y);
+}
 
 typedef struct {
     om_weights w;
@@ -673,6 +898,15 @@ OM_API om_model *om_model_new(const om_weights *w) {
         memcpy(copy, *fields[f], sizeof(void *) * L);
         *fields[f] = copy;
     }
+    for (int f = 0; f < 7; f++) {
+        if (!w->q8[f]) continue;
+        const int8_t **qc = (const int8_t **)malloc(sizeof(void *) * L);
+        const float **sc = (const float **)malloc(sizeof(void *) * L);
+        memcpy(qc, w->q8[f], sizeof(void *) * L);
+        memcpy(sc, w->s8[f], sizeof(void *) * L);
+        m->w.q8[f] = qc;
+        m->w.s8[f] = sc;
+    }
     rope_init(&m->rope, (size_t)w->head_dim, w->theta);
     size_t H = w->hidden, qd = (size_t)w->n_heads * w->head_dim, kvd = (size_t)w->n_kv * w->head_dim;
     size_t I = w->inter;
@@ -701,6 +935,10 @@ OM_API void om_model_free(om_model *m) {
     free((void *)m->w.wd);
     free((void *)m->w.in_norm);
     free((void *)m->w.post_norm);
+    for (int f = 0; f < 7; f++) {
+        free((void *)m->w.q8[f]);
+        free((void *)m->w.s8[f]);
+    }
     rope_free(&m->rope);
     free(m->x);
     free(m->attn_in);
@@ -787,9 +1025,9 @@ OM_API int om_forward_token(om_model *m, om_cache *c, uint32_t token, float *log
     float *x = m->x;
     for (int l = 0; l < w->layers; l++) {
         om_rms_norm(x, w->in_norm[l], w->eps, H, m->attn_in);
-        om_matmul_w(m->attn_in, w->wq[l], qd, H, m->q);
-        om_matmul_w(m->attn_in, w->wk[l], kvd, H, m->k);
-        om_matmul_w(m->attn_in, w->wv[l], kvd, H, m->v);
+        lin(w, W_Q, l, m->attn_in, qd, H, m->q);
+        lin(w, W_K, l, m->attn_in, kvd, H, m->k);
+        lin(w, W_V, l, m->attn_in, kvd, H, m->v);
         size_t pos = c->lens[l];
         for (size_t h = 0; h < nq; h++) rope_rotate_tab(&m->rope, m->q + h * hd, pos);
         for (size_t h = 0; h < nkv; h++) rope_rotate_tab(&m->rope, m->k + h * hd, pos);
@@ -803,16 +1041,16 @@ OM_API int om_forward_token(om_model *m, om_cache *c, uint32_t token, float *log
         for (size_t h = 0; h < nq; h++)
             attn_head(m->q + h * hd, c->keys[l], c->vals[l], kvd, (h / group) * hd, hd, n_ctx, scale,
                       m->attn_out + h * hd, m->scores);
-        om_matmul_w(m->attn_out, w->wo[l], H, qd, m->proj);
+        lin(w, W_O, l, m->attn_out, H, qd, m->proj);
         for (size_t i = 0; i < H; i++) x[i] += m->proj[i];
         om_rms_norm(x, w->post_norm[l], w->eps, H, m->mlp_in);
-        om_matmul_w(m->mlp_in, w->wg[l], I, H, m->gate);
-        om_matmul_w(m->mlp_in, w->wu[l], I, H, m->up);
+        lin(w, W_G, l, m->mlp_in, I, H, m->gate);
+        lin(w, W_U, l, m->mlp_in, I, H, m->up);
         for (size_t i = 0; i < I; i++) {
             float g = m->gate[i];
             m->gate[i] = g / (1.0f + expf(-g)) * m->up[i];
         }
-        om_matmul_w(m->gate, w->wd[l], H, I, m->down);
+        lin(w, W_D, l, m->gate, H, I, m->down);
         for (size_t i = 0; i < H; i++) x[i] += m->down[i];
     }
     om_rms_norm(x, w->final_norm, w->eps, H, m->attn_in);
@@ -844,9 +1082,9 @@ OM_API int om_forward_seq(om_model *m, om_cache *c, const uint32_t *tokens, size
     for (int l = 0; l < w->layers; l++) {
         memcpy(normed, x, sizeof(float) * T * H);
         om_rms_norm_batch(normed, w->in_norm[l], w->eps, H, T);
-        om_matmul_batch_w(normed, w->wq[l], qd, H, T, q);
-        om_matmul_batch_w(normed, w->wk[l], kvd, H, T, k);
-        om_matmul_batch_w(normed, w->wv[l], kvd, H, T, v);
+        lin_batch(w, W_Q, l, normed, qd, H, T, q);
+        lin_batch(w, W_K, l, normed, kvd, H, T, k);
+        lin_batch(w, W_V, l, normed, kvd, H, T, v);
         for (size_t t = 0; t < T; t++) {
             size_t pos = start + t;
             for (size_t h = 0; h < nq; h++) rope_rotate_tab(&m->rope, q + t * qd + h * hd, pos);
@@ -854,17 +1092,17 @@ OM_API int om_forward_seq(om_model *m, om_cache *c, const uint32_t *tokens, size
         }
         for (size_t t = 0; t < T; t++) om_cache_push(c, l, k + t * kvd, v + t * kvd);
         om_attention_batch(q, c->keys[l], c->vals[l], T, nq, nkv, hd, start, att);
-        om_matmul_batch_w(att, w->wo[l], H, qd, T, proj);
+        lin_batch(w, W_O, l, att, H, qd, T, proj);
         for (size_t i = 0; i < T * H; i++) x[i] += proj[i];
         memcpy(normed, x, sizeof(float) * T * H);
         om_rms_norm_batch(normed, w->post_norm[l], w->eps, H, T);
-        om_matmul_batch_w(normed, w->wg[l], I, H, T, gate);
-        om_matmul_batch_w(normed, w->wu[l], I, H, T, up);
+        lin_batch(w, W_G, l, normed, I, H, T, gate);
+        lin_batch(w, W_U, l, normed, I, H, T, up);
         for (size_t i = 0; i < T * I; i++) {
             float g = gate[i];
             gate[i] = g / (1.0f + expf(-g)) * up[i];
         }
-        om_matmul_batch_w(gate, w->wd[l], H, I, T, proj);
+        lin_batch(w, W_D, l, gate, H, I, T, proj);
         for (size_t i = 0; i < T * H; i++) x[i] += proj[i];
     }
     float *last = x + (T - 1) * H;

@@ -113,6 +113,8 @@ SIGNATURES = {
          C.POINTER(C.c_size_t), PF, PF],
     ),
     "tmg_gemv_bf16": (C.c_int, [P, P, P, C.c_uint32, C.c_uint32, P]),
+    "tmg_gemv_i8": (C.c_int, [P, P, P, P, C.c_uint32, C.c_uint32, P]),
+    "tmg_quantize_i8": (C.c_int, [P, C.c_uint32, C.c_uint32, P, P, P]),
     "tmg_decode_greedy": (C.c_int, [P, P, C.c_uint32, C.c_uint32, PU32, PF]),
     "tmg_profile_decode_step": (
         C.c_int, [P, P, C.c_uint32, C.POINTER(tmg_kernel_record), C.c_size_t, C.POINTER(C.c_size_t)]),

@@ -237,6 +237,24 @@ static int load_model(tmg_model *m, const SafeTensorsFile &f) {
         if ((rc = upload_raw(m, stage.data(), stage.size() * 2, &ly.gu))) return rc;
         if ((rc = upload_raw(m, f.data(*wd), H * I * 2, &ly.down))) return rc;
         if ((rc = upload_f32(m, f, n1, &ly.in_norm)) || (rc = upload_f32(m, f, n2, &ly.post_norm))) return rc;
+        if (m->i8) {
+            // per-row quantization commutes with the row permutations above
+            struct {
+                uint16_t *w;
+                int rows, in;
+                int8_t **q8;
+                float **sc;
+            } mats[4] = {{ly.qkv, m->qkv_rows, m->H, &ly.qkv8, &ly.qkv_s},
+                         {ly.o, m->H, m->qd, &ly.o8, &ly.o_s},
+                         {ly.gu, 2 * m->I, m->H, &ly.gu8, &ly.gu_s},
+                         {ly.down, m->H, m->I, &ly.down8, &ly.down_s}};
+            for (auto &mt : mats) {
+                if ((rc = dev_alloc(m, mt.q8, (size_t)mt.rows * mt.in)) || (rc = dev_alloc(m, mt.sc, (size_t)mt.rows)))
+                    return rc;
+                TMG_HIP(launch_quantize_i8(mt.w, mt.rows, mt.in, *mt.q8, *mt.sc, true, m->stream));
+            }
+            TMG_HIP(hipStreamSynchronize(m->stream));
+        }
     }
     const TensorEntry *fn;
     if ((rc = need(f, "model.norm.weight", {H}, &fn)) || (rc = upload_f32(m, f, fn, &m->final_norm))) return rc;
@@ -271,7 +289,8 @@ static int load_model(tmg_model *m, const SafeTensorsFile &f) {
     // persistent decode: instantiated for this shape, cooperative launch
     // supported, and at least 8 workgroups co-resident (at most 2 per CU)
     const int kc_h = (m->H + 2047) / 2048, kc_q = (m->qd + 2047) / 2048, kc_i = (m->I + 2047) / 2048;
-    const void *pk = persistent_kernel(kc_h, kc_q, kc_i, m->hd, group);
+    // (BF16 rows only: int8 models take the per-kernel step)
+    const void *pk = m->i8 ? nullptr : persistent_kernel(kc_h, kc_q, kc_i, m->hd, group);
     int coop = 0, cus = 0, per_cu = 0;
     if (pk && m->L <= kMaxPlanLayers &&
         hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, m->device) == hipSuccess && coop &&
@@ -308,6 +327,8 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
     hipStream_t s = m->stream;
     const int H = m->H, I = m->I, qd = m->qd, kvd = m->kvd;
     const double n_ctx_est = (double)c->len + 1;
+    // bytes per weight and per row scale of the layer matrices
+    const double wb = m->i8 ? 1.0 : 2.0, sb = m->i8 ? 4.0 : 0.0;
     for (int l = 0; l < m->L; l++) {
         const tmg_model::Layer &ly = m->layers[l];
         float *kc = c->k + (size_t)l * c->max_pos * kvd;
@@ -337,7 +358,11 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
             qa.embed_f32 = m->embed_f32;
             qa.x_store = m->x;
         }
-        if (!rec || rec->want("gemv_qkv_rope", (double)m->qkv_rows * H * 2 + H * 8.0 + (qd + 2 * kvd) * 4.0)) TMG_HIP(launch_gemv(pro, EPI_QKV, qa, s));
+        if (m->i8) {
+            qa.W8 = ly.qkv8;
+            qa.wscale = ly.qkv_s;
+        }
+        if (!rec || rec->want("gemv_qkv_rope", (double)m->qkv_rows * (H * wb + sb) + H * 8.0 + (qd + 2 * kvd) * 4.0)) TMG_HIP(launch_gemv(pro, EPI_QKV, qa, s));
 
         AttnArgs aa{};
         aa.q = m->q;
@@ -375,7 +400,11 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
             oa.hd = m->hd;
             oa.group = m->nq / m->nkv;
         }
-        if (!rec || rec->want("gemv_o_resid", (double)H * qd * 2 + qd * 4.0 + H * 8.0)) TMG_HIP(launch_gemv(fused ? PRO_ATTN_COMBINE : PRO_PLAIN, EPI_RESID, oa, s));
+        if (m->i8) {
+            oa.W8 = ly.o8;
+            oa.wscale = ly.o_s;
+        }
+        if (!rec || rec->want("gemv_o_resid", (double)H * (qd * wb + sb) + qd * 4.0 + H * 8.0)) TMG_HIP(launch_gemv(fused ? PRO_ATTN_COMBINE : PRO_PLAIN, EPI_RESID, oa, s));
 
         GemvArgs ga{};
         ga.W = ly.gu;
@@ -385,7 +414,11 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
         ga.norm_w = ly.post_norm;
         ga.eps = m->cfg.rms_norm_eps;
         ga.y = m->h;
-        if (!rec || rec->want("gemv_gateup_swiglu", 2.0 * I * H * 2 + H * 8.0 + I * 4.0)) TMG_HIP(launch_gemv(PRO_NORM, EPI_SWIGLU, ga, s));
+        if (m->i8) {
+            ga.W8 = ly.gu8;
+            ga.wscale = ly.gu_s;
+        }
+        if (!rec || rec->want("gemv_gateup_swiglu", 2.0 * I * (H * wb + sb) + H * 8.0 + I * 4.0)) TMG_HIP(launch_gemv(PRO_NORM, EPI_SWIGLU, ga, s));
 
         GemvArgs da{};
         da.W = ly.down;
@@ -393,7 +426,11 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
         da.in = I;
         da.x = m->h;
         da.y = m->x;
-        if (!rec || rec->want("gemv_down_resid", (double)H * I * 2 + I * 4.0 + H * 8.0)) TMG_HIP(launch_gemv(PRO_PLAIN, EPI_RESID, da, s));
+        if (m->i8) {
+            da.W8 = ly.down8;
+            da.wscale = ly.down_s;
+        }
+        if (!rec || rec->want("gemv_down_resid", (double)H * (I * wb + sb) + I * 4.0 + H * 8.0)) TMG_HIP(launch_gemv(PRO_PLAIN, EPI_RESID, da, s));
     }
     GemvArgs la{};
     la.W = m->lm_head;
@@ -731,6 +768,7 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         g.v_cache = vc;
         g.part = m->pf_part;
         g.cnt = m->pf_cnt;
+        if (m->i8) g.wscale = ly.qkv_s;
         TMG_HIP(launch_gemm(GEPI_QKV, g, s));
 
         AttnArgs aa{};
@@ -770,6 +808,7 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         o.y = m->pf_x;
         o.part = m->pf_part;
         o.cnt = m->pf_cnt;
+        if (m->i8) o.wscale = ly.o_s;
         TMG_HIP(launch_gemm(GEPI_RESID, o, s));
 
         TMG_HIP(launch_rmsnorm_split(m->pf_x, ly.post_norm, m->cfg.rms_norm_eps, T, H, m->pf_hi, m->pf_lo, s));
@@ -784,6 +823,7 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         gu.h_lo = m->pf_hlo;
         gu.part = m->pf_part;
         gu.cnt = m->pf_cnt;
+        if (m->i8) gu.wscale = ly.gu_s;
         TMG_HIP(launch_gemm(GEPI_SWIGLU, gu, s));
 
         GemmArgs d{};
@@ -796,6 +836,7 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         d.y = m->pf_x;
         d.part = m->pf_part;
         d.cnt = m->pf_cnt;
+        if (m->i8) d.wscale = ly.down_s;
         TMG_HIP(launch_gemm(GEPI_RESID, d, s));
     }
     // final norm of the last row (batch association) + lm_head + argmax
@@ -846,6 +887,11 @@ extern "C" int tmg_model_load(const char *path, int device, tmg_model **out) {
         return set_error(TMG_E_INVALID, "device index out of range");
     }
     m->device = device;
+    {
+        // the reference's gate: std::env::var("TMG_I8") == "1" (src/model.rs:61)
+        const char *e = getenv("TMG_I8");
+        m->i8 = e && strcmp(e, "1") == 0;
+    }
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
         model_release(m);
         return set_error(TMG_E_DEVICE, "cannot create a HIP stream on the device");
@@ -1030,6 +1076,34 @@ extern "C" int tmg_gemv_bf16(const uint16_t *w, const float *x, float *y, uint32
     a.x = x;
     a.y = y;
     TMG_HIP(launch_gemv(PRO_PLAIN, EPI_STORE, a, (hipStream_t)stream));
+    return TMG_OK;
+}
+
+extern "C" int tmg_gemv_i8(const int8_t *q, const float *scale, const float *x, float *y, uint32_t out, uint32_t in,
+                           void *stream) {
+    if (!q || !scale || !x || !y || out == 0 || in == 0) return set_error(TMG_E_INVALID, "bad argument to tmg_gemv_i8");
+    if (in % 8 != 0 || in > 16384) return set_error(TMG_E_INVALID, "in must be a multiple of 8 and <= 16384");
+    if (((uintptr_t)q & 7) || ((uintptr_t)x & 15) || ((uintptr_t)scale & 3))
+        return set_error(TMG_E_INVALID, "q must be 8-byte, x 16-byte and scale 4-byte aligned");
+    GemvArgs a{};
+    a.W8 = q;
+    a.wscale = scale;
+    a.out = (int)out;
+    a.in = (int)in;
+    a.x = x;
+    a.y = y;
+    TMG_HIP(launch_gemv(PRO_PLAIN, EPI_STORE, a, (hipStream_t)stream));
+    return TMG_OK;
+}
+
+extern "C" int tmg_quantize_i8(const uint16_t *w, uint32_t rows, uint32_t in, int8_t *q, float *scale, void *stream) {
+    if (!w || !q || !scale || rows == 0 || in == 0) return set_error(TMG_E_INVALID, "bad argument to tmg_quantize_i8");
+    if (in % 8 != 0 || rows > 0x7fffffffu || in > 0x7fffffffu)
+        return set_error(TMG_E_INVALID, "in must be a multiple of 8");
+    if (((uintptr_t)w & 15) || ((uintptr_t)q & 7) || ((uintptr_t)scale & 3))
+        return set_error(TMG_E_INVALID, "w must be 16-byte, q 8-byte and scale 4-byte aligned");
+    // rewrite = false: w is only read
+    TMG_HIP(launch_quantize_i8(const_cast<uint16_t *>(w), (int)rows, (int)in, q, scale, false, (hipStream_t)stream));
     return TMG_OK;
 }
 

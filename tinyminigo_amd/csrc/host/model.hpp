@@ -21,7 +21,13 @@ struct tmg_model {
         uint16_t *gu = nullptr;    // [2I, H]: gate row p at 2p, up row p at 2p+1
         uint16_t *down = nullptr;  // [H, I]
         float *in_norm = nullptr, *post_norm = nullptr;  // [H]
+        // int8 mode: the same four matrices as int8 rows plus f32 row scales
+        // (then qkv/o/gu/down above hold the int8 codes as BF16, for prefill)
+        int8_t *qkv8 = nullptr, *o8 = nullptr, *gu8 = nullptr, *down8 = nullptr;
+        float *qkv_s = nullptr, *o_s = nullptr, *gu_s = nullptr, *down_s = nullptr;
     };
+    // int8 weight-only mode (TMG_I8=1 at load, reference src/model.rs:57-76)
+    bool i8 = false;
     std::vector<Layer> layers;
     float *final_norm = nullptr;
     uint16_t *embed_bf16 = nullptr;  // [V, H] when the file stores BF16

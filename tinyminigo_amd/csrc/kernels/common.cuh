@@ -35,9 +35,19 @@ __device__ __forceinline__ void split_bf16(float x, uint16_t *hi, uint16_t *lo) 
 //   permlane16_swap(a, b) -> {[a0-15, b0-15, a32-47, b32-47],
 //                             [a16-31, b16-31, a48-63, b48-63]}
 //   permlane32_swap(a, b) -> {[a0-31, b0-31], [a32-63, b32-63]}
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+template <class T>
+__device__ __forceinline__ uint32_t as_u32(T v) {
+    static_assert(sizeof(T) == 4, "32-bit lanes only");
+    return __builtin_bit_cast(uint32_t, v);
+}
+template <class T>
+__device__ __forceinline__ T from_u32(uint32_t u) {
+    return __builtin_bit_cast(T, u);
+}
+
+template <int CTRL, class T>
+__device__ __forceinline__ T dpp_mov(T v) {
+    return from_u32<T>((uint32_t)__builtin_amdgcn_update_dpp(0, (int)as_u32(v), CTRL, 0xf, 0xf, false));
 }
 constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
@@ -45,19 +55,21 @@ constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
 constexpr int kDppRor8 = 0x128;       // row_ror:8
 
 // x + (x of lane l^16), and x + (x of lane l^32)
-__device__ __forceinline__ float add_xor16(float x) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+template <class T>
+__device__ __forceinline__ T add_xor16(T x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(as_u32(x), as_u32(x), false, false);
+    return from_u32<T>(r[0]) + from_u32<T>(r[1]);
 }
-__device__ __forceinline__ float add_xor32(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+template <class T>
+__device__ __forceinline__ T add_xor32(T x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(as_u32(x), as_u32(x), false, false);
+    return from_u32<T>(r[0]) + from_u32<T>(r[1]);
 }
 
 // Sum within aligned groups of W lanes (W a power of two <= 64); every lane
-// of a group receives the group's sum.
-template <int W>
-__device__ __forceinline__ float group_sum(float v) {
+// of a group receives the group's sum.  T is float or a 32-bit integer.
+template <int W, class T>
+__device__ __forceinline__ T group_sum(T v) {
     static_assert(W == 1 || W == 2 || W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "W must be a power of two");
     if constexpr (W >= 2) v += dpp_mov<kDppXor1>(v);
     if constexpr (W >= 4) v += dpp_mov<kDppXor2>(v);
@@ -91,33 +103,31 @@ __device__ __forceinline__ float wave_max(float v) {
 // 8 by DPP) that halve the live values, then a plain butterfly within the
 // remaining lane group.  On return every lane holds the wave sum of value
 // (lane >> (6 - log2 R)).
-template <int R>
-__device__ __forceinline__ float multi_wave_sum(float (&v)[R], int lane) {
+template <int R, class T>
+__device__ __forceinline__ T multi_wave_sum(T (&v)[R], int lane) {
     static_assert(R == 1 || R == 2 || R == 4 || R == 8, "R must be 1, 2, 4 or 8");
     constexpr int LR = R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
-    float cur[R];
+    T cur[R];
 #pragma unroll
     for (int i = 0; i < R; i++) cur[i] = v[i];
     if constexpr (LR >= 1) {  // lanes 32-63 keep values [R/2, R)
 #pragma unroll
         for (int i = 0; i < R / 2; i++) {
-            const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(cur[i]), __float_as_uint(cur[i + R / 2]),
-                                                            false, false);
-            cur[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+            const auto r = __builtin_amdgcn_permlane32_swap(as_u32(cur[i]), as_u32(cur[i + R / 2]), false, false);
+            cur[i] = from_u32<T>(r[0]) + from_u32<T>(r[1]);
         }
     }
     if constexpr (LR >= 2) {  // lanes with bit 4 set keep the upper half
 #pragma unroll
         for (int i = 0; i < R / 4; i++) {
-            const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(cur[i]), __float_as_uint(cur[i + R / 4]),
-                                                            false, false);
-            cur[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+            const auto r = __builtin_amdgcn_permlane16_swap(as_u32(cur[i]), as_u32(cur[i + R / 4]), false, false);
+            cur[i] = from_u32<T>(r[0]) + from_u32<T>(r[1]);
         }
     }
     if constexpr (LR >= 3) {  // lanes with bit 3 set keep cur[1]
         const bool up = (lane & 8) != 0;
-        const float send = up ? cur[0] : cur[1];
-        const float keep = up ? cur[1] : cur[0];
+        const T send = up ? cur[0] : cur[1];
+        const T keep = up ? cur[1] : cur[0];
         cur[0] = keep + dpp_mov<kDppRor8>(send);
     }
     return group_sum<(64 >> LR)>(cur[0]);

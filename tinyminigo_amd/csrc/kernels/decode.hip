@@ -48,11 +48,54 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(const GemvArgs a) {
     }
 }
 
+// The same GEMV over int8 rows (GemvArgs::W8): the activation prologue and
+// the epilogues are shared with gemv_kernel; between them the activation is
+// quantized (quantize_act) and the rows are dotted in int32 (gemv_dot8).
+template <int KC, int R, int PRO, int EPI>
+__global__ __launch_bounds__(kBlock) void gemv_i8_kernel(const GemvArgs a) {
+    __shared__ float red[4][R];
+    __shared__ float scratch[4];
+    WeightRegs8<KC, R> W;
+    float xv[KC][8];
+    EpiIn pre{};
+    int pos = 0;
+    if constexpr (PRO == PRO_EMBED_NORM) {
+        gemv_load8<KC, R>(a, blockIdx.x, W);
+        epi_issue_scale<R, EPI>(a, blockIdx.x, pre);
+        if constexpr (EPI == EPI_QKV) pos = *a.pos;
+        gemv_prologue<KC, PRO, false>(a, *a.token, pos, xv, scratch, blockIdx.x == 0);
+        if constexpr (EPI == EPI_QKV) epi_load_rope<R>(a, blockIdx.x, pos, pre);
+    } else {
+        ActIn<KC, PRO> in;
+        act_issue<KC, PRO>(a, in);
+        if constexpr (EPI == EPI_RESID) epi_issue_resid<R>(a, blockIdx.x, pre);
+        epi_issue_scale<R, EPI>(a, blockIdx.x, pre);
+        gemv_load8<KC, R>(a, blockIdx.x, W);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (EPI == EPI_QKV || PRO == PRO_ATTN_COMBINE) pos = *a.pos;
+        if constexpr (EPI == EPI_QKV) epi_load_rope<R>(a, blockIdx.x, pos, pre);
+        act_finish<KC, PRO>(a, pos, in, xv, scratch);
+    }
+    int xq[KC][2];
+    const float xs = quantize_act<KC>(xv, xq, scratch);
+    gemv_dot8<KC, R>(W, xq, red);
+    __syncthreads();
+    gemv_epilogue<R, EPI, false, true, true>(a, blockIdx.x, pos, red, pre, xs);
+}
+
 template <int KC, int PRO, int EPI>
 hipError_t launch_kc(const GemvArgs &a, hipStream_t s) {
     constexpr int R = gemv_rows<KC>();
     const int grid = (a.out + R - 1) / R;
-    hipLaunchKernelGGL((gemv_kernel<KC, R, PRO, EPI>), dim3(grid), dim3(kBlock), 0, s, a);
+    if (a.W8) {
+        if constexpr (EPI == EPI_LOGITS || PRO == PRO_NORM_BATCH) {
+            return hipErrorInvalidValue;  // lm_head keeps BF16 rows
+        } else {
+            hipLaunchKernelGGL((gemv_i8_kernel<KC, R, PRO, EPI>), dim3(grid), dim3(kBlock), 0, s, a);
+        }
+    } else {
+        hipLaunchKernelGGL((gemv_kernel<KC, R, PRO, EPI>), dim3(grid), dim3(kBlock), 0, s, a);
+    }
     return hipGetLastError();
 }
 
@@ -70,6 +113,46 @@ hipError_t launch_pe(const GemvArgs &a, hipStream_t s) {
         case 7: return launch_kc<8, PRO, EPI>(a, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+// WMat::quantize_i8 (src/tensor.rs:275-293) of BF16 rows, one workgroup per
+// row: the row's max |w| (block reduction), scale = max/127 or 1 for a zero
+// row, q = round(w / scale) with halves away from zero, clamped to +-127.
+__global__ __launch_bounds__(kBlock) void quantize_i8_kernel(uint16_t *w, int in, int8_t *q8, float *scale,
+                                                             int rewrite) {
+    __shared__ float scratch[4];
+    const int row = blockIdx.x;
+    uint16_t *wr = w + (size_t)row * in;
+    int8_t *qr = q8 + (size_t)row * in;
+    float m[1] = {0.0f};
+    for (int k = threadIdx.x * 8; k < in; k += kBlock * 8) {
+        const uint4 u = *reinterpret_cast<const uint4 *>(wr + k);
+        const uint32_t p[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) m[0] = fmaxf(fabsf(bf16_hi(p[j])), fmaxf(fabsf(bf16_lo(p[j])), m[0]));
+    }
+    block_max_n<1>(m, scratch);
+    const float sc = m[0] > 0.0f ? __fdiv_rn(m[0], 127.0f) : 1.0f;
+    for (int k = threadIdx.x * 8; k < in; k += kBlock * 8) {
+        const uint4 u = *reinterpret_cast<const uint4 *>(wr + k);
+        const uint32_t p[4] = {u.x, u.y, u.z, u.w};
+        uint32_t packed[2] = {0u, 0u}, codes[4];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float v = (j & 1) ? bf16_hi(p[j >> 1]) : bf16_lo(p[j >> 1]);
+            const float r = roundf(__fdiv_rn(v, sc));
+            const int q = r == r ? (int)fminf(fmaxf(r, -127.0f), 127.0f) : 0;
+            packed[j >> 2] |= ((uint32_t)q & 0xffu) << (8 * (j & 3));
+            const uint32_t b = f32_to_bf16_rne((float)q);  // exact: |q| <= 127
+            if (j & 1)
+                codes[j >> 1] |= b << 16;
+            else
+                codes[j >> 1] = b;
+        }
+        *reinterpret_cast<uint2 *>(qr + k) = make_uint2(packed[0], packed[1]);
+        if (rewrite) *reinterpret_cast<uint4 *>(wr + k) = make_uint4(codes[0], codes[1], codes[2], codes[3]);
+    }
+    if (threadIdx.x == 0) scale[row] = sc;
 }
 
 // ---------------------------------------------------------------------------
@@ -206,6 +289,13 @@ hipError_t launch_gemv(int pro, int epi, const GemvArgs &a, hipStream_t s) {
     TMG_PE(PRO_NORM_BATCH, EPI_LOGITS)
 #undef TMG_PE
     return hipErrorInvalidValue;
+}
+
+hipError_t launch_quantize_i8(uint16_t *w, int rows, int in, int8_t *q8, float *scale, bool rewrite,
+                              hipStream_t s) {
+    if (rows <= 0 || in <= 0 || in % 8) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(quantize_i8_kernel, dim3(rows), dim3(kBlock), 0, s, w, in, q8, scale, rewrite ? 1 : 0);
+    return hipGetLastError();
 }
 
 hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {

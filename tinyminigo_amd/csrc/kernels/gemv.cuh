@@ -24,6 +24,7 @@ namespace tmg {
 constexpr int kChunk = kBlock * 8;  // elements per chunk: 8 per thread
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 template <int KC>
 __host__ __device__ constexpr int gemv_rows() {
@@ -222,19 +223,33 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs &a, int tok, int po
 struct EpiIn {
     float resid;
     float rc[4], rs[4];
+    float sc[2];  // int8 rows: the scales of the thread's epilogue rows
 };
 
 __device__ __forceinline__ float pick4(const float (&v)[4], int i) {
     return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
 }
 
-// FMAs over a loaded block, the block reduction and the epilogue.
-// `red` is LDS of 4*R floats.  Returns after the epilogue; the caller
-// separates consecutive calls with a __syncthreads (red is reused).  With
-// PRE the residual / RoPE inputs come from `pre` instead of memory.
-template <int KC, int R, int EPI, bool COH, bool PRE = false>
-__device__ __forceinline__ void gemv_finish(const GemvArgs &a, int blk, int pos, const WeightRegs<KC, R> &W,
-                                            const float (&xv)[KC][8], float (*red)[R], const EpiIn &pre = EpiIn{}) {
+// Value of local row i of a block from the four per-wave partials in `red`:
+// the f32 sum (BF16 rows), or for int8 rows the exact integer dot times the
+// activation scale and the row scale, y = (dot as f32) * xs * scale[o]
+// (matmul_w_into's WMat::I8 arm, src/tensor.rs:349-353).
+template <int R, bool Q8>
+__device__ __forceinline__ float row_value(float (*red)[R], int i, float xs, float sc) {
+    if constexpr (Q8) {
+        const int d = (__float_as_int(red[0][i]) + __float_as_int(red[1][i])) +
+                      (__float_as_int(red[2][i]) + __float_as_int(red[3][i]));
+        return __fmul_rn(__fmul_rn((float)d, xs), sc);
+    } else {
+        return (red[0][i] + red[1][i]) + (red[2][i] + red[3][i]);
+    }
+}
+
+// FMAs over a loaded block of BF16 rows and the per-wave reduction into
+// `red` (LDS of 4*R floats).
+template <int KC, int R>
+__device__ __forceinline__ void gemv_dot(const GemvArgs &a, const WeightRegs<KC, R> &W, const float (&xv)[KC][8],
+                                         float (*red)[R]) {
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     float acc[R];
@@ -255,17 +270,24 @@ __device__ __forceinline__ void gemv_finish(const GemvArgs &a, int blk, int pos,
         }
         acc[r] = s0 + s1;
     }
-    {
-        constexpr int LR = R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
-        const float s = multi_wave_sum<R>(acc, lane);
-        if ((lane & ((64 >> LR) - 1)) == 0) red[wave][lane >> (6 - LR)] = s;
-    }
-    __syncthreads();
+    constexpr int LR = R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
+    const float sum = multi_wave_sum<R>(acc, lane);
+    if ((lane & ((64 >> LR) - 1)) == 0) red[wave][lane >> (6 - LR)] = sum;
+}
+
+// The epilogue of a block whose per-wave partials are in `red` (after a
+// __syncthreads).  With PRE the residual / RoPE inputs come from `pre`
+// instead of memory; with Q8 the rows are int8 (row scales in pre.sc, xs the
+// activation scale).
+template <int R, int EPI, bool COH, bool PRE, bool Q8>
+__device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int blk, int pos, float (*red)[R], const EpiIn &pre,
+                                              float xs) {
+    const int t = threadIdx.x;
     const int row0 = blk * R;
     if constexpr (EPI == EPI_STORE || EPI == EPI_RESID || EPI == EPI_LOGITS) {
         if (t < R) {
             const int row = row0 + t;
-            const float v = (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
+            const float v = row_value<R, Q8>(red, t, xs, pre.sc[0]);
             const bool ok = row < a.out;
             if (ok) {
                 if constexpr (EPI == EPI_RESID)
@@ -288,8 +310,8 @@ __device__ __forceinline__ void gemv_finish(const GemvArgs &a, int blk, int pos,
     } else {
         if (t < R / 2) {
             const int P = row0 / 2 + t;  // global pair index
-            const float va = (red[0][2 * t] + red[1][2 * t]) + (red[2][2 * t] + red[3][2 * t]);
-            const float vb = (red[0][2 * t + 1] + red[1][2 * t + 1]) + (red[2][2 * t + 1] + red[3][2 * t + 1]);
+            const float va = row_value<R, Q8>(red, 2 * t, xs, pre.sc[0]);
+            const float vb = row_value<R, Q8>(red, 2 * t + 1, xs, pre.sc[1]);
             if (2 * P + 1 < a.out) {
                 if constexpr (EPI == EPI_SWIGLU) {
                     stf<COH>(a.y + P, swiglu(va, vb));
@@ -319,6 +341,125 @@ __device__ __forceinline__ void gemv_finish(const GemvArgs &a, int blk, int pos,
             }
         }
     }
+}
+
+// FMAs over a loaded block, the block reduction and the epilogue.
+// `red` is LDS of 4*R floats.  Returns after the epilogue; the caller
+// separates consecutive calls with a __syncthreads (red is reused).  With
+// PRE the residual / RoPE inputs come from `pre` instead of memory.
+template <int KC, int R, int EPI, bool COH, bool PRE = false>
+__device__ __forceinline__ void gemv_finish(const GemvArgs &a, int blk, int pos, const WeightRegs<KC, R> &W,
+                                            const float (&xv)[KC][8], float (*red)[R], const EpiIn &pre = EpiIn{}) {
+    gemv_dot<KC, R>(a, W, xv, red);
+    __syncthreads();
+    gemv_epilogue<R, EPI, COH, PRE, false>(a, blk, pos, red, pre, 0.0f);
+}
+
+// ---------------------------------------------------------------------------
+// int8 rows (the TMG_I8 weight-only mode, reference src/model.rs:57-76):
+// W8 [out, in] int8 with one f32 scale per row.  Same element mapping as the
+// BF16 rows -- thread t takes elements c*2048 + 8t .. +7 of every row -- with
+// 8-byte loads.  The activation is quantized like quantize_row_i8
+// (src/tensor.rs:125-139) by every workgroup from the registers it already
+// holds, and the dots are exact int32 v_dot4_i32_i8 sums, as dot_i8's i16
+// madd sums are (src/tensor.rs:144-170).
+// ---------------------------------------------------------------------------
+
+template <int KC, int R>
+struct WeightRegs8 {
+    u32x2 w[R][KC];
+};
+
+template <int KC, int R>
+__device__ __forceinline__ void gemv_load8(const GemvArgs &a, int blk, WeightRegs8<KC, R> &W) {
+    const int t = threadIdx.x;
+    const int row0 = blk * R;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int row = min(row0 + r, a.out - 1);
+        const u32x2 *wr = reinterpret_cast<const u32x2 *>(a.W8 + (size_t)row * a.in);
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            // clamped like gemv_load; the activation codes past the row end
+            // are zero, so those lanes add nothing
+            const int k = c * kChunk + t * 8;
+            W.w[r][c] = __builtin_nontemporal_load(wr + (min(k, a.in - 8) >> 3));
+        }
+    }
+}
+
+// Scales of the rows this thread's epilogue writes: row blk*R + t (t < R), or
+// the pair 2t, 2t+1 (t < R/2) for the pair epilogues.
+template <int R, int EPI>
+__device__ __forceinline__ void epi_issue_scale(const GemvArgs &a, int blk, EpiIn &pre) {
+    const int t = threadIdx.x;
+    const int row0 = blk * R;
+    pre.sc[0] = pre.sc[1] = 0.0f;
+    if constexpr (EPI == EPI_SWIGLU || EPI == EPI_QKV) {
+        const int r = row0 + 2 * t;
+        if (t < R / 2 && r + 1 < a.out) {
+            const float2 v = *reinterpret_cast<const float2 *>(a.wscale + r);
+            pre.sc[0] = v.x;
+            pre.sc[1] = v.y;
+        }
+    } else {
+        const int r = row0 + t;
+        if (t < R && r < a.out) pre.sc[0] = a.wscale[r];
+    }
+}
+
+// quantize_row_i8 of the activation held in registers: xs = max|x| / 127,
+// q = round(x * (1 / xs)) (half away from zero) clamped to [-127, 127], four
+// codes per int; an all-zero vector gives zero codes and xs = 0.  Every
+// thread returns xs.  `scratch` holds 4 floats of LDS.
+template <int KC>
+__device__ __forceinline__ float quantize_act(const float (&xv)[KC][8], int (&xq)[KC][2], float *scratch) {
+    float m[1] = {0.0f};
+#pragma unroll
+    for (int c = 0; c < KC; c++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) m[0] = fmaxf(fabsf(xv[c][j]), m[0]);
+    block_max_n<1>(m, scratch);
+    const float maxabs = m[0];
+    const float s = __fdiv_rn(maxabs, 127.0f);
+    const float inv = maxabs == 0.0f ? 0.0f : __fdiv_rn(1.0f, s);
+#pragma unroll
+    for (int c = 0; c < KC; c++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            uint32_t packed = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float r = roundf(__fmul_rn(xv[c][4 * h + j], inv));
+                // `as i8` after clamp: NaN becomes 0
+                const int q = r == r ? (int)fminf(fmaxf(r, -127.0f), 127.0f) : 0;
+                packed |= ((uint32_t)q & 0xffu) << (8 * j);
+            }
+            xq[c][h] = (int)packed;
+        }
+    return maxabs == 0.0f ? 0.0f : s;
+}
+
+// Exact integer dots of a loaded int8 block and the per-wave reduction into
+// `red` (int32 bit patterns in LDS of 4*R floats).
+template <int KC, int R>
+__device__ __forceinline__ void gemv_dot8(const WeightRegs8<KC, R> &W, const int (&xq)[KC][2], float (*red)[R]) {
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    int acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        int d = 0;
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            d = __builtin_amdgcn_sdot4(xq[c][0], (int)W.w[r][c].x, d, false);
+            d = __builtin_amdgcn_sdot4(xq[c][1], (int)W.w[r][c].y, d, false);
+        }
+        acc[r] = d;
+    }
+    constexpr int LR = R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
+    const int sum = multi_wave_sum<R>(acc, lane);
+    if ((lane & ((64 >> LR) - 1)) == 0) red[wave][lane >> (6 - LR)] = __int_as_float(sum);
 }
 
 // ---------------------------------------------------------------------------

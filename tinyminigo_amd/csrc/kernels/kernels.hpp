@@ -35,6 +35,10 @@ enum GemvEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV = 3, EPI_LO
 
 struct GemvArgs {
     const uint16_t *W;  // [out, in] BF16 rows (pair-interleaved for SWIGLU/QKV)
+    // int8 rows instead (the TMG_I8 mode): [out, in] codes and [out] f32 row
+    // scales, same row order as W; null selects the BF16 rows
+    const int8_t *W8;
+    const float *wscale;
     int out, in;
     const float *x;       // activation (PRO_PLAIN) or residual stream (PRO_NORM*)
     const float *norm_w;  // [in] f32 RMSNorm weight
@@ -61,6 +65,12 @@ struct GemvArgs {
 };
 
 hipError_t launch_gemv(int pro, int epi, const GemvArgs &a, hipStream_t s);
+// WMat::quantize_i8 of BF16 rows (src/tensor.rs:275-293, widened from BF16 as
+// wmat_maybe_i8 does, src/model.rs:60-68): q8 [rows, in] codes and scale
+// [rows].  With rewrite, w is overwritten with the codes as BF16 (exact), the
+// dequantized weight up to the row scale, for the prefill GEMMs.
+hipError_t launch_quantize_i8(uint16_t *w, int rows, int in, int8_t *q8, float *scale, bool rewrite,
+                              hipStream_t s);
 // Workgroups (= argmax partials) of a GEMV launch with `out` rows of `in`.
 int gemv_blocks(int out, int in);
 
@@ -130,6 +140,7 @@ enum GemmEpi { GEPI_STORE = 0, GEPI_RESID = 1, GEPI_SWIGLU = 2, GEPI_QKV = 3 };
 
 struct GemmArgs {
     const uint16_t *W;  // [M, K] BF16
+    const float *wscale;  // [M] row scales applied before the epilogue (int8 weights held as BF16 codes), or null
     const uint16_t *Bhi, *Blo;  // [N, K] split-bf16 activations
     int M, N, K;
     // epilogues

@@ -79,8 +79,16 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_split_kernel(const float *x, c
 // Epilogue of one MFMA output fragment: rows mb .. mb+3 (mb a multiple of 4)
 // of token column n.  Pair epilogues use rows (mb, mb+1) and (mb+2, mb+3).
 template <int EPI>
-__device__ __forceinline__ void gemm_store(const GemmArgs &a, int mb, int n, const f32x4 &v) {
+__device__ __forceinline__ void gemm_store(const GemmArgs &a, int mb, int n, const f32x4 &acc) {
     if (n >= a.N) return;
+    f32x4 v = acc;
+    if (a.wscale) {
+        // int8 weights: the row scale at write-back, y = acc * scale[o]
+        // (src/tensor.rs:839-840)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (mb + i < a.M) v[i] = __fmul_rn(v[i], a.wscale[mb + i]);
+    }
     if constexpr (EPI == GEPI_STORE || EPI == GEPI_RESID) {
         float *yr = a.y + (size_t)n * a.M;
 #pragma unroll

@@ -19,7 +19,7 @@ from ._lib import (
 )
 
 __all__ = [
-    "ModelConfig", "Model", "KvCache", "GenParams", "GenOutput", "generate", "gemv_bf16",
+    "ModelConfig", "Model", "KvCache", "GenParams", "GenOutput", "generate", "gemv_bf16", "gemv_i8", "quantize_i8",
     "synth_model", "synth_tokens", "synth_normal_bf16", "synth_normal_f32", "TmgError",
 ]
 
@@ -241,6 +241,18 @@ def gemv_bf16(w_dev: int, x_dev: int, y_dev: int, out: int, in_: int, stream: in
     """tensor::matmul_w (src/tensor.rs:315-338) on device pointers."""
     check(lib.tmg_gemv_bf16(C.c_void_p(w_dev), C.c_void_p(x_dev), C.c_void_p(y_dev), out, in_,
                             C.c_void_p(stream)))
+
+
+def gemv_i8(q_dev: int, scale_dev: int, x_dev: int, y_dev: int, out: int, in_: int, stream: int = 0) -> None:
+    """matmul_w_into over WMat::I8 (src/tensor.rs:341-364) on device pointers."""
+    check(lib.tmg_gemv_i8(C.c_void_p(q_dev), C.c_void_p(scale_dev), C.c_void_p(x_dev), C.c_void_p(y_dev), out,
+                          in_, C.c_void_p(stream)))
+
+
+def quantize_i8(w_dev: int, rows: int, in_: int, q_dev: int, scale_dev: int, stream: int = 0) -> None:
+    """WMat::quantize_i8 (src/tensor.rs:275-293) of BF16 rows on device pointers."""
+    check(lib.tmg_quantize_i8(C.c_void_p(w_dev), rows, in_, C.c_void_p(q_dev), C.c_void_p(scale_dev),
+                              C.c_void_p(stream)))
 
 
 # -- synthetic inputs ---------------------------------------------------------

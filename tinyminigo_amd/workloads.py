@@ -41,12 +41,16 @@ class Workload:
         return synth_tokens(self.prompt_seed, self.prompt_len, self.vocab_size)
 
     # algorithmic bytes streamed per decode token (BF16 weights, f32 norms,
-    # one embedding row, f32 KV read at n_ctx and the KV row written)
-    def weight_bytes(self) -> int:
+    # one embedding row, f32 KV read at n_ctx and the KV row written); with
+    # i8 the layer matrices are int8 codes plus one f32 scale per row and the
+    # lm_head stays BF16
+    def weight_bytes(self, i8: bool = False) -> int:
         H, I, V = self.hidden_size, self.intermediate_size, self.vocab_size
         qd = self.num_attention_heads * self.head_dim
         kvd = self.num_key_value_heads * self.head_dim
-        per_layer = (qd * H + 2 * kvd * H + H * qd + 3 * H * I) * 2
+        params = qd * H + 2 * kvd * H + H * qd + 3 * H * I
+        rows = qd + 2 * kvd + H + 2 * I + H
+        per_layer = params + 4 * rows if i8 else params * 2
         return self.num_hidden_layers * per_layer + V * H * 2
 
     def kv_bytes(self, n_ctx: int) -> int:
@@ -57,8 +61,8 @@ class Workload:
         H = self.hidden_size
         return (2 * self.num_hidden_layers + 1) * H * 4 + H * 2
 
-    def decode_bytes(self, n_ctx: int) -> int:
-        return self.weight_bytes() + self.kv_bytes(n_ctx) + self.misc_bytes()
+    def decode_bytes(self, n_ctx: int, i8: bool = False) -> int:
+        return self.weight_bytes(i8) + self.kv_bytes(n_ctx) + self.misc_bytes()
 
     def prefill_flops(self, T: int, start: int = 0) -> float:
         H, I, V = self.hidden_size, self.intermediate_size, self.vocab_size
