@@ -105,8 +105,8 @@ __device__ __forceinline__ float wave_max(float v) {
 // (lane >> (6 - log2 R)).
 template <int R, class T>
 __device__ __forceinline__ T multi_wave_sum(T (&v)[R], int lane) {
-    static_assert(R == 1 || R == 2 || R == 4 || R == 8, "R must be 1, 2, 4 or 8");
-    constexpr int LR = R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
+    static_assert(R == 1 || R == 2 || R == 4 || R == 8 || R == 16, "R must be 1, 2, 4, 8 or 16");
+    constexpr int LR = R == 16 ? 4 : R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
     T cur[R];
 #pragma unroll
     for (int i = 0; i < R; i++) cur[i] = v[i];
@@ -124,11 +124,21 @@ __device__ __forceinline__ T multi_wave_sum(T (&v)[R], int lane) {
             cur[i] = from_u32<T>(r[0]) + from_u32<T>(r[1]);
         }
     }
-    if constexpr (LR >= 3) {  // lanes with bit 3 set keep cur[1]
-        const bool up = (lane & 8) != 0;
+    if constexpr (LR >= 3) {  // lanes with bit 3 set keep the upper half
+#pragma unroll
+        for (int i = 0; i < R / 8; i++) {
+            const bool up = (lane & 8) != 0;
+            const T send = up ? cur[i] : cur[i + R / 8];
+            const T keep = up ? cur[i + R / 8] : cur[i];
+            cur[i] = keep + dpp_mov<kDppRor8>(send);
+        }
+    }
+    if constexpr (LR >= 4) {  // lanes with bit 2 set keep cur[1]; the partner
+        // across the half-row mirror (7 - l within 8 lanes) has bit 2 clear
+        const bool up = (lane & 4) != 0;
         const T send = up ? cur[0] : cur[1];
         const T keep = up ? cur[1] : cur[0];
-        cur[0] = keep + dpp_mov<kDppRor8>(send);
+        cur[0] = keep + dpp_mov<kDppHalfMirror>(send);
     }
     return group_sum<(64 >> LR)>(cur[0]);
 }
@@ -187,9 +197,12 @@ __device__ __forceinline__ float swiglu(float g, float u) { return __fmul_rn(__f
 
 // rotate_half RoPE of the pair (a, b) = (v[i], v[i+hd/2]) without FMA
 // contraction, as the reference computes it (src/tensor.rs:1031-1036).
+// (HIP's __fmul_rn / __fsub_rn are plain operators compiled where
+// contraction is on; the operators written under the pragma are not fused.)
 __device__ __forceinline__ void rope_pair(float a, float b, float c, float s, float *oa, float *ob) {
-    *oa = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s));
-    *ob = __fadd_rn(__fmul_rn(a, s), __fmul_rn(b, c));
+#pragma clang fp contract(off)
+    *oa = a * c - b * s;
+    *ob = a * s + b * c;
 }
 
 }  // namespace tmg

@@ -91,7 +91,9 @@ hipError_t launch_kc(const GemvArgs &a, hipStream_t s) {
         if constexpr (EPI == EPI_LOGITS || PRO == PRO_NORM_BATCH) {
             return hipErrorInvalidValue;  // lm_head keeps BF16 rows
         } else {
-            hipLaunchKernelGGL((gemv_i8_kernel<KC, R, PRO, EPI>), dim3(grid), dim3(kBlock), 0, s, a);
+            constexpr int R8 = gemv_rows8<KC, PRO>();
+            hipLaunchKernelGGL((gemv_i8_kernel<KC, R8, PRO, EPI>), dim3((a.out + R8 - 1) / R8), dim3(kBlock), 0, s,
+                               a);
         }
     } else {
         hipLaunchKernelGGL((gemv_kernel<KC, R, PRO, EPI>), dim3(grid), dim3(kBlock), 0, s, a);

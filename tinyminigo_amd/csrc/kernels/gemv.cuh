@@ -222,6 +222,8 @@ __device__ __forceinline__ void gemv_prologue(const GemvArgs &a, int tok, int po
 // (thread t < R) and the RoPE cos/sin of the block's R/2 rotation pairs.
 struct EpiIn {
     float resid;
+    // RoPE cos/sin: all R/2 pairs of the block (uniform scalar loads) when
+    // R <= 8; with R = 16, entry 0 holds this thread's own pair
     float rc[4], rs[4];
     float sc[2];  // int8 rows: the scales of the thread's epilogue rows
 };
@@ -236,10 +238,13 @@ __device__ __forceinline__ float pick4(const float (&v)[4], int i) {
 // (matmul_w_into's WMat::I8 arm, src/tensor.rs:349-353).
 template <int R, bool Q8>
 __device__ __forceinline__ float row_value(float (*red)[R], int i, float xs, float sc) {
+    // the product is rounded before any residual add, as the reference
+    // stores y and adds it afterwards (no contraction into an FMA)
+#pragma clang fp contract(off)
     if constexpr (Q8) {
         const int d = (__float_as_int(red[0][i]) + __float_as_int(red[1][i])) +
                       (__float_as_int(red[2][i]) + __float_as_int(red[3][i]));
-        return __fmul_rn(__fmul_rn((float)d, xs), sc);
+        return ((float)d * xs) * sc;
     } else {
         return (red[0][i] + red[1][i]) + (red[2][i] + red[3][i]);
     }
@@ -270,7 +275,7 @@ __device__ __forceinline__ void gemv_dot(const GemvArgs &a, const WeightRegs<KC,
         }
         acc[r] = s0 + s1;
     }
-    constexpr int LR = R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
+    constexpr int LR = R == 16 ? 4 : R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
     const float sum = multi_wave_sum<R>(acc, lane);
     if ((lane & ((64 >> LR) - 1)) == 0) red[wave][lane >> (6 - LR)] = sum;
 }
@@ -321,8 +326,8 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int blk, int po
                     const int kvd = a.nkv * a.hd;
                     if (head < a.nq + a.nkv) {
                         float oa, ob;
-                        const float rc = PRE ? pick4(pre.rc, t) : a.rope_cos[(size_t)pos * half + j];
-                        const float rs = PRE ? pick4(pre.rs, t) : a.rope_sin[(size_t)pos * half + j];
+                        const float rc = !PRE ? a.rope_cos[(size_t)pos * half + j] : R == 16 ? pre.rc[0] : pick4(pre.rc, t);
+                        const float rs = !PRE ? a.rope_sin[(size_t)pos * half + j] : R == 16 ? pre.rs[0] : pick4(pre.rs, t);
                         rope_pair(va, vb, rc, rs, &oa, &ob);
                         if (head < a.nq) {
                             stf<COH>(a.q_out + head * a.hd + j, oa);
@@ -364,6 +369,15 @@ __device__ __forceinline__ void gemv_finish(const GemvArgs &a, int blk, int pos,
 // holds, and the dots are exact int32 v_dot4_i32_i8 sums, as dot_i8's i16
 // madd sums are (src/tensor.rs:144-170).
 // ---------------------------------------------------------------------------
+
+// Rows per workgroup of the int8 GEMV: every workgroup reads the whole
+// activation (and, with a fused RMSNorm, the norm weights) and reduces it
+// twice, so at 1 byte per weight a normalizing single-chunk GEMV takes 16
+// rows to keep that per-workgroup cost small against its weight bytes.
+template <int KC, int PRO>
+__host__ __device__ constexpr int gemv_rows8() {
+    return (KC == 1 && (PRO == PRO_NORM || PRO == PRO_EMBED_NORM)) ? 16 : gemv_rows<KC>();
+}
 
 template <int KC, int R>
 struct WeightRegs8 {
@@ -408,6 +422,15 @@ __device__ __forceinline__ void epi_issue_scale(const GemvArgs &a, int blk, EpiI
     }
 }
 
+// round(a * b) with the product rounded to f32 first, as the reference
+// computes (x * inv).round(): the subtraction inside round() is not allowed
+// to fuse with the multiply.
+__device__ __forceinline__ float round_product(float a, float b) {
+#pragma clang fp contract(off)
+    const float p = a * b;
+    return roundf(p);
+}
+
 // quantize_row_i8 of the activation held in registers: xs = max|x| / 127,
 // q = round(x * (1 / xs)) (half away from zero) clamped to [-127, 127], four
 // codes per int; an all-zero vector gives zero codes and xs = 0.  Every
@@ -430,7 +453,7 @@ __device__ __forceinline__ float quantize_act(const float (&xv)[KC][8], int (&xq
             uint32_t packed = 0;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float r = roundf(__fmul_rn(xv[c][4 * h + j], inv));
+                const float r = round_product(xv[c][4 * h + j], inv);
                 // `as i8` after clamp: NaN becomes 0
                 const int q = r == r ? (int)fminf(fmaxf(r, -127.0f), 127.0f) : 0;
                 packed |= ((uint32_t)q & 0xffu) << (8 * j);
@@ -457,7 +480,7 @@ __device__ __forceinline__ void gemv_dot8(const WeightRegs8<KC, R> &W, const int
         }
         acc[r] = d;
     }
-    constexpr int LR = R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
+    constexpr int LR = R == 16 ? 4 : R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
     const int sum = multi_wave_sum<R>(acc, lane);
     if ((lane & ((64 >> LR) - 1)) == 0) red[wave][lane >> (6 - LR)] = __int_as_float(sum);
 }
@@ -572,7 +595,7 @@ __device__ __forceinline__ void epi_issue_resid(const GemvArgs &a, int blk, EpiI
 }
 
 // RoPE cos/sin of the block's pairs at position pos: the R/2 pairs of a block
-// are consecutive frequencies of one head (hd/2 is a multiple of 4), so the
+// are consecutive frequencies of one head (hd/2 is a multiple of R/2), so the
 // addresses are uniform over the workgroup.
 template <int R>
 __device__ __forceinline__ void epi_load_rope(const GemvArgs &a, int blk, int pos, EpiIn &pre) {
@@ -581,15 +604,23 @@ __device__ __forceinline__ void epi_load_rope(const GemvArgs &a, int blk, int po
     const int j0 = P0 - (P0 / half) * half;
     const float *cb = a.rope_cos + (size_t)pos * half + j0;
     const float *sb = a.rope_sin + (size_t)pos * half + j0;
+    if constexpr (R == 16) {
+        // eight pairs: one vector load per thread; eight scalar pairs and a
+        // per-thread select would be kept in LDS by the compiler
+        const int t = threadIdx.x;
+        pre.rc[0] = t < 8 ? cb[t] : 0.0f;
+        pre.rs[0] = t < 8 ? sb[t] : 0.0f;
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        pre.rc[i] = i < R / 2 ? cb[i] : 0.0f;
-        pre.rs[i] = i < R / 2 ? sb[i] : 0.0f;
+        for (int i = 0; i < 4; i++) {
+            pre.rc[i] = i < R / 2 ? cb[i] : 0.0f;
+            pre.rs[i] = i < R / 2 ? sb[i] : 0.0f;
+        }
+        // pin the (scalar) loads here rather than letting them sink into the
+        // epilogue, where their latency would add to the kernel's tail
+#pragma unroll
+        for (int i = 0; i < 4; i++) asm volatile("" ::"s"(pre.rc[i]), "s"(pre.rs[i]));
     }
-    // pin the (scalar) loads here rather than letting them sink into the
-    // epilogue, where their latency would add to the kernel's tail
-#pragma unroll
-    for (int i = 0; i < 4; i++) asm volatile("" ::"s"(pre.rc[i]), "s"(pre.rs[i]));
 }
 
 }  // namespace tmg

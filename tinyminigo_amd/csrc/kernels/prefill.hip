@@ -84,10 +84,11 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &a, int mb, int n, con
     f32x4 v = acc;
     if (a.wscale) {
         // int8 weights: the row scale at write-back, y = acc * scale[o]
-        // (src/tensor.rs:839-840)
+        // (src/tensor.rs:839-840), rounded before the residual add
+#pragma clang fp contract(off)
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            if (mb + i < a.M) v[i] = __fmul_rn(v[i], a.wscale[mb + i]);
+            if (mb + i < a.M) v[i] = v[i] * a.wscale[mb + i];
     }
     if constexpr (EPI == GEPI_STORE || EPI == GEPI_RESID) {
         float *yr = a.y + (size_t)n * a.M;
