@@ -150,15 +150,16 @@ def gemv_sweep(T):
     return res
 
 
-TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_1b_gemv_traffic.md")
+TRAFFIC_FILES = {w: os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f)
+                 for w, f in (("bf16", "decode_1b_gemv_traffic.md"), ("i8", "decode_1b_i8_gemv_traffic.md"))}
 
 
-def pmc_traffic(kernel):
+def pmc_traffic(kernel, weights="bf16"):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
     summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known size);
     None when the summary has no line for it."""
     try:
-        for line in open(TRAFFIC_FILE):
+        for line in open(TRAFFIC_FILES[weights]):
             if line.startswith("traffic-bytes-per-launch:"):
                 f = dict(kv.split("=", 1) for kv in line.split(":", 1)[1].split())
                 if f.get("kernel") == kernel:
@@ -291,7 +292,7 @@ def main():
     kernels = {k: {"launches": n, "avg_us": round(ms * 1e3, 2),
                    "GB_s": round(b / (ms * 1e-3) / 1e9, 1) if b else None,
                    "share": round(n * ms / step_kern_ms, 3)} for k, (n, b, ms) in per.items()}
-    traffic = pmc_traffic(name) if (args.workload == "1b" and not i8) else None
+    traffic = pmc_traffic(name, args.weights) if args.workload == "1b" else None
 
     sweep = None if (args.no_sweep or args.workload != "1b" or i8) else gemv_sweep(T)
 
