@@ -189,6 +189,8 @@ def main():
     ap.add_argument("--weights", choices=["bf16", "i8"], default="bf16",
                     help="i8: load with TMG_I8=1, the reference's int8 weight-only mode (per-row int8 q/k/v/o/"
                          "gate/up/down, BF16 lm_head); the CPU baseline then times the oracle's int8 path")
+    ap.add_argument("--format", choices=["safetensors", "tmb"], default="safetensors",
+                    help="tmb: repack the model into a TMB1 file once (the reference's --repack) and load that")
     ap.add_argument("--model-dir", default=os.environ.get("TMG_MODEL_DIR",
                                                            os.path.join(tempfile.gettempdir(), "tmg_models")))
     args = ap.parse_args()
@@ -219,8 +221,17 @@ def main():
         os.environ["TMG_I8"] = "1"  # read by tmg_model_load, as the reference reads it at load
     else:
         os.environ.pop("TMG_I8", None)
-    m = T.Model.load(path)
-    log(f"model loaded ({args.weights} weights)")
+    load_path = path
+    if args.format == "tmb":
+        load_path = os.path.splitext(path)[0] + ".tmb"
+        if not os.path.exists(load_path) or os.path.getmtime(load_path) < os.path.getmtime(path):
+            T.repack_tmb(path, load_path + ".part")
+            os.replace(load_path + ".part", load_path)
+    t0 = time.perf_counter()
+    m = T.Model.load(load_path)
+    sync()
+    load_s = time.perf_counter() - t0
+    log(f"model loaded ({args.weights} weights, {args.format}) in {load_s:.2f} s")
 
     # prefill tok/s: median over repetitions on fresh caches (one for 8k)
     pf = []
@@ -328,6 +339,8 @@ def main():
                       "exact int32 dots; BF16 lm_head; f32 KV cache" if i8 else
                       "BF16 weights, f32 activations/accumulation, f32 KV cache"),
         },
+        "load_s": round(load_s, 3),
+        "format": args.format,
         "prefill_tok_s": round(P / prefill_s, 1),
         "prefill_ms": round(prefill_s * 1e3, 3),
         "prefill_tflops": round(wl.prefill_flops(P) / prefill_s / 1e12, 2),

@@ -89,6 +89,23 @@ int tmg_config_load(const char *config_json_path, tmg_config *out);
  * arithmetic), prefill multiplies by the same codes, dequantized, in f32
  * (src/tensor.rs:795-858); lm_head stays BF16. */
 int tmg_model_load(const char *safetensors_path, int device, tmg_model **out);
+
+/* A TMB1 file (reference src/tmb.rs) is accepted by tmg_model_load too: a
+ * file that starts with "TMB1" is read as load_model_tmb does
+ * (src/model.rs:90-179) -- config from the file, BF16 weight views, f32
+ * embedding and norms -- and TMG_I8 does not apply to it. */
+
+/* write_tmb (src/tmb.rs:137-262), the reference's `--repack`: converts the
+ * safetensors model (config.json next to it) into a TMB1 file.  Host only. */
+int tmg_tmb_repack(const char *safetensors_path, const char *tmb_path);
+
+/* The config a TMB1 file carries (parse_tmb_header + ModelConfig::from_json,
+ * src/tmb.rs:81-120, src/config.rs:37-91).  Host only.  As in the
+ * reference, the EOS ids written under "eos_token_ids" are not read back
+ * (from_json reads "eos_token_id"), so n_eos is 0 for files this or the
+ * reference's writer produced.  tied_lm_head is 1 when the file has no
+ * lm_head.weight. */
+int tmg_tmb_config(const char *tmb_path, tmg_config *out);
 void tmg_model_free(tmg_model *model);
 int tmg_model_config(const tmg_model *model, tmg_config *out);
 

@@ -325,6 +325,14 @@ def load_config(path: str) -> Config:
             cfg = json.loads(f.read().decode())
     except OSError as e:
         raise OracleError(f"reading config {path}: {e}")
+    return config_from_json(cfg)
+
+
+def config_from_json(cfg) -> Config:
+    """The field rules of ModelConfig::load, which ModelConfig::from_json
+    (src/config.rs:37-91) repeats for a TMB file's embedded config."""
+    if not isinstance(cfg, dict):
+        cfg = {}
 
     def need(key):
         v = _as_u64(cfg.get(key))
@@ -571,7 +579,15 @@ class OracleModel:
 
     @classmethod
     def load(cls, model_path: str, i8: bool = False) -> "OracleModel":
-        """Model::load -> load_model_safetensors (src/model.rs:181-244)."""
+        """Model::load -> load_model (src/model.rs:90-96): a TMB1 file goes to
+        load_model_tmb (oracle/tmb.py; no int8 path there), anything else to
+        load_model_safetensors (src/model.rs:181-244)."""
+        with open(model_path, "rb") as f:
+            head = f.read(4)
+        if head == b"TMB1":
+            from oracle import tmb
+            config, tensors = tmb.load_model_tmb(model_path)
+            return cls(config, tensors)
         cpath = os.path.join(os.path.dirname(os.path.abspath(model_path)), "config.json")
         if not os.path.exists(cpath):
             raise OracleError(f"config.json not found next to {model_path}")

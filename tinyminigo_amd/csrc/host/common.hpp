@@ -43,11 +43,17 @@ class SafeTensorsFile {
 
     // Returns TMG_OK or an error code (message via set_error).
     int open(const std::string &path);
+    // A TMB1 file (reference src/tmb.rs) seen through the same interface:
+    // every index entry becomes a 1-D tensor, BF16 for the weight matrices
+    // and F32 for the embedding and norms, as the writer stores them.  The
+    // embedded config is parsed into *cfg.
+    int open_tmb(const std::string &path, tmg_config *cfg);
     const TensorEntry *find(const std::string &name) const;
     const uint8_t *data(const TensorEntry &e) const { return base_ + data_off_ + e.begin; }
     const std::vector<TensorEntry> &entries() const { return entries_; }
 
   private:
+    int map_file(const std::string &path);
     std::string path_;
     uint8_t *base_ = nullptr;
     size_t size_ = 0;
@@ -66,6 +72,17 @@ float f16_to_f32(uint16_t h);
 // ---- config (reference src/config.rs:112-184) ----------------------------
 
 int config_load(const std::string &path, tmg_config *out);
+struct JsonValue;
+int config_from_json(const JsonValue &cfg, tmg_config *out);
+
+// ---- TMB1 (reference src/tmb.rs) --------------------------------------------
+
+// True when the file starts with the TMB1 magic (reference is_tmb,
+// src/model.rs:98-103).
+bool is_tmb(const std::string &path);
+// write_tmb (src/tmb.rs:137-262): repack a safetensors model (config.json
+// next to it) into a TMB1 file.
+int tmb_write(const std::string &src, const std::string &dst);
 // config_path_for_model: <dir of model>/config.json if it exists.
 bool config_path_for_model(const std::string &model_path, std::string *out);
 

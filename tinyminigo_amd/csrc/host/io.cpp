@@ -51,7 +51,7 @@ static uint64_t dtype_size(const std::string &s) {
     return 0;
 }
 
-int SafeTensorsFile::open(const std::string &path) {
+int SafeTensorsFile::map_file(const std::string &path) {
     path_ = path;
     int fd = ::open(path.c_str(), O_RDONLY);
     if (fd < 0) return set_error(TMG_E_IO, "opening " + path + ": " + strerror(errno));
@@ -61,14 +61,21 @@ int SafeTensorsFile::open(const std::string &path) {
         return set_error(TMG_E_IO, "stat " + path + ": " + strerror(errno));
     }
     size_ = (size_t)st.st_size;
-    if (size_ < 8) {
+    if (size_ == 0) {
         ::close(fd);
-        return set_error(TMG_E_FORMAT, "safetensors file too small: " + path);
+        return TMG_OK;
     }
     void *m = mmap(nullptr, size_, PROT_READ, MAP_PRIVATE | MAP_POPULATE, fd, 0);
     ::close(fd);
     if (m == MAP_FAILED) return set_error(TMG_E_IO, "mmapping " + path + ": " + strerror(errno));
     base_ = (uint8_t *)m;
+    return TMG_OK;
+}
+
+int SafeTensorsFile::open(const std::string &path) {
+    int rc = map_file(path);
+    if (rc) return rc;
+    if (size_ < 8) return set_error(TMG_E_FORMAT, "safetensors file too small: " + path);
     uint64_t n;
     memcpy(&n, base_, 8);  // little-endian header length
     if (n > size_ - 8) return set_error(TMG_E_FORMAT, "safetensors header truncated: " + path);
@@ -106,6 +113,89 @@ int SafeTensorsFile::open(const std::string &path) {
         entries_.push_back(std::move(e));
     }
     return TMG_OK;
+}
+
+// parse_tmb_header (src/tmb.rs:81-120) with every read bounds-checked: the
+// reference slices the map and panics on a short file; here that is a
+// format error.  Tensor ranges are checked up front, where the reference
+// checks them when a tensor is first borrowed.
+static bool tmb_is_bf16(const std::string &name) {
+    auto ends = [&](const char *suf) {
+        size_t n = strlen(suf);
+        return name.size() >= n && name.compare(name.size() - n, n, suf) == 0;
+    };
+    return ends("_proj.weight") || name == "lm_head.weight";
+}
+
+int SafeTensorsFile::open_tmb(const std::string &path, tmg_config *cfg) {
+    int rc = map_file(path);
+    if (rc) return rc;
+    const std::string where = " in " + path;
+    if (size_ < 16) return set_error(TMG_E_FORMAT, "TMB file too small" + where);
+    if (memcmp(base_, "TMB1", 4) != 0) return set_error(TMG_E_FORMAT, "not a TMB1 file (wrong magic)" + where);
+    uint64_t cfg_len;
+    uint32_t n;
+    memcpy(&cfg_len, base_ + 4, 8);
+    memcpy(&n, base_ + 12, 4);
+    uint64_t pos = 16;
+    if (cfg_len > size_ - pos) return set_error(TMG_E_FORMAT, "TMB config extends past the end of the file" + where);
+    JsonValue cj;
+    std::string err;
+    if (!json_parse((const char *)base_ + pos, (size_t)cfg_len, &cj, &err))
+        return set_error(TMG_E_FORMAT, "TMB config JSON: " + err + where);
+    pos += cfg_len;
+    if (size_ - pos < 8) return set_error(TMG_E_FORMAT, "TMB weights length missing" + where);
+    uint64_t weights_len;
+    memcpy(&weights_len, base_ + pos, 8);
+    const uint64_t weights_off = (pos + 8 + 7) & ~(uint64_t)7;
+    if (weights_off > size_ || weights_len > size_ - weights_off)
+        return set_error(TMG_E_FORMAT, "TMB weights section extends past the end of the file" + where);
+    pos = weights_off + weights_len;
+    entries_.clear();
+    index_.clear();
+    for (uint32_t i = 0; i < n; i++) {
+        uint32_t name_len;
+        if (size_ - pos < 4) return set_error(TMG_E_FORMAT, "TMB index truncated" + where);
+        memcpy(&name_len, base_ + pos, 4);
+        pos += 4;
+        if (size_ - pos < (uint64_t)name_len + 16) return set_error(TMG_E_FORMAT, "TMB index truncated" + where);
+        TensorEntry e;
+        e.name.assign((const char *)base_ + pos, name_len);
+        pos += name_len;
+        uint64_t off, len;
+        memcpy(&off, base_ + pos, 8);
+        memcpy(&len, base_ + pos + 8, 8);
+        pos += 16;
+        if (off > size_ || len > size_ - off)
+            return set_error(TMG_E_FORMAT, "TMB tensor range out of bounds: `" + e.name + "`" + where);
+        const bool bf = tmb_is_bf16(e.name);
+        if (len % (bf ? 2 : 4))
+            return set_error(TMG_E_FORMAT, std::string(bf ? "TMB BF16 tensor has odd byte length"
+                                                          : "TMB f32 tensor has non-multiple-of-4 byte length") +
+                                               ": `" + e.name + "`" + where);
+        e.dtype = bf ? DType::BF16 : DType::F32;
+        e.dtype_name = bf ? "BF16" : "F32";
+        e.shape = {len / (bf ? 2 : 4)};
+        e.begin = off;  // data section = the whole file
+        e.end = off + len;
+        auto it = index_.find(e.name);  // a repeated name: the later entry wins, as in a HashMap
+        if (it != index_.end()) {
+            entries_[it->second] = std::move(e);
+        } else {
+            index_[e.name] = entries_.size();
+            entries_.push_back(std::move(e));
+        }
+    }
+    data_off_ = 0;
+    if (cj.kind != JsonValue::Object)
+        return set_error(TMG_E_MISSING, "config missing integer field `hidden_size`");
+    return config_from_json(cj, cfg);
+}
+
+bool is_tmb(const std::string &path) {
+    std::ifstream in(path, std::ios::binary);
+    char m[4];
+    return in && in.read(m, 4) && memcmp(m, "TMB1", 4) == 0;
 }
 
 const TensorEntry *SafeTensorsFile::find(const std::string &name) const {
@@ -194,6 +284,13 @@ int config_load(const std::string &path, tmg_config *out) {
     std::string err;
     if (!json_parse(text.data(), text.size(), &cfg, &err) || cfg.kind != JsonValue::Object)
         return set_error(TMG_E_FORMAT, "parsing " + path + ": " + err);
+    return config_from_json(cfg, out);
+}
+
+// ModelConfig::load's field rules (src/config.rs:112-172), which
+// ModelConfig::from_json repeats for the config a TMB file embeds
+// (src/config.rs:37-91).
+int config_from_json(const JsonValue &cfg, tmg_config *out) {
     tmg_config c;
     memset(&c, 0, sizeof(c));
     int rc;

@@ -130,11 +130,20 @@ static int upload_raw(tmg_model *m, const void *src, size_t bytes, uint16_t **ds
 
 // Host-only phase: config.json + every tensor's presence, shape and dtype,
 // so file errors surface before any device work (and without a GPU).
+// A TMB1 file (reference load_model_tmb, src/model.rs:105-179) carries its
+// config and is read through the same tensor interface.
 static int validate_files(tmg_model *m, const std::string &path, SafeTensorsFile *f) {
-    std::string cpath;
-    if (!config_path_for_model(path, &cpath)) return set_error(TMG_E_MISSING, "config.json not found next to " + path);
-    int rc = config_load(cpath, &m->cfg);
-    if (rc) return rc;
+    int rc;
+    const bool tmb = is_tmb(path);
+    if (tmb) {
+        if ((rc = f->open_tmb(path, &m->cfg))) return rc;
+    } else {
+        std::string cpath;
+        if (!config_path_for_model(path, &cpath))
+            return set_error(TMG_E_MISSING, "config.json not found next to " + path);
+        if ((rc = config_load(cpath, &m->cfg))) return rc;
+    }
+    m->from_tmb = tmb;
     const tmg_config &c = m->cfg;
     m->H = c.hidden_size;
     m->L = c.num_hidden_layers;
@@ -156,7 +165,7 @@ static int validate_files(tmg_model *m, const std::string &path, SafeTensorsFile
     if (m->H % 32 || m->qd % 32 || m->I % 32 || m->H > 16384 || m->qd > 16384 || m->I > 16384)
         return set_error(TMG_E_INVALID, "hidden, q and intermediate sizes must be multiples of 32 and <= 16384");
     if (m->V == 0) return set_error(TMG_E_INVALID, "vocab_size is 0");
-    if ((rc = f->open(path))) return rc;
+    if (!tmb && (rc = f->open(path))) return rc;
     const uint64_t H = m->H, I = m->I, V = m->V, qd = m->qd, kvd = m->kvd;
     const TensorEntry *e;
     if ((rc = need(*f, "model.embed_tokens.weight", {V, H}, &e))) return rc;
@@ -177,7 +186,17 @@ static int validate_files(tmg_model *m, const std::string &path, SafeTensorsFile
     if (f->find("lm_head.weight")) {
         if ((rc = need_bf16(*f, "lm_head.weight", {V, H}, &e))) return rc;
     } else if (f->find("model.embed_tokens.weight")->dtype != DType::BF16) {
-        return set_error(TMG_E_DTYPE, "tied lm_head needs a BF16 embedding table on the GPU path");
+        // a tied lm_head streams the table as BF16: an F16/F32 table is
+        // accepted when every value is a BF16 value (a TMB file stores the
+        // embedding widened to f32)
+        std::vector<float> v;
+        if ((rc = tensor_to_f32(*f, *f->find("model.embed_tokens.weight"), &v))) return rc;
+        for (float x : v) {
+            uint32_t u;
+            memcpy(&u, &x, 4);
+            if (u & 0xFFFFu)
+                return set_error(TMG_E_DTYPE, "tied lm_head needs an embedding table of BF16 values on the GPU path");
+        }
     }
     return TMG_OK;
 }
@@ -188,13 +207,35 @@ static int load_model(tmg_model *m, const SafeTensorsFile &f) {
     const int group = m->nq / m->nkv;
     const uint64_t H = m->H, I = m->I, V = m->V, qd = m->qd, kvd = m->kvd;
 
-    // embedding: raw BF16 on the device, else converted to f32 as the reference does
+    // embedding: raw BF16 on the device, else f32 as the reference converts
+    // it (an F32 table -- a TMB file's -- uploads as it lies in the file);
+    // a tied lm_head streams the table as BF16, so then a table of BF16
+    // values is narrowed back exactly (validate_files checked that)
     const TensorEntry *emb;
     if ((rc = need(f, "model.embed_tokens.weight", {V, H}, &emb))) return rc;
+    const bool tied = f.find("lm_head.weight") == nullptr;
     if (emb->dtype == DType::BF16) {
         if ((rc = upload_raw(m, f.data(*emb), V * H * 2, &m->embed_bf16))) return rc;
+    } else if (emb->dtype == DType::F32 && !tied) {
+        if ((rc = dev_alloc(m, &m->embed_f32, V * H))) return rc;
+        TMG_HIP(hipMemcpy(m->embed_f32, f.data(*emb), V * H * 4, hipMemcpyHostToDevice));
     } else {
-        if ((rc = upload_f32(m, f, emb, &m->embed_f32))) return rc;
+        std::vector<float> v;
+        if ((rc = tensor_to_f32(f, *emb, &v))) return rc;
+        bool exact = true;
+        std::vector<uint16_t> nb(v.size());
+        for (size_t i = 0; i < v.size(); i++) {
+            uint32_t u;
+            memcpy(&u, &v[i], 4);
+            exact = exact && (u & 0xFFFFu) == 0;
+            nb[i] = (uint16_t)(u >> 16);
+        }
+        if (exact && tied) {
+            if ((rc = upload_raw(m, nb.data(), nb.size() * 2, &m->embed_bf16))) return rc;
+        } else {
+            if ((rc = dev_alloc(m, &m->embed_f32, v.size()))) return rc;
+            TMG_HIP(hipMemcpy(m->embed_f32, v.data(), v.size() * 4, hipMemcpyHostToDevice));
+        }
     }
 
     const int half = m->hd / 2;
@@ -888,9 +929,10 @@ extern "C" int tmg_model_load(const char *path, int device, tmg_model **out) {
     }
     m->device = device;
     {
-        // the reference's gate: std::env::var("TMG_I8") == "1" (src/model.rs:61)
+        // the reference's gate: std::env::var("TMG_I8") == "1" (src/model.rs:61);
+        // a TMB file always loads its BF16 views (load_model_tmb has no int8 path)
         const char *e = getenv("TMG_I8");
-        m->i8 = e && strcmp(e, "1") == 0;
+        m->i8 = e && strcmp(e, "1") == 0 && !m->from_tmb;
     }
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
         model_release(m);

@@ -28,6 +28,8 @@ struct tmg_model {
     };
     // int8 weight-only mode (TMG_I8=1 at load, reference src/model.rs:57-76)
     bool i8 = false;
+    // loaded from a TMB1 file
+    bool from_tmb = false;
     std::vector<Layer> layers;
     float *final_norm = nullptr;
     uint16_t *embed_bf16 = nullptr;  // [V, H] when the file stores BF16

@@ -19,7 +19,7 @@ from ._lib import (
 )
 
 __all__ = [
-    "ModelConfig", "Model", "KvCache", "GenParams", "GenOutput", "generate", "gemv_bf16", "gemv_i8", "quantize_i8",
+    "ModelConfig", "Model", "KvCache", "GenParams", "GenOutput", "generate", "gemv_bf16", "gemv_i8", "quantize_i8", "repack_tmb",
     "synth_model", "synth_tokens", "synth_normal_bf16", "synth_normal_f32", "TmgError",
 ]
 
@@ -65,6 +65,13 @@ class ModelConfig:
         """ModelConfig::load (src/config.rs:112-172)."""
         c = tmg_config()
         check(lib.tmg_config_load(path.encode(), C.byref(c)))
+        return cls._from_c(c)
+
+    @classmethod
+    def from_tmb(cls, path: str) -> "ModelConfig":
+        """The config embedded in a TMB1 file (src/tmb.rs:81-120)."""
+        c = tmg_config()
+        check(lib.tmg_tmb_config(path.encode(), C.byref(c)))
         return cls._from_c(c)
 
 
@@ -241,6 +248,11 @@ def gemv_bf16(w_dev: int, x_dev: int, y_dev: int, out: int, in_: int, stream: in
     """tensor::matmul_w (src/tensor.rs:315-338) on device pointers."""
     check(lib.tmg_gemv_bf16(C.c_void_p(w_dev), C.c_void_p(x_dev), C.c_void_p(y_dev), out, in_,
                             C.c_void_p(stream)))
+
+
+def repack_tmb(safetensors_path: str, tmb_path: str) -> None:
+    """write_tmb (src/tmb.rs:137-262): the reference's `--repack`."""
+    check(lib.tmg_tmb_repack(safetensors_path.encode(), tmb_path.encode()))
 
 
 def gemv_i8(q_dev: int, scale_dev: int, x_dev: int, y_dev: int, out: int, in_: int, stream: int = 0) -> None:
