@@ -143,6 +143,20 @@ int tmg_generate(tmg_model *model, const uint32_t *prompt, size_t n_prompt, cons
                  tmg_on_token_fn on_token, void *user, uint32_t *out_tokens, size_t out_cap, size_t *n_out,
                  float *first_logits, float *prefill_secs);
 
+/* Greedy generation for n_seq independent prompts in one batch (1..128
+ * sequences).  No counterpart in the reference, which decodes one sequence
+ * per generate call; this is the multi-sequence batching its design notes
+ * list next.  For every sequence b the ids are the ones generate
+ * (src/model.rs:614-663) gives for prompts[b] alone with temperature 0 and
+ * repetition penalty 1 -- stopping after an EOS id -- up to f32 rounding at
+ * a near tie: each decode step streams the layer weights once for all
+ * sequences (MFMA GEMM over the batch) instead of once per sequence.
+ * out_tokens is [n_seq][max_tokens]; n_out[b] receives sequence b's count;
+ * *decode_ms (may be NULL) the device time of the batched decode steps.
+ * Models loaded with TMG_I8=1 are rejected (TMG_E_INVALID). */
+int tmg_generate_batch(tmg_model *model, const uint32_t *const *prompts, const size_t *n_prompt, size_t n_seq,
+                       uint32_t max_tokens, uint32_t *out_tokens, size_t *n_out, float *decode_ms);
+
 /* Kernel level: y[out] = W[out,in] x[in] with W raw BF16 row-major and x, y
  * f32, all DEVICE pointers (reference tensor::matmul_w / matmul_w_into,
  * src/tensor.rs:315-338, BF16 case).  `stream` is a hipStream_t (NULL = the

@@ -112,6 +112,8 @@ SIGNATURES = {
         [P, PU32, C.c_size_t, C.POINTER(tmg_gen_params), ON_TOKEN, P, PU32, C.c_size_t,
          C.POINTER(C.c_size_t), PF, PF],
     ),
+    "tmg_generate_batch": (C.c_int, [P, C.POINTER(PU32), C.POINTER(C.c_size_t), C.c_size_t, C.c_uint32, PU32,
+                                     C.POINTER(C.c_size_t), PF]),
     "tmg_tmb_repack": (C.c_int, [C.c_char_p, C.c_char_p]),
     "tmg_tmb_config": (C.c_int, [C.c_char_p, C.POINTER(tmg_config)]),
     "tmg_gemv_bf16": (C.c_int, [P, P, P, C.c_uint32, C.c_uint32, P]),

@@ -1,0 +1,289 @@
+// Batched greedy decode of several independent sequences (tmg_generate_batch).
+//
+// The reference decodes one sequence at a time (generate, src/model.rs:
+// 614-663, one forward_token per step).  Here B sequences share every
+// decode step: the B input tokens form one activation block, so each layer
+// matrix is streamed from HBM once per step for all of them by the
+// short-prompt MFMA GEMM (the batched prefill's, src/tensor.rs:741-858),
+// the QKV epilogue appends each sequence's K/V at its own position in its
+// own cache, attention runs one (sequence, KV head) per workgroup over that
+// sequence's cache, and the lm_head is one GEMM over the B rows followed by
+// a per-sequence argmax.  Each sequence's ids are the ones generate gives
+// for its prompt alone (temperature 0, no penalty), up to f32 rounding at a
+// near tie.  One step is captured into a hipGraph and replayed.
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <vector>
+
+#include "model.hpp"
+
+namespace tmg {
+namespace {
+
+#define TMG_HIPB(expr)                                                                                     \
+    do {                                                                                                   \
+        hipError_t e_ = (expr);                                                                            \
+        if (e_ != hipSuccess)                                                                              \
+            return set_error(TMG_E_DEVICE, std::string("HIP error ") + hipGetErrorString(e_) + " in " #expr); \
+    } while (0)
+
+// Device allocations of one call, released on every exit path.
+struct Allocs {
+    std::vector<void *> p;
+    ~Allocs() {
+        for (void *q : p) (void)hipFree(q);
+    }
+    template <class T>
+    int get(T **out, size_t count) {
+        void *q = nullptr;
+        if (hipMalloc(&q, (count ? count : 1) * sizeof(T)) != hipSuccess)
+            return set_error(TMG_E_NOMEM, "batched decode: allocation of " + std::to_string(count * sizeof(T)) +
+                                              " bytes failed");
+        p.push_back(q);
+        *out = (T *)q;
+        return TMG_OK;
+    }
+};
+
+struct Batch {
+    int B = 0;
+    uint32_t max_pos = 0;
+    float *k = nullptr, *v = nullptr;  // [B][L][max_pos][kvd]
+    float **kptr = nullptr, **vptr = nullptr;  // device [B]: sequence b's cache base
+    int *tokens = nullptr, *pos = nullptr, *plen = nullptr, *out = nullptr;
+    int out_stride = 0;
+    float *x = nullptr, *q = nullptr, *logits = nullptr;
+    uint16_t *hi = nullptr, *lo = nullptr, *ahi = nullptr, *alo = nullptr, *hhi = nullptr, *hlo = nullptr;
+};
+
+int enqueue_batch_step(tmg_model *m, const Batch &bt) {
+    hipStream_t s = m->stream;
+    const int B = bt.B, H = m->H, I = m->I, qd = m->qd, kvd = m->kvd;
+    const float eps = m->cfg.rms_norm_eps;
+    TMG_HIPB(launch_embed_gather(bt.tokens, B, H, m->embed_bf16, m->embed_f32, bt.x, s));
+    for (int l = 0; l < m->L; l++) {
+        const tmg_model::Layer &ly = m->layers[l];
+        const size_t layer_off = (size_t)l * bt.max_pos * kvd;
+        // forward_token's RMSNorm association, (v*inv)*w (src/tensor.rs:975)
+        TMG_HIPB(launch_rmsnorm_split(bt.x, ly.in_norm, eps, B, H, bt.hi, bt.lo, s, true));
+        GemmArgs g{};
+        g.W = ly.qkv;
+        g.Bhi = bt.hi;
+        g.Blo = bt.lo;
+        g.M = m->qkv_rows;
+        g.N = B;
+        g.K = H;
+        g.rope_cos = m->rope_cos;
+        g.rope_sin = m->rope_sin;
+        g.hd = m->hd;
+        g.nq = m->nq;
+        g.nkv = m->nkv;
+        g.q_out = bt.q;
+        g.pos_seq = bt.pos;
+        g.k_seq = bt.kptr;
+        g.v_seq = bt.vptr;
+        g.kv_layer_off = layer_off;
+        g.part = m->pf_part;
+        g.cnt = m->pf_cnt;
+        TMG_HIPB(launch_gemm(GEPI_QKV, g, s));
+
+        AttnArgs aa{};
+        aa.q = bt.q;
+        aa.nq = m->nq;
+        aa.nkv = m->nkv;
+        aa.hd = m->hd;
+        aa.T = B;
+        aa.scale = 1.0f / sqrtf((float)m->hd);
+        aa.nsplit = 1;
+        aa.pos_seq = bt.pos;
+        aa.k_seq = bt.kptr;
+        aa.v_seq = bt.vptr;
+        aa.kv_layer_off = layer_off;
+        aa.part = m->attn_part;
+        aa.part_ml = m->attn_ml;
+        aa.out_hi = bt.ahi;
+        aa.out_lo = bt.alo;
+        TMG_HIPB(launch_attn(aa, s));
+
+        GemmArgs o{};
+        o.W = ly.o;
+        o.Bhi = bt.ahi;
+        o.Blo = bt.alo;
+        o.M = H;
+        o.N = B;
+        o.K = qd;
+        o.y = bt.x;
+        o.part = m->pf_part;
+        o.cnt = m->pf_cnt;
+        TMG_HIPB(launch_gemm(GEPI_RESID, o, s));
+
+        TMG_HIPB(launch_rmsnorm_split(bt.x, ly.post_norm, eps, B, H, bt.hi, bt.lo, s, true));
+        GemmArgs gu{};
+        gu.W = ly.gu;
+        gu.Bhi = bt.hi;
+        gu.Blo = bt.lo;
+        gu.M = 2 * I;
+        gu.N = B;
+        gu.K = H;
+        gu.h_hi = bt.hhi;
+        gu.h_lo = bt.hlo;
+        gu.part = m->pf_part;
+        gu.cnt = m->pf_cnt;
+        TMG_HIPB(launch_gemm(GEPI_SWIGLU, gu, s));
+
+        GemmArgs d{};
+        d.W = ly.down;
+        d.Bhi = bt.hhi;
+        d.Blo = bt.hlo;
+        d.M = H;
+        d.N = B;
+        d.K = I;
+        d.y = bt.x;
+        d.part = m->pf_part;
+        d.cnt = m->pf_cnt;
+        TMG_HIPB(launch_gemm(GEPI_RESID, d, s));
+    }
+    TMG_HIPB(launch_rmsnorm_split(bt.x, m->final_norm, eps, B, H, bt.hi, bt.lo, s, true));
+    GemmArgs lm{};  // no split-K: the lm_head's row tiles alone fill the GPU
+    lm.W = m->lm_head;
+    lm.Bhi = bt.hi;
+    lm.Blo = bt.lo;
+    lm.M = m->V;
+    lm.N = B;
+    lm.K = H;
+    lm.y = bt.logits;
+    TMG_HIPB(launch_gemm(GEPI_STORE, lm, s));
+    BatchSelectArgs sa{bt.logits, m->V, B, bt.tokens, bt.pos, bt.plen, bt.out, bt.out_stride};
+    TMG_HIPB(launch_batch_select(sa, s));
+    return TMG_OK;
+}
+
+}  // namespace
+}  // namespace tmg
+
+using namespace tmg;
+
+extern "C" int tmg_generate_batch(tmg_model *m, const uint32_t *const *prompts, const size_t *n_prompt, size_t n_seq,
+                                  uint32_t max_tokens, uint32_t *out_tokens, size_t *n_out, float *decode_ms) {
+    clear_error();
+    if (!m || !prompts || !n_prompt || !n_out || (max_tokens && !out_tokens))
+        return set_error(TMG_E_INVALID, "bad argument to tmg_generate_batch");
+    if (n_seq == 0 || n_seq > (size_t)kMaxBatch)
+        return set_error(TMG_E_INVALID, "n_seq must be 1.." + std::to_string(kMaxBatch));
+    for (size_t b = 0; b < n_seq; b++) {
+        n_out[b] = 0;
+        if (n_prompt[b] == 0) return set_error(TMG_E_EMPTY, "empty prompt");
+        if (!prompts[b]) return set_error(TMG_E_INVALID, "null prompt");
+        for (size_t i = 0; i < n_prompt[b]; i++)
+            if (prompts[b][i] >= (uint32_t)m->V) return set_error(TMG_E_INVALID, "prompt token id out of range");
+    }
+    if (m->i8)
+        return set_error(TMG_E_INVALID, "batched decode multiplies BF16 weights: load the model without TMG_I8");
+    if (decode_ms) *decode_ms = 0.0f;
+    if (max_tokens == 0) return TMG_OK;
+    (void)hipSetDevice(m->device);
+
+    const int B = (int)n_seq;
+    size_t longest = 0;
+    for (size_t b = 0; b < n_seq; b++) longest = std::max(longest, n_prompt[b]);
+    if (longest + max_tokens + 1 > 0x7fffffff) return set_error(TMG_E_INVALID, "sequence too long");
+    Batch bt;
+    bt.B = B;
+    bt.max_pos = (uint32_t)(longest + max_tokens);
+    bt.out_stride = (int)max_tokens;
+    const size_t kv = (size_t)B * m->L * bt.max_pos * m->kvd;
+    const int wide = std::max(std::max(m->H, m->qd), m->I);
+    Allocs al;
+    int rc;
+    DevState *st = nullptr;
+    if ((rc = al.get(&bt.k, kv)) || (rc = al.get(&bt.v, kv)) || (rc = al.get(&bt.kptr, B)) ||
+        (rc = al.get(&bt.vptr, B)) || (rc = al.get(&bt.tokens, B)) || (rc = al.get(&bt.pos, B)) ||
+        (rc = al.get(&bt.plen, B)) || (rc = al.get(&bt.out, (size_t)B * max_tokens)) ||
+        (rc = al.get(&bt.x, (size_t)B * m->H)) || (rc = al.get(&bt.q, (size_t)B * m->qd)) ||
+        (rc = al.get(&bt.logits, (size_t)B * m->V)) || (rc = al.get(&bt.hi, (size_t)B * wide)) ||
+        (rc = al.get(&bt.lo, (size_t)B * wide)) || (rc = al.get(&bt.ahi, (size_t)B * m->qd)) ||
+        (rc = al.get(&bt.alo, (size_t)B * m->qd)) || (rc = al.get(&bt.hhi, (size_t)B * m->I)) ||
+        (rc = al.get(&bt.hlo, (size_t)B * m->I)) || (rc = al.get(&st, B)))
+        return rc;
+    if ((rc = ensure_rope(m, (int)bt.max_pos + 1))) return rc;
+    std::vector<float *> kp(B), vp(B);
+    std::vector<int> pl(B);
+    for (int b = 0; b < B; b++) {
+        kp[b] = bt.k + (size_t)b * m->L * bt.max_pos * m->kvd;
+        vp[b] = bt.v + (size_t)b * m->L * bt.max_pos * m->kvd;
+        pl[b] = (int)n_prompt[b];
+    }
+    TMG_HIPB(hipMemcpy(bt.kptr, kp.data(), B * sizeof(float *), hipMemcpyHostToDevice));
+    TMG_HIPB(hipMemcpy(bt.vptr, vp.data(), B * sizeof(float *), hipMemcpyHostToDevice));
+    TMG_HIPB(hipMemcpy(bt.plen, pl.data(), B * 4, hipMemcpyHostToDevice));
+    TMG_HIPB(hipMemcpy(bt.pos, pl.data(), B * 4, hipMemcpyHostToDevice));
+
+    // prefill each prompt into its cache (forward_seq), first id = argmax
+    for (int b = 0; b < B; b++) {
+        tmg_cache c;  // a view of sequence b's region of the batch caches
+        c.model = m;
+        c.max_pos = bt.max_pos;
+        c.k = kp[b];
+        c.v = vp[b];
+        c.st = st + b;
+        if ((rc = run_prefill(m, &c, prompts[b], n_prompt[b]))) return rc;
+        TMG_HIPB(launch_batch_first(m->argmax_part, m->argmax_nparts, m->V, b, bt.tokens, bt.out, bt.out_stride,
+                                    m->stream));
+        // run_prefill stages the prompt through the model's pinned buffer:
+        // the next prompt may overwrite it only after these copies ran
+        TMG_HIPB(hipStreamSynchronize(m->stream));
+    }
+
+    // the decode steps: one captured step, replayed
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    auto cleanup = [&]() {
+        if (exec) (void)hipGraphExecDestroy(exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        if (e0) (void)hipEventDestroy(e0);
+        if (e1) (void)hipEventDestroy(e1);
+        (void)hipStreamSynchronize(m->stream);
+    };
+    struct Guard {
+        decltype(cleanup) &f;
+        ~Guard() { f(); }
+    } guard{cleanup};
+    TMG_HIPB(hipEventCreate(&e0));
+    TMG_HIPB(hipEventCreate(&e1));
+    if (max_tokens > 1) {
+        TMG_HIPB(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+        rc = enqueue_batch_step(m, bt);
+        hipError_t e = hipStreamEndCapture(m->stream, &graph);
+        if (rc) return rc;
+        TMG_HIPB(e);
+        TMG_HIPB(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+    }
+    TMG_HIPB(hipEventRecord(e0, m->stream));
+    for (uint32_t i = 1; i < max_tokens; i++) TMG_HIPB(hipGraphLaunch(exec, m->stream));
+    TMG_HIPB(hipEventRecord(e1, m->stream));
+    TMG_HIPB(hipEventSynchronize(e1));
+    if (decode_ms) TMG_HIPB(hipEventElapsedTime(decode_ms, e0, e1));
+
+    std::vector<int> ids((size_t)B * max_tokens);
+    TMG_HIPB(hipMemcpy(ids.data(), bt.out, ids.size() * 4, hipMemcpyDeviceToHost));
+    const tmg_config &cfg = m->cfg;
+    for (int b = 0; b < B; b++) {
+        size_t n = 0;
+        for (; n < max_tokens; n++) {
+            const uint32_t t = (uint32_t)ids[(size_t)b * max_tokens + n];
+            out_tokens[(size_t)b * max_tokens + n] = t;
+            bool eos = false;
+            for (uint32_t e = 0; e < cfg.n_eos; e++) eos = eos || cfg.eos_token_ids[e] == t;
+            if (eos) {  // generate stops after emitting an EOS id (src/model.rs:649-651)
+                n++;
+                break;
+            }
+        }
+        n_out[b] = n;
+    }
+    return TMG_OK;
+}

@@ -99,6 +99,9 @@ namespace tmg {
 // splits (at most kMaxSplits).  Up to kFusedSplits the merge runs in the
 // o_proj GEMV prologue; above that a combine kernel runs first.
 constexpr int kMaxSplits = 32;
+// Sequences per tmg_generate_batch call (the short-prompt GEMM takes up to
+// 255 token rows; the bound keeps the per-call KV allocation in view).
+constexpr int kMaxBatch = 128;
 
 // Launch filter used by tmg_profile_decode_step: every kernel of the step is
 // announced with its name and algorithmic bytes; when `only` is set, just the

@@ -75,8 +75,8 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
     const int kvd = a.nkv * HD;
     const int qd = a.nq * HD;
     // lane lt owns dims (v TS + lt) 4 .. + 3 for v < VPL
-    const float *kbase = a.k_cache + g * HD + lt * 4;
-    const float *vbase = a.v_cache + g * HD + lt * 4;
+    const float *kbase = (a.k_seq ? a.k_seq[ti] + a.kv_layer_off : a.k_cache) + g * HD + lt * 4;
+    const float *vbase = (a.v_seq ? a.v_seq[ti] + a.kv_layer_off : a.v_cache) + g * HD + lt * 4;
 
     float4 qv[GROUP][VPL];
     const float *qrow = a.q + (size_t)ti * qd;

@@ -177,7 +177,7 @@ __global__ __launch_bounds__(kBlock) void attn_kernel(const AttnArgs a) {
             return;
         }
     }
-    const int qpos = (a.pos_dev ? *a.pos_dev : a.start) + ti;
+    const int qpos = a.pos_seq ? a.pos_seq[ti] : (a.pos_dev ? *a.pos_dev : a.start) + ti;
     const int active = active_splits(qpos + 1, a.nsplit);
     if (split >= active) return;
     attn_item<HD, GROUP, false>(a, split, g, ti, qpos, active, sm);
@@ -276,7 +276,77 @@ __global__ __launch_bounds__(1024) void finalize_kernel(const FinalizeArgs a) {
     st->argmax_key = kArgmaxInit;
 }
 
+// ---------------------------------------------------------------------------
+// Batched greedy decode: the per-sequence argmax of a [B][V] logit block
+// (generate's `next = argmax(logits)`, src/model.rs:636-637, for every
+// sequence), one workgroup per sequence, same packed-key tie rule as the
+// single-sequence path (largest value, lowest id; all -inf/NaN -> id 0).
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(1024) void batch_select_kernel(const BatchSelectArgs a) {
+    __shared__ unsigned long long red[16];
+    const int b = blockIdx.x;
+    const float *row = a.logits + (size_t)b * a.V;
+    unsigned long long best = kArgmaxInit;
+    for (int i = threadIdx.x; i < a.V; i += blockDim.x) {
+        const float v = row[i];
+        if (v == v) {
+            const unsigned long long k = argmax_key(v, (uint32_t)i);
+            best = k > best ? k : best;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = shfl_xor_u64(best, off);
+        best = o > best ? o : best;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) best = red[w] > best ? red[w] : best;
+    int tok = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
+    if (tok < 0 || tok >= a.V) tok = 0;
+    a.tokens[b] = tok;
+    const int p = a.pos[b];
+    const int i = p - a.plen[b] + 1;  // index of the id chosen from position p's logits
+    if (i >= 0 && i < a.out_stride) a.out[(size_t)b * a.out_stride + i] = tok;
+    a.pos[b] = p + 1;
+}
+
+__global__ __launch_bounds__(1024) void batch_first_kernel(const unsigned long long *part, int nparts, int V, int b,
+                                                           int *tokens, int *out, int out_stride) {
+    __shared__ unsigned long long red[16];
+    unsigned long long best = kArgmaxInit;
+    for (int i = threadIdx.x; i < nparts; i += blockDim.x) best = part[i] > best ? part[i] : best;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = shfl_xor_u64(best, off);
+        best = o > best ? o : best;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) best = red[w] > best ? red[w] : best;
+    int tok = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
+    if (tok < 0 || tok >= V) tok = 0;
+    tokens[b] = tok;
+    out[(size_t)b * out_stride] = tok;
+}
+
 }  // namespace
+
+hipError_t launch_batch_select(const BatchSelectArgs &a, hipStream_t s) {
+    if (a.B <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(batch_select_kernel, dim3(a.B), dim3(1024), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_batch_first(const unsigned long long *argmax_part, int nparts, int V, int b, int *tokens, int *out,
+                              int out_stride, hipStream_t s) {
+    hipLaunchKernelGGL(batch_first_kernel, dim3(1), dim3(1024), 0, s, argmax_part, nparts, V, b, tokens, out,
+                       out_stride);
+    return hipGetLastError();
+}
 
 hipError_t launch_gemv(int pro, int epi, const GemvArgs &a, hipStream_t s) {
 #define TMG_PE(P, E) \

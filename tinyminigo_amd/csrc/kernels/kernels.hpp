@@ -88,6 +88,13 @@ struct AttnArgs {
     float *part_ml;   // [T][nkv][nsplit][group][2] (max of the log2-scaled scores, sum)
     float *out_f32;   // [T][nq*hd] when one split covers the row, or null
     uint16_t *out_hi, *out_lo;  // [T][nq*hd] split-bf16 output (prefill), or null
+    // several sequences at once (batched decode, nsplit 1): query row ti is
+    // sequence ti at position pos_seq[ti] over its own cache k_seq[ti] /
+    // v_seq[ti] + kv_layer_off
+    const int *pos_seq;
+    float *const *k_seq;
+    float *const *v_seq;
+    size_t kv_layer_off;
     // MFMA prefill attention: the cache rows [0, start+T) as split-bf16, keys
     // [pos][nkv*hd] and values transposed [nkv][hd][vt_pitch]
     const uint16_t *kh, *kl, *vth, *vtl;
@@ -126,15 +133,34 @@ struct FinalizeArgs {
 
 hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t s);
 
+// Batched greedy decode (several sequences per step): the argmax of each of
+// the B logit rows [B][V] becomes that sequence's next input token, is
+// written to out[b * out_stride + pos[b] - plen[b]] when that index is below
+// out_stride, and pos[b] advances.
+struct BatchSelectArgs {
+    const float *logits;
+    int V, B;
+    int *tokens, *pos;
+    const int *plen;
+    int *out;
+    int out_stride;
+};
+hipError_t launch_batch_select(const BatchSelectArgs &a, hipStream_t s);
+// The first generated id of sequence b from a prefill's per-workgroup argmax
+// keys: tokens[b] = id, out[b * out_stride] = id.
+hipError_t launch_batch_first(const unsigned long long *argmax_part, int nparts, int V, int b, int *tokens, int *out,
+                              int out_stride, hipStream_t s);
+
 // ---- prefill -------------------------------------------------------------
 
 hipError_t launch_embed_gather(const int *tokens, int T, int H, const uint16_t *embed_bf16, const float *embed_f32,
                                float *x, hipStream_t s);
 
-// Row-wise RMSNorm with the batch association v*(inv*w), written as
-// split-bf16 hi/lo operands for the MFMA GEMM.
+// Row-wise RMSNorm with the batch association v*(inv*w) (or, with
+// decode_assoc, forward_token's (v*inv)*w), written as split-bf16 hi/lo
+// operands for the MFMA GEMM.
 hipError_t launch_rmsnorm_split(const float *x, const float *w, float eps, int T, int H, uint16_t *hi, uint16_t *lo,
-                                hipStream_t s);
+                                hipStream_t s, bool decode_assoc = false);
 
 enum GemmEpi { GEPI_STORE = 0, GEPI_RESID = 1, GEPI_SWIGLU = 2, GEPI_QKV = 3 };
 
@@ -152,6 +178,13 @@ struct GemmArgs {
     int hd, nq, nkv;
     float *q_out;  // [N][nq*hd]
     float *k_cache, *v_cache;
+    // several sequences at once (batched decode): token n is sequence n at
+    // position pos_seq[n], its K/V rows go to k_seq[n] / v_seq[n] +
+    // kv_layer_off; null pos_seq: one sequence, token n at start + n
+    const int *pos_seq;
+    float *const *k_seq;
+    float *const *v_seq;
+    size_t kv_layer_off;
     // split-K workspace of the short-prompt kernel: partial tiles and one
     // arrival counter per quarter tile (zero between launches; each launch
     // leaves them zero).  Null disables split-K.

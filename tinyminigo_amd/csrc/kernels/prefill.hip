@@ -28,13 +28,19 @@ __global__ __launch_bounds__(kBlock) void embed_gather_kernel(const int *tokens,
         x[(size_t)row * H + i] = eb ? bf16_to_f32(eb[(size_t)tok * H + i]) : ef[(size_t)tok * H + i];
 }
 
+// v*(inv*w) (rms_norm_batch, src/tensor.rs:951) or (v*inv)*w (rms_norm_into,
+// src/tensor.rs:975).
+__device__ __forceinline__ float norm_scale(float v, float inv, float w, int decode_assoc) {
+    return decode_assoc ? (v * inv) * w : v * (inv * w);
+}
+
 // rms_norm_batch (src/tensor.rs:946-954): inv = 1/sqrt(ss/n + eps), v*(inv*w).
 // One wavefront per row (four rows per workgroup), sum of squares reduced in
 // registers + DPP.  Rows of up to 4096 floats in 256-float blocks are held in
 // registers with the norm weights (every load issued up front); other widths
 // take a strided loop.
 __global__ __launch_bounds__(kBlock) void rmsnorm_split_kernel(const float *x, const float *w, float eps, int H, int T,
-                                                              uint16_t *hi, uint16_t *lo) {
+                                                              uint16_t *hi, uint16_t *lo, int decode_assoc) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= T) return;
     const float *xr = x + (size_t)row * H;
@@ -58,8 +64,10 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_split_kernel(const float *x, c
         for (int b = 0; b < 16; b++) {
             if (b < nb) {
                 const int i = b * 256 + lane * 4;
-                const float e[4] = {__fmul_rn(v[b].x, __fmul_rn(inv, wv[b].x)), __fmul_rn(v[b].y, __fmul_rn(inv, wv[b].y)),
-                                    __fmul_rn(v[b].z, __fmul_rn(inv, wv[b].z)), __fmul_rn(v[b].w, __fmul_rn(inv, wv[b].w))};
+                const float e[4] = {norm_scale(v[b].x, inv, wv[b].x, decode_assoc),
+                                    norm_scale(v[b].y, inv, wv[b].y, decode_assoc),
+                                    norm_scale(v[b].z, inv, wv[b].z, decode_assoc),
+                                    norm_scale(v[b].w, inv, wv[b].w, decode_assoc)};
                 uint16_t h[4], l[4];
 #pragma unroll
                 for (int c = 0; c < 4; c++) split_bf16(e[c], &h[c], &l[c]);
@@ -73,7 +81,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_split_kernel(const float *x, c
     for (int i = lane; i < H; i += 64) ss += xr[i] * xr[i];
     ss = wave_sum(ss);
     const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-    for (int i = lane; i < H; i += 64) split_bf16(__fmul_rn(xr[i], __fmul_rn(inv, w[i])), hr + i, lr + i);
+    for (int i = lane; i < H; i += 64) split_bf16(norm_scale(xr[i], inv, w[i], decode_assoc), hr + i, lr + i);
 }
 
 // Epilogue of one MFMA output fragment: rows mb .. mb+3 (mb a multiple of 4)
@@ -115,8 +123,10 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &a, int mb, int n, con
             } else {  // GEPI_QKV
                 const int half = a.hd >> 1;
                 const int head = P / half, j = P - head * half;
-                const int pos = a.start + n;
+                const int pos = a.pos_seq ? a.pos_seq[n] : a.start + n;
                 const int kvd = a.nkv * a.hd;
+                float *const kcache = a.k_seq ? a.k_seq[n] + a.kv_layer_off : a.k_cache;
+                float *const vcache = a.v_seq ? a.v_seq[n] + a.kv_layer_off : a.v_cache;
                 if (head < a.nq + a.nkv) {
                     float oa, ob;
                     rope_pair(va, vb, a.rope_cos[(size_t)pos * half + j], a.rope_sin[(size_t)pos * half + j], &oa,
@@ -126,12 +136,12 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &a, int mb, int n, con
                         qr[j] = oa;
                         qr[j + half] = ob;
                     } else {
-                        float *kr = a.k_cache + (size_t)pos * kvd + (head - a.nq) * a.hd;
+                        float *kr = kcache + (size_t)pos * kvd + (head - a.nq) * a.hd;
                         kr[j] = oa;
                         kr[j + half] = ob;
                     }
                 } else {
-                    float *vr = a.v_cache + (size_t)pos * kvd + (head - a.nq - a.nkv) * a.hd;
+                    float *vr = vcache + (size_t)pos * kvd + (head - a.nq - a.nkv) * a.hd;
                     vr[j] = va;
                     vr[j + half] = vb;
                 }
@@ -475,8 +485,9 @@ hipError_t launch_embed_gather(const int *tokens, int T, int H, const uint16_t *
 }
 
 hipError_t launch_rmsnorm_split(const float *x, const float *w, float eps, int T, int H, uint16_t *hi, uint16_t *lo,
-                                hipStream_t s) {
-    hipLaunchKernelGGL(rmsnorm_split_kernel, dim3((T + 3) / 4), dim3(kBlock), 0, s, x, w, eps, H, T, hi, lo);
+                                hipStream_t s, bool decode_assoc) {
+    hipLaunchKernelGGL(rmsnorm_split_kernel, dim3((T + 3) / 4), dim3(kBlock), 0, s, x, w, eps, H, T, hi, lo,
+                       decode_assoc ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -20,6 +20,7 @@ from ._lib import (
 
 __all__ = [
     "ModelConfig", "Model", "KvCache", "GenParams", "GenOutput", "generate", "gemv_bf16", "gemv_i8", "quantize_i8", "repack_tmb",
+    "generate_batch",
     "synth_model", "synth_tokens", "synth_normal_bf16", "synth_normal_f32", "TmgError",
 ]
 
@@ -248,6 +249,22 @@ def gemv_bf16(w_dev: int, x_dev: int, y_dev: int, out: int, in_: int, stream: in
     """tensor::matmul_w (src/tensor.rs:315-338) on device pointers."""
     check(lib.tmg_gemv_bf16(C.c_void_p(w_dev), C.c_void_p(x_dev), C.c_void_p(y_dev), out, in_,
                             C.c_void_p(stream)))
+
+
+def generate_batch(model: Model, prompts: Sequence[Sequence[int]], max_tokens: int):
+    """Greedy generation for several prompts at once (tmg_generate_batch): for
+    each prompt the ids generate (src/model.rs:614-663) gives alone at
+    temperature 0.  Returns (list of id lists, device ms of the decode steps)."""
+    n = len(prompts)
+    arrs = [_u32(p) for p in prompts]
+    ptrs = (C.POINTER(C.c_uint32) * n)(*[a.ctypes.data_as(C.POINTER(C.c_uint32)) for a in arrs])
+    lens = (C.c_size_t * n)(*[a.size for a in arrs])
+    out = np.zeros(max(1, n * max_tokens), np.uint32)
+    n_out = (C.c_size_t * n)()
+    ms = C.c_float(0.0)
+    check(lib.tmg_generate_batch(model._h, ptrs, lens, n, max_tokens, out.ctypes.data_as(C.POINTER(C.c_uint32)),
+                                 n_out, C.byref(ms)))
+    return [[int(x) for x in out[b * max_tokens:b * max_tokens + n_out[b]]] for b in range(n)], ms.value
 
 
 def repack_tmb(safetensors_path: str, tmb_path: str) -> None:
