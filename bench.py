@@ -172,6 +172,39 @@ def pmc_traffic(kernel, weights="bf16"):
 SAMPLED = dict(temperature=0.8, top_k=50, top_p=0.9, repetition_penalty=1.1, seed=42)
 
 
+def bench_batch(args, T, W, wl, m, load_s):
+    """B prompts of the workload's length (prompt seeds s, s+1, ...), K greedy
+    decode steps each through tmg_generate_batch; the device time of the
+    batched steps (HIP events around the graph replays) gives the aggregate
+    rate.  Step bytes: the weights once + every sequence's KV at its mean
+    context."""
+    from tinyminigo_amd.model import synth_tokens
+    B, P = args.batch, wl.prompt_len
+    K = args.steps if args.steps is not None else wl.gen_tokens
+    prompts = [[int(t) for t in synth_tokens(wl.prompt_seed + i, P, wl.vocab_size)] for i in range(B)]
+    T.generate_batch(m, prompts, min(K, args.warmup) + 1)
+    out, ms = T.generate_batch(m, prompts, K + 1)
+    ms_per_step = ms / K
+    n_ctx_avg = P + (K + 1) / 2.0
+    step_bytes = wl.weight_bytes() + B * (wl.kv_bytes(int(round(n_ctx_avg))) + wl.misc_bytes())
+    gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"batch {B}: {K} steps in {ms:.1f} ms -> {B * K / (ms * 1e-3):.0f} tok/s aggregate")
+    print(json.dumps({
+        "metric": METRIC + " [batched decode]",
+        "value": round(B * K / (ms * 1e-3), 1), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{wl.name}: {B} prompts of {P} tokens, {K} greedy decode steps each, batched",
+                   "global_batch": B, "seq_len": P + K, "parallelism": "none (1 GPU)"},
+        "load_s": round(load_s, 3),
+        "roofline": {"bound": "hbm", "kernel": "batched decode step (all kernels)", "achieved": round(gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_step": step_bytes},
+        "per_sequence_tok_s": round(K / (ms * 1e-3), 1),
+        "cpu_baseline": None,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -189,6 +222,9 @@ def main():
     ap.add_argument("--weights", choices=["bf16", "i8"], default="bf16",
                     help="i8: load with TMG_I8=1, the reference's int8 weight-only mode (per-row int8 q/k/v/o/"
                          "gate/up/down, BF16 lm_head); the CPU baseline then times the oracle's int8 path")
+    ap.add_argument("--batch", type=int, default=1,
+                    help="B > 1: greedy decode of B prompts at once (tmg_generate_batch); value = aggregate "
+                         "decode tok/s over the B sequences")
     ap.add_argument("--format", choices=["safetensors", "tmb"], default="safetensors",
                     help="tmb: repack the model into a TMB1 file once (the reference's --repack) and load that")
     ap.add_argument("--model-dir", default=os.environ.get("TMG_MODEL_DIR",
@@ -232,6 +268,9 @@ def main():
     sync()
     load_s = time.perf_counter() - t0
     log(f"model loaded ({args.weights} weights, {args.format}) in {load_s:.2f} s")
+
+    if args.batch > 1:
+        return bench_batch(args, T, W, wl, m, load_s)
 
     # prefill tok/s: median over repetitions on fresh caches (one for 8k)
     pf = []
