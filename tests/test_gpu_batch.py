@@ -62,6 +62,21 @@ def test_batch_matches_per_sequence_generate(T, O, untied):
     assert [f[0] for f in first] == [r[0] for r in got] and all(len(f) == 1 for f in first)
 
 
+def test_batch_of_more_than_eight_takes_the_gemm_path(T, O, untied):
+    # up to 8 sequences run the multi-row GEMVs, more run the MFMA GEMMs
+    g, o, wl = untied
+    lens = [1, 2, 3, 5, 8, 13, 21, 34, 7, 4, 9, 30]
+    prompts = [[int(t) for t in T.synth_tokens(100 + i, n, wl.vocab_size)] for i, n in enumerate(lens)]
+    print("batch tiny x12", flush=True)
+    got, _ = T.generate_batch(g, prompts, 16)
+    for b, p in enumerate(prompts):
+        assert got[b] == O.generate(o, p, 16).tokens, f"sequence {b}"
+    # the same sequences in batches of 8 and 4 (GEMV path) agree
+    lo, _ = T.generate_batch(g, prompts[:8], 16)
+    hi, _ = T.generate_batch(g, prompts[8:], 16)
+    assert lo + hi == got
+
+
 def test_batch_tied_and_k_not_multiple_of_64(T, O, W, tiny_path):
     import dataclasses
     wl = dataclasses.replace(W.TINY, name="tiny-llama-h96-kv3-i160-s13", hidden_size=96, num_attention_heads=6,

@@ -8,9 +8,12 @@
 // the QKV epilogue appends each sequence's K/V at its own position in its
 // own cache, attention runs one (sequence, KV head) per workgroup over that
 // sequence's cache, and the lm_head is one GEMM over the B rows followed by
-// a per-sequence argmax.  Each sequence's ids are the ones generate gives
-// for its prompt alone (temperature 0, no penalty), up to f32 rounding at a
-// near tie.  One step is captured into a hipGraph and replayed.
+// a per-sequence argmax.  Up to kMtMaxSeq sequences take the decode GEMVs
+// instead, over all rows at once (enqueue_batch_step_mt): at so few rows the
+// GEMMs' fixed cost per launch exceeds the weight stream.  Each sequence's
+// ids are the ones generate gives for its prompt alone (temperature 0, no
+// penalty), up to f32 rounding at a near tie.  One step is captured into a
+// hipGraph and replayed.
 #include <algorithm>
 #include <chrono>
 #include <cmath>
@@ -57,7 +60,105 @@ struct Batch {
     int out_stride = 0;
     float *x = nullptr, *q = nullptr, *logits = nullptr;
     uint16_t *hi = nullptr, *lo = nullptr, *ahi = nullptr, *alo = nullptr, *hhi = nullptr, *hlo = nullptr;
+    // the multi-row GEMV path (B <= kMtMaxSeq): f32 attention and SwiGLU
+    // outputs, lm_head argmax keys [B][parts]
+    float *attn = nullptr, *h = nullptr;
+    unsigned long long *parts = nullptr;
+    int nparts = 0;
 };
+
+// A decode step for B <= kMtMaxSeq sequences: the decode GEMVs over all B
+// activation rows at once (each weight row read once per step), with the
+// single-sequence path's fusions (RMSNorm prologues, RoPE + KV append,
+// residual and SwiGLU epilogues, lm_head argmax keys).
+int enqueue_batch_step_mt(tmg_model *m, const Batch &bt) {
+    hipStream_t s = m->stream;
+    const int B = bt.B, H = m->H, I = m->I, qd = m->qd, kvd = m->kvd;
+    const float eps = m->cfg.rms_norm_eps;
+    TMG_HIPB(launch_embed_gather(bt.tokens, B, H, m->embed_bf16, m->embed_f32, bt.x, s));
+    for (int l = 0; l < m->L; l++) {
+        const tmg_model::Layer &ly = m->layers[l];
+        const size_t layer_off = (size_t)l * bt.max_pos * kvd;
+        GemvArgs qa{};
+        qa.W = ly.qkv;
+        qa.out = m->qkv_rows;
+        qa.in = H;
+        qa.x = bt.x;
+        qa.norm_w = ly.in_norm;
+        qa.eps = eps;
+        qa.rope_cos = m->rope_cos;
+        qa.rope_sin = m->rope_sin;
+        qa.hd = m->hd;
+        qa.nq = m->nq;
+        qa.nkv = m->nkv;
+        qa.q_out = bt.q;
+        qa.nb = B;
+        qa.pos_seq = bt.pos;
+        qa.k_seq = bt.kptr;
+        qa.v_seq = bt.vptr;
+        qa.kv_layer_off = layer_off;
+        TMG_HIPB(launch_gemv_mt(PRO_NORM, EPI_QKV, qa, s));
+
+        AttnArgs aa{};
+        aa.q = bt.q;
+        aa.nq = m->nq;
+        aa.nkv = m->nkv;
+        aa.hd = m->hd;
+        aa.T = B;
+        aa.scale = 1.0f / sqrtf((float)m->hd);
+        aa.nsplit = 1;
+        aa.pos_seq = bt.pos;
+        aa.k_seq = bt.kptr;
+        aa.v_seq = bt.vptr;
+        aa.kv_layer_off = layer_off;
+        aa.part = m->attn_part;
+        aa.part_ml = m->attn_ml;
+        aa.out_f32 = bt.attn;
+        TMG_HIPB(launch_attn(aa, s));
+
+        GemvArgs oa{};
+        oa.W = ly.o;
+        oa.out = H;
+        oa.in = qd;
+        oa.x = bt.attn;
+        oa.y = bt.x;
+        oa.nb = B;
+        TMG_HIPB(launch_gemv_mt(PRO_PLAIN, EPI_RESID, oa, s));
+
+        GemvArgs ga{};
+        ga.W = ly.gu;
+        ga.out = 2 * I;
+        ga.in = H;
+        ga.x = bt.x;
+        ga.norm_w = ly.post_norm;
+        ga.eps = eps;
+        ga.y = bt.h;
+        ga.nb = B;
+        TMG_HIPB(launch_gemv_mt(PRO_NORM, EPI_SWIGLU, ga, s));
+
+        GemvArgs da{};
+        da.W = ly.down;
+        da.out = H;
+        da.in = I;
+        da.x = bt.h;
+        da.y = bt.x;
+        da.nb = B;
+        TMG_HIPB(launch_gemv_mt(PRO_PLAIN, EPI_RESID, da, s));
+    }
+    GemvArgs la{};
+    la.W = m->lm_head;
+    la.out = m->V;
+    la.in = H;
+    la.x = bt.x;
+    la.norm_w = m->final_norm;
+    la.eps = eps;
+    la.argmax_part = bt.parts;
+    la.nb = B;
+    TMG_HIPB(launch_gemv_mt(PRO_NORM, EPI_LOGITS, la, s));
+    BatchSelectArgs sa{nullptr, m->V, B, bt.tokens, bt.pos, bt.plen, bt.out, bt.out_stride};
+    TMG_HIPB(launch_batch_select_parts(bt.parts, bt.nparts, sa, s));
+    return TMG_OK;
+}
 
 int enqueue_batch_step(tmg_model *m, const Batch &bt) {
     hipStream_t s = m->stream;
@@ -208,6 +309,13 @@ extern "C" int tmg_generate_batch(tmg_model *m, const uint32_t *const *prompts, 
         (rc = al.get(&bt.alo, (size_t)B * m->qd)) || (rc = al.get(&bt.hhi, (size_t)B * m->I)) ||
         (rc = al.get(&bt.hlo, (size_t)B * m->I)) || (rc = al.get(&st, B)))
         return rc;
+    const bool mt = B <= kMtMaxSeq;
+    if (mt) {
+        bt.nparts = gemv_mt_blocks(m->V, m->H, B);
+        if ((rc = al.get(&bt.attn, (size_t)B * m->qd)) || (rc = al.get(&bt.h, (size_t)B * m->I)) ||
+            (rc = al.get(&bt.parts, (size_t)B * bt.nparts)))
+            return rc;
+    }
     if ((rc = ensure_rope(m, (int)bt.max_pos + 1))) return rc;
     std::vector<float *> kp(B), vp(B);
     std::vector<int> pl(B);
@@ -254,16 +362,23 @@ extern "C" int tmg_generate_batch(tmg_model *m, const uint32_t *const *prompts, 
     } guard{cleanup};
     TMG_HIPB(hipEventCreate(&e0));
     TMG_HIPB(hipEventCreate(&e1));
-    if (max_tokens > 1) {
+    const bool use_graph = step_graphs_enabled();  // TMG_DECODE_GRAPH=0: launch the kernels one by one
+    if (max_tokens > 1 && use_graph) {
         TMG_HIPB(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-        rc = enqueue_batch_step(m, bt);
+        rc = mt ? enqueue_batch_step_mt(m, bt) : enqueue_batch_step(m, bt);
         hipError_t e = hipStreamEndCapture(m->stream, &graph);
         if (rc) return rc;
         TMG_HIPB(e);
         TMG_HIPB(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
     }
     TMG_HIPB(hipEventRecord(e0, m->stream));
-    for (uint32_t i = 1; i < max_tokens; i++) TMG_HIPB(hipGraphLaunch(exec, m->stream));
+    for (uint32_t i = 1; i < max_tokens; i++) {
+        if (use_graph) {
+            TMG_HIPB(hipGraphLaunch(exec, m->stream));
+        } else if ((rc = mt ? enqueue_batch_step_mt(m, bt) : enqueue_batch_step(m, bt))) {
+            return rc;
+        }
+    }
     TMG_HIPB(hipEventRecord(e1, m->stream));
     TMG_HIPB(hipEventSynchronize(e1));
     if (decode_ms) TMG_HIPB(hipEventElapsedTime(decode_ms, e0, e1));

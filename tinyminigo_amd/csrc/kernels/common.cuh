@@ -105,8 +105,8 @@ __device__ __forceinline__ float wave_max(float v) {
 // (lane >> (6 - log2 R)).
 template <int R, class T>
 __device__ __forceinline__ T multi_wave_sum(T (&v)[R], int lane) {
-    static_assert(R == 1 || R == 2 || R == 4 || R == 8 || R == 16, "R must be 1, 2, 4, 8 or 16");
-    constexpr int LR = R == 16 ? 4 : R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
+    static_assert(R == 1 || R == 2 || R == 4 || R == 8 || R == 16 || R == 32 || R == 64, "R must be 2^k <= 64");
+    constexpr int LR = R == 64 ? 6 : R == 32 ? 5 : R == 16 ? 4 : R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
     T cur[R];
 #pragma unroll
     for (int i = 0; i < R; i++) cur[i] = v[i];
@@ -133,12 +133,31 @@ __device__ __forceinline__ T multi_wave_sum(T (&v)[R], int lane) {
             cur[i] = keep + dpp_mov<kDppRor8>(send);
         }
     }
-    if constexpr (LR >= 4) {  // lanes with bit 2 set keep cur[1]; the partner
-        // across the half-row mirror (7 - l within 8 lanes) has bit 2 clear
-        const bool up = (lane & 4) != 0;
+    if constexpr (LR >= 4) {  // lanes with bit 2 set keep the upper half; the
+        // partner across the half-row mirror (7 - l within 8 lanes) has bit 2
+        // clear and the same higher bits, so it holds the same values
+#pragma unroll
+        for (int i = 0; i < R / 16; i++) {
+            const bool up = (lane & 4) != 0;
+            const T send = up ? cur[i] : cur[i + R / 16];
+            const T keep = up ? cur[i + R / 16] : cur[i];
+            cur[i] = keep + dpp_mov<kDppHalfMirror>(send);
+        }
+    }
+    if constexpr (LR >= 5) {  // bit 1, partner l ^ 2
+#pragma unroll
+        for (int i = 0; i < R / 32; i++) {
+            const bool up = (lane & 2) != 0;
+            const T send = up ? cur[i] : cur[i + R / 32];
+            const T keep = up ? cur[i + R / 32] : cur[i];
+            cur[i] = keep + dpp_mov<kDppXor2>(send);
+        }
+    }
+    if constexpr (LR >= 6) {  // bit 0, partner l ^ 1
+        const bool up = (lane & 1) != 0;
         const T send = up ? cur[0] : cur[1];
         const T keep = up ? cur[1] : cur[0];
-        cur[0] = keep + dpp_mov<kDppHalfMirror>(send);
+        cur[0] = keep + dpp_mov<kDppXor1>(send);
     }
     return group_sum<(64 >> LR)>(cur[0]);
 }

@@ -117,6 +117,67 @@ hipError_t launch_pe(const GemvArgs &a, hipStream_t s) {
     }
 }
 
+// The GEMV over several activation rows (batched decode, gemv.cuh): the
+// first group's activation loads, then the block's weight rows, then the
+// groups one after another against the weights held in registers.
+template <int KC, int R, int TG, int PRO, int EPI>
+__global__ __launch_bounds__(kBlock) void gemv_mt_kernel(const GemvArgs a) {
+    __shared__ float red[4][R * TG];
+    __shared__ float scratch[4 * TG];
+    float wv[KC][8];
+    if constexpr (PRO == PRO_NORM) {
+        load_norm_w<KC>(a, wv);
+    } else {
+#pragma unroll
+        for (int c = 0; c < KC; c++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) wv[c][j] = 0.0f;
+    }
+    float xv[TG][KC][8];
+    mt_issue<KC, TG>(a, 0, xv);
+    WeightRegs<KC, R> W;
+    gemv_load<KC, R>(a, blockIdx.x, W);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int b0 = 0; b0 < a.nb; b0 += TG) {
+        if (b0 > 0) mt_issue<KC, TG>(a, b0, xv);
+        mt_norm<KC, TG, PRO>(a, wv, xv, scratch);
+        mt_dot<KC, R, TG>(a, W, xv, red);
+        __syncthreads();
+        mt_epilogue<R, TG, EPI>(a, blockIdx.x, b0, red);
+        __syncthreads();  // red and scratch are reused by the next group
+    }
+}
+
+template <int KC, int TG, int PRO, int EPI>
+hipError_t launch_mt_kt(const GemvArgs &a, hipStream_t s) {
+    constexpr int R = gemv_mt_rows(KC, TG);
+    hipLaunchKernelGGL((gemv_mt_kernel<KC, R, TG, PRO, EPI>), dim3((a.out + R - 1) / R), dim3(kBlock), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int KC, int PRO, int EPI>
+hipError_t launch_mt_kc(const GemvArgs &a, hipStream_t s) {
+    if constexpr (KC <= 3) {
+        if (gemv_mt_group(KC, a.nb) == 4) return launch_mt_kt<KC, 4, PRO, EPI>(a, s);
+    }
+    return launch_mt_kt<KC, 2, PRO, EPI>(a, s);
+}
+
+template <int PRO, int EPI>
+hipError_t launch_mt_pe(const GemvArgs &a, hipStream_t s) {
+    switch ((a.in + kChunk - 1) / kChunk) {
+        case 1: return launch_mt_kc<1, PRO, EPI>(a, s);
+        case 2: return launch_mt_kc<2, PRO, EPI>(a, s);
+        case 3: return launch_mt_kc<3, PRO, EPI>(a, s);
+        case 4: return launch_mt_kc<4, PRO, EPI>(a, s);
+        case 5: return launch_mt_kc<5, PRO, EPI>(a, s);
+        case 6: return launch_mt_kc<6, PRO, EPI>(a, s);
+        case 8:
+        case 7: return launch_mt_kc<8, PRO, EPI>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 // WMat::quantize_i8 (src/tensor.rs:275-293) of BF16 rows, one workgroup per
 // row: the row's max |w| (block reduction), scale = max/127 or 1 for a zero
 // row, q = round(w / scale) with halves away from zero, clamped to +-127.
@@ -313,6 +374,35 @@ __global__ __launch_bounds__(1024) void batch_select_kernel(const BatchSelectArg
     a.pos[b] = p + 1;
 }
 
+// Same selection from per-workgroup keys [B][nparts] of the multi-row
+// lm_head GEMV.
+__global__ __launch_bounds__(1024) void batch_select_parts_kernel(const unsigned long long *parts, int nparts,
+                                                                  const BatchSelectArgs a) {
+    __shared__ unsigned long long red[16];
+    const int b = blockIdx.x;
+    unsigned long long best = kArgmaxInit;
+    for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
+        const unsigned long long k = parts[(size_t)b * nparts + i];
+        best = k > best ? k : best;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = shfl_xor_u64(best, off);
+        best = o > best ? o : best;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) best = red[w] > best ? red[w] : best;
+    int tok = (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
+    if (tok < 0 || tok >= a.V) tok = 0;
+    a.tokens[b] = tok;
+    const int p = a.pos[b];
+    const int i = p - a.plen[b] + 1;
+    if (i >= 0 && i < a.out_stride) a.out[(size_t)b * a.out_stride + i] = tok;
+    a.pos[b] = p + 1;
+}
+
 __global__ __launch_bounds__(1024) void batch_first_kernel(const unsigned long long *part, int nparts, int V, int b,
                                                            int *tokens, int *out, int out_stride) {
     __shared__ unsigned long long red[16];
@@ -338,6 +428,28 @@ __global__ __launch_bounds__(1024) void batch_first_kernel(const unsigned long l
 hipError_t launch_batch_select(const BatchSelectArgs &a, hipStream_t s) {
     if (a.B <= 0) return hipErrorInvalidValue;
     hipLaunchKernelGGL(batch_select_kernel, dim3(a.B), dim3(1024), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_mt(int pro, int epi, const GemvArgs &a, hipStream_t s) {
+    if (a.nb < 1 || a.nb > kMtMaxSeq || a.W8) return hipErrorInvalidValue;
+    if (pro == PRO_NORM && epi == EPI_QKV) return launch_mt_pe<PRO_NORM, EPI_QKV>(a, s);
+    if (pro == PRO_PLAIN && epi == EPI_RESID) return launch_mt_pe<PRO_PLAIN, EPI_RESID>(a, s);
+    if (pro == PRO_NORM && epi == EPI_SWIGLU) return launch_mt_pe<PRO_NORM, EPI_SWIGLU>(a, s);
+    if (pro == PRO_NORM && epi == EPI_LOGITS) return launch_mt_pe<PRO_NORM, EPI_LOGITS>(a, s);
+    return hipErrorInvalidValue;
+}
+
+int gemv_mt_blocks(int out, int in, int nb) {
+    const int kc = (in + kChunk - 1) / kChunk;
+    const int R = gemv_mt_rows(kc, gemv_mt_group(kc, nb));
+    return (out + R - 1) / R;
+}
+
+hipError_t launch_batch_select_parts(const unsigned long long *parts, int nparts, const BatchSelectArgs &a,
+                                     hipStream_t s) {
+    if (a.B <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(batch_select_parts_kernel, dim3(a.B), dim3(1024), 0, s, parts, nparts, a);
     return hipGetLastError();
 }
 

@@ -623,4 +623,181 @@ __device__ __forceinline__ void epi_load_rope(const GemvArgs &a, int blk, int po
     }
 }
 
+// ---------------------------------------------------------------------------
+// Several activation rows per launch (batched decode of up to kMtMaxSeq
+// sequences).  A workgroup loads its R weight rows once (as gemv_load does)
+// and walks the sequences in groups of TG: per group it loads the TG
+// activation rows (KC chunks of 8 per thread each), applies each row's
+// RMSNorm (forward_token's (v*inv)*w), forms the R*TG dots, reduces them in
+// one transposed butterfly, and runs the epilogue per (row, sequence).
+// ---------------------------------------------------------------------------
+
+// Activation rows per group: 2 for two sequences, else 4 (2 above three
+// chunks); activation registers TG * KC * 8.
+__host__ __device__ constexpr int gemv_mt_group(int KC, int nb) { return (nb <= 2 || KC > 3) ? 2 : 4; }
+// Rows per workgroup: every workgroup reads each group's activation rows
+// from L2, so more rows per workgroup mean fewer re-reads per weight byte;
+// R * TG dots stay within 32 (registers, and two waves per SIMD).
+__host__ __device__ constexpr int gemv_mt_rows(int KC, int TG) { return KC == 1 ? 32 / TG : KC <= 3 ? 16 / TG : 4; }
+
+// Raw loads of activation rows b0 .. b0+TG-1 (zeros past a.nb).
+template <int KC, int TG>
+__device__ __forceinline__ void mt_issue(const GemvArgs &a, int b0, float (&xv)[TG][KC][8]) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < TG; u++) {
+        const bool live = b0 + u < a.nb;
+        const float *src = a.x + (size_t)(live ? b0 + u : 0) * a.in;
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            const int k = c * kChunk + t * 8;
+            if (live && k < a.in) {
+                const float4 p = *reinterpret_cast<const float4 *>(src + k);
+                const float4 q = *reinterpret_cast<const float4 *>(src + k + 4);
+                xv[u][c][0] = p.x;
+                xv[u][c][1] = p.y;
+                xv[u][c][2] = p.z;
+                xv[u][c][3] = p.w;
+                xv[u][c][4] = q.x;
+                xv[u][c][5] = q.y;
+                xv[u][c][6] = q.z;
+                xv[u][c][7] = q.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; j++) xv[u][c][j] = 0.0f;
+            }
+        }
+    }
+}
+
+// Each row's RMSNorm (PRO_NORM); `scratch` holds 4*TG floats of LDS.
+template <int KC, int TG, int PRO>
+__device__ __forceinline__ void mt_norm(const GemvArgs &a, const float (&wv)[KC][8], float (&xv)[TG][KC][8],
+                                        float *scratch) {
+    if constexpr (PRO == PRO_NORM) {
+        float ss[TG];
+#pragma unroll
+        for (int u = 0; u < TG; u++) {
+            ss[u] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < KC; c++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) ss[u] += xv[u][c][j] * xv[u][c][j];
+        }
+        block_sum_n<TG>(ss, scratch);
+#pragma unroll
+        for (int u = 0; u < TG; u++) {
+            const float inv = 1.0f / sqrtf(ss[u] / (float)a.in + a.eps);
+#pragma unroll
+            for (int c = 0; c < KC; c++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) xv[u][c][j] = (xv[u][c][j] * inv) * wv[c][j];
+        }
+    }
+}
+
+// Dots of the R loaded rows with the TG activation rows, reduced into
+// red[wave][r * TG + u].
+template <int KC, int R, int TG>
+__device__ __forceinline__ void mt_dot(const GemvArgs &a, const WeightRegs<KC, R> &W, const float (&xv)[TG][KC][8],
+                                       float (*red)[R * TG]) {
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    float acc[R * TG];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int u = 0; u < TG; u++) {
+            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+            for (int c = 0; c < KC; c++) {
+                const u32x4 w = (c * kChunk + t * 8 < a.in) ? W.w[r][c] : u32x4{0u, 0u, 0u, 0u};
+                s0 = fmaf(xv[u][c][0], bf16_lo(w.x), s0);
+                s1 = fmaf(xv[u][c][1], bf16_hi(w.x), s1);
+                s0 = fmaf(xv[u][c][2], bf16_lo(w.y), s0);
+                s1 = fmaf(xv[u][c][3], bf16_hi(w.y), s1);
+                s0 = fmaf(xv[u][c][4], bf16_lo(w.z), s0);
+                s1 = fmaf(xv[u][c][5], bf16_hi(w.z), s1);
+                s0 = fmaf(xv[u][c][6], bf16_lo(w.w), s0);
+                s1 = fmaf(xv[u][c][7], bf16_hi(w.w), s1);
+            }
+            acc[r * TG + u] = s0 + s1;
+        }
+    }
+    constexpr int N = R * TG;
+    constexpr int LN = N == 64 ? 6 : N == 32 ? 5 : N == 16 ? 4 : N == 8 ? 3 : N == 4 ? 2 : N == 2 ? 1 : 0;
+    const float sum = multi_wave_sum<N>(acc, lane);
+    if ((lane & ((64 >> LN) - 1)) == 0) red[wave][lane >> (6 - LN)] = sum;
+}
+
+// Epilogue of sequences b0 .. b0+TG-1 (those below a.nb) for block blk.
+// LOGITS: argmax key of the block's rows per sequence.
+template <int R, int TG, int EPI>
+__device__ __forceinline__ void mt_epilogue(const GemvArgs &a, int blk, int b0, float (*red)[R * TG]) {
+    const int t = threadIdx.x;
+    const int row0 = blk * R;
+    auto val = [&](int r, int u) {
+        const int i = r * TG + u;
+        return (red[0][i] + red[1][i]) + (red[2][i] + red[3][i]);
+    };
+    if constexpr (EPI == EPI_RESID) {
+        if (t < R * TG) {
+            const int r = t / TG, u = t % TG, row = row0 + r, b = b0 + u;
+            if (row < a.out && b < a.nb) {
+                float *y = a.y + (size_t)b * a.out + row;
+                *y = *y + val(r, u);
+            }
+        }
+    } else if constexpr (EPI == EPI_LOGITS) {
+        if (t < TG) {
+            const int b = b0 + t;
+            unsigned long long key = 0ull;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const float v = val(r, t);
+                const int row = row0 + r;
+                if (row < a.out && v == v) {
+                    const unsigned long long k = argmax_key(v, (uint32_t)row);
+                    key = k > key ? k : key;
+                }
+            }
+            if (b < a.nb) a.argmax_part[(size_t)b * gridDim.x + blk] = key;
+        }
+    } else {
+        if (t < (R / 2) * TG) {
+            const int pr = t / TG, u = t % TG, b = b0 + u;
+            const int P = row0 / 2 + pr;
+            if (2 * P + 1 < a.out && b < a.nb) {
+                const float va = val(2 * pr, u), vb = val(2 * pr + 1, u);
+                if constexpr (EPI == EPI_SWIGLU) {
+                    a.y[(size_t)b * (a.out / 2) + P] = swiglu(va, vb);
+                } else {  // EPI_QKV
+                    const int half = a.hd >> 1;
+                    const int head = P / half, j = P - head * half;
+                    const int kvd = a.nkv * a.hd;
+                    const int pos = a.pos_seq[b];
+                    if (head < a.nq + a.nkv) {
+                        float oa, ob;
+                        rope_pair(va, vb, a.rope_cos[(size_t)pos * half + j], a.rope_sin[(size_t)pos * half + j],
+                                  &oa, &ob);
+                        if (head < a.nq) {
+                            float *q = a.q_out + (size_t)b * a.nq * a.hd + head * a.hd;
+                            q[j] = oa;
+                            q[j + half] = ob;
+                        } else {
+                            float *kr = a.k_seq[b] + a.kv_layer_off + (size_t)pos * kvd + (head - a.nq) * a.hd;
+                            kr[j] = oa;
+                            kr[j + half] = ob;
+                        }
+                    } else {
+                        float *vr = a.v_seq[b] + a.kv_layer_off + (size_t)pos * kvd + (head - a.nq - a.nkv) * a.hd;
+                        vr[j] = va;
+                        vr[j + half] = vb;
+                    }
+                }
+            }
+        }
+    }
+}
+
 }  // namespace tmg

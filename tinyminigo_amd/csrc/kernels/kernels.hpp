@@ -62,9 +62,26 @@ struct GemvArgs {
     // the split-K partials of the decode attention kernel (see AttnArgs)
     const float *part, *part_ml;
     int nsplit, group;
+    // several sequences (launch_gemv_mt): nb activation rows x[b * in], outputs
+    // y[b * out] (RESID) / y[b * out / 2] (SWIGLU) / q_out[b * nq * hd] (QKV),
+    // argmax keys argmax_part[b * blocks + block] (LOGITS); sequence b is at
+    // position pos_seq[b] with its K/V rows in k_seq[b] / v_seq[b] +
+    // kv_layer_off
+    int nb;
+    const int *pos_seq;
+    float *const *k_seq;
+    float *const *v_seq;
+    size_t kv_layer_off;
 };
 
 hipError_t launch_gemv(int pro, int epi, const GemvArgs &a, hipStream_t s);
+// The decode GEMV over a.nb <= kMtMaxSeq activation rows at once (batched
+// decode of several sequences): every weight row is read once and dotted
+// with all rows.  PRO_NORM or PRO_PLAIN; EPI_QKV, EPI_RESID, EPI_SWIGLU or
+// EPI_LOGITS (argmax keys only).  gemv_mt_blocks: workgroups of a launch.
+constexpr int kMtMaxSeq = 8;
+hipError_t launch_gemv_mt(int pro, int epi, const GemvArgs &a, hipStream_t s);
+int gemv_mt_blocks(int out, int in, int nb);
 // WMat::quantize_i8 of BF16 rows (src/tensor.rs:275-293, widened from BF16 as
 // wmat_maybe_i8 does, src/model.rs:60-68): q8 [rows, in] codes and scale
 // [rows].  With rewrite, w is overwritten with the codes as BF16 (exact), the
@@ -146,6 +163,10 @@ struct BatchSelectArgs {
     int out_stride;
 };
 hipError_t launch_batch_select(const BatchSelectArgs &a, hipStream_t s);
+// The same selection from per-workgroup argmax keys [B][nparts] (the
+// multi-row lm_head GEMV's).
+hipError_t launch_batch_select_parts(const unsigned long long *parts, int nparts, const BatchSelectArgs &a,
+                                     hipStream_t s);
 // The first generated id of sequence b from a prefill's per-workgroup argmax
 // keys: tokens[b] = id, out[b * out_stride] = id.
 hipError_t launch_batch_first(const unsigned long long *argmax_part, int nparts, int V, int b, int *tokens, int *out,
