@@ -205,8 +205,12 @@ def device_draw(seed: int, i: int) -> float:
     return float(np.float32((mix((key + (i + 1) * 0x9E3779B97F4A7C15) & M) >> 40) * 2.0**-24))
 
 
+# top_k <= 64: slice candidates; top_k = 0 with top_p = 1: full softmax;
+# top_k > 64, or top_p < 1 without top_k: the whole-vocabulary threshold search
 @pytest.mark.parametrize("temp,k,p,pen", [(0.8, 50, 0.9, 1.1), (1.0, 0, 1.0, 1.0), (0.0, 0, 1.0, 1.3),
-                                          (0.7, 7, 1.0, 1.0), (1.2, 64, 0.5, 1.05)])
+                                          (0.7, 7, 1.0, 1.0), (1.2, 64, 0.5, 1.05),
+                                          (0.8, 0, 0.9, 1.0), (0.6, 0, 0.3, 1.2), (1.0, 200, 0.95, 1.1),
+                                          (0.9, 500, 1.0, 1.0), (1.5, 1000, 0.8, 1.0), (2.0, 65, 0.99, 1.0)])
 def test_sampling_teacher_forced(T, O, untied, temp, k, p, pen):
     g, o, wl = untied
     prompt = [int(t) for t in T.synth_tokens(23, 12, wl.vocab_size)]
@@ -247,6 +251,25 @@ def test_one_b_prefill_and_greedy(T, O, W, one_b):
     for i, t in enumerate(ref.tokens[:8]):
         close_logits(lg, ref.step_logits[i], f"1B step {i}")
         lg = g.forward_token(t, gc)
+
+
+@pytest.mark.parametrize("temp,k,p", [(0.9, 0, 0.9), (1.0, 300, 0.95), (1.3, 40, 0.8)])
+def test_one_b_sampling_teacher_forced(T, O, one_b, temp, k, p):
+    # 73448 ids: 36 slices on the top-k path, 72 ids per thread on the
+    # whole-vocabulary path
+    g, o = one_b
+    prompt = [int(t) for t in T.synth_tokens(5, 16, o.config.vocab_size)]
+    n = 12
+    out = T.generate(g, prompt, T.GenParams(max_tokens=n, temperature=temp, top_k=k, top_p=p,
+                                            repetition_penalty=1.1, seed=7))
+    assert len(out.tokens) == n
+    ref = O.generate(o, prompt, n, forced=out.tokens, repetition_penalty=1.1, keep_logits=True)
+    mism = 0
+    for i, (tok, lg) in enumerate(zip(out.tokens, ref.step_logits)):
+        tr = O.sample(lg, temp, k, p, device_draw(7, i))
+        mism += tr.token != tok
+        assert tok in set(int(c) for c, pr in zip(tr.cand_ids, tr.cand_probs) if pr > 0), f"step {i}"
+    assert mism <= 1, f"{mism} of {n} sampled ids differ"
 
 
 @pytest.mark.parametrize("max_pos", [64, 512, 1024])

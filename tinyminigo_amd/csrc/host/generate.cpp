@@ -76,18 +76,12 @@ extern "C" int tmg_generate(tmg_model *m, const uint32_t *prompt, size_t n_promp
     int mode;
     if (greedy) {
         mode = p->repetition_penalty != 1.0f ? SEL_PENALTY_ARGMAX : SEL_ARGMAX;
-    } else if (use_k) {
-        if (p->top_k > (uint32_t)kSampleMaxK)
-            return set_error(TMG_E_INVALID, "top_k above " + std::to_string(kSampleMaxK) +
-                                                " is not supported by the device sampler");
-        mode = SEL_TOPK;
     } else {
-        if (p->top_p < 1.0f)
-            return set_error(TMG_E_INVALID, "top_p < 1 without top_k (a full-vocabulary nucleus sort) is not "
-                                            "supported by the device sampler");
-        mode = SEL_FULL;
+        // small k: per-slice candidate lists; no k or a larger one: threshold
+        // searches over the whole vocabulary
+        mode = use_k && p->top_k <= (uint32_t)kSampleMaxK ? SEL_TOPK : SEL_FULL;
     }
-    if ((size_t)m->V > (size_t)kSampleSlice * 64 && mode != SEL_ARGMAX)
+    if ((size_t)m->V > (size_t)kSampleMaxVocab && mode != SEL_ARGMAX)
         return set_error(TMG_E_INVALID, "vocabulary too large for the device sampler");
 
     (void)hipSetDevice(m->device);

@@ -84,6 +84,7 @@ struct tmg_cache {
     int attn_nsplit = 1;               // split-K width of decode attention for this cache
     unsigned *seen = nullptr;          // bitmap of generated ids (repetition penalty)
     unsigned long long *cand = nullptr;  // sampler candidates
+    float *gsc = nullptr;                // [2V] scratch of the whole-vocabulary sampler
     tmg::GridBar *bar = nullptr;       // persistent-kernel barrier counters
     tmg::PersistPlan *plan = nullptr;  // persistent-kernel argument blocks
     bool persist_broken = false;       // a barrier timed out: use the graph path
@@ -119,7 +120,7 @@ enum SelectMode {
     SEL_ARGMAX = 0,          // greedy, argmax fused into the lm_head GEMV
     SEL_PENALTY_ARGMAX = 1,  // greedy after the repetition penalty
     SEL_TOPK = 2,            // temperature sampling with 0 < top_k <= kSampleMaxK
-    SEL_FULL = 3,            // temperature sampling over the whole vocabulary
+    SEL_FULL = 3,            // temperature sampling, any other top_k / top_p
 };
 
 int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mode);

@@ -293,6 +293,8 @@ constexpr int kSampleSlice = 2048;
 // Candidates the second sampling pass holds (16 per thread of 512): slices x
 // kSampleMaxK may not exceed it, i.e. vocabularies up to 262144 ids.
 constexpr int kSampleSelectKeys = 8192;
+// Largest vocabulary either sampling path takes.
+constexpr int kSampleMaxVocab = 262144;
 
 struct SampleArgs {
     float *logits;  // [V]; penalized in place like the reference
@@ -305,6 +307,9 @@ struct SampleArgs {
     int hist_cap;
     int greedy;       // temperature <= 0: argmax of the penalized logits
     int advance_pos;  // 1 after a decode step, 0 after prefill
+    // whole-vocabulary path (cand null, not greedy): [2V] floats (scaled
+    // logits, then unnormalized probabilities)
+    float *scratch;
 };
 
 hipError_t launch_sample(const SampleArgs &a, hipStream_t s);

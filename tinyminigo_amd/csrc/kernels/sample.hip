@@ -12,8 +12,9 @@
 //   lane runs the reference's sequential tail over the k candidates in
 //   order: softmax (max, exp, sequential sum, divide), nucleus cut at the
 //   first cumulative sum > top_p, renormalization, and the inverse-CDF walk.
-// Full-vocabulary path (no top-k, top_p >= 1): one workgroup computes the
-// softmax and finds the draw with a block prefix sum in id order.
+// Whole-vocabulary path (no top-k, or top_k > kSampleMaxK): one workgroup
+// replaces each of the reference's sorts with a threshold search over the
+// whole vocabulary (sample_general_kernel below).
 //
 // Keys order by value descending, then id ascending, which is the reference
 // argmax tie rule; the reference's sort_unstable_by leaves equal-value order
@@ -316,78 +317,394 @@ __global__ __launch_bounds__(kSelectThreads) void sample_select_kernel(const Sam
     if (lane == 0) emit_token(a, key_index(((unsigned long long)khi << 32) | klo));
 }
 
-// No top-k: candidates are all ids in id order (src/tensor.rs:1169-1179).
-__global__ __launch_bounds__(1024) void sample_full_kernel(const SampleArgs a) {
-    __shared__ float red[32];
-    __shared__ float pre[1024];
-    const DevState st = *a.st;
-    const int nt = blockDim.x, t = threadIdx.x;
-    const int per = (a.V + nt - 1) / nt;
-    const int b = min(a.V, t * per), e = min(a.V, b + per);
-    float mx = -INFINITY;
-    for (int i = b; i < e; i++) mx = fmaxf(mx, adjusted(a.logits, a.seen, st, i, false));
-    // block max
-    mx = wave_max(mx);
-    if ((t & 63) == 0) red[t >> 6] = mx;
-    __syncthreads();
-    if (t < 64) {
-        float v = t < (nt >> 6) ? red[t] : -INFINITY;
-        v = wave_max(v);
-        if (t == 0) red[16] = v;
+// ---------------------------------------------------------------------------
+// Whole-vocabulary path: no top-k (with or without a nucleus cut), or top_k
+// above kSampleMaxK.  One workgroup of kGenThreads.  Wave w owns the ids
+// [w*wsz, (w+1)*wsz) (wsz a multiple of 256), lane l of it the ids
+// w*wsz + 64*j + l, so every pass is coalesced; rows of 256 ids are the
+// units of the id-order searches.  a.scratch holds the scaled logits [V],
+// then the unnormalized probabilities [V].  The orders the reference gets by
+// sorting are found by threshold searches instead: among the selected ids,
+// in a given order, the first at which a running total of weights exceeds
+// a target.  Weight 1 in (scaled logit descending, id ascending) order gives
+// the k-th largest logit; the probability as weight gives the nucleus cut
+// (first cumulative sum > top_p) and the inverse-CDF walk.  Probability
+// masses are summed in 2^-40 fixed point, so every sum is exact and
+// independent of summation order.
+// ---------------------------------------------------------------------------
+
+constexpr int kGenThreads = 1024;
+constexpr int kGenWaves = kGenThreads / 64;
+constexpr int kGenRow = 256;       // ids per row of an id-order search
+constexpr int kGenMaxRows = 64;    // rows per wave: one per lane
+constexpr int kGenBins = 4096;     // 12-bit digits: key bits 31..20, 19..8, then 7..0
+constexpr double kFx = 1099511627776.0;  // 2^40
+static_assert(kGenWaves * kGenMaxRows * kGenRow >= kSampleMaxVocab, "rows must cover the vocabulary");
+
+struct GenShared {
+    union {
+        unsigned long long bins[kGenBins];                 // key histogram
+        unsigned long long rowt[kGenWaves][kGenMaxRows];   // row totals
+    };
+    unsigned long long wtot[kGenWaves];
+    unsigned long long res[4];
+    float fred[kGenWaves];
+};
+
+// Which ids this thread owns: i = base + 64*j, i < end.
+struct GenLayout {
+    int V, wsz, nrow, base, end;
+    __device__ explicit GenLayout(int v) : V(v) {
+        nrow = (V + kGenWaves * kGenRow - 1) / (kGenWaves * kGenRow);
+        wsz = nrow * kGenRow;
+        const int w = (int)(threadIdx.x >> 6);
+        base = w * wsz + (int)(threadIdx.x & 63);
+        end = min(V, (w + 1) * wsz);
     }
-    __syncthreads();
-    const float M = red[16];
-    __syncthreads();
-    float s = 0.0f;
-    for (int i = b; i < e; i++) s += expf(adjusted(a.logits, a.seen, st, i, false) - M);
-    float ws = wave_sum(s);
-    if ((t & 63) == 0) red[t >> 6] = ws;
-    __syncthreads();
-    if (t < 64) {
-        float v = t < (nt >> 6) ? red[t] : 0.0f;
-        v = wave_sum(v);
-        if (t == 0) red[17] = v;
-    }
-    __syncthreads();
-    const float S = red[17];
-    // per-thread sums of probabilities, then an exclusive prefix in id order
-    float c = 0.0f;
-    for (int i = b; i < e; i++) c += expf(adjusted(a.logits, a.seen, st, i, false) - M) / S;
-    pre[t] = c;
-    __syncthreads();
-    if (t == 0) {
-        const float r = uniform_f32(st.seed, (unsigned long long)st.step);
-        float cum = 0.0f;
-        int pick = -1;
-        for (int th = 0; th < nt && pick < 0; th++) {
-            if (r < cum + pre[th]) {
-                const int bb = min(a.V, th * per), ee = min(a.V, bb + per);
-                for (int i = bb; i < ee; i++) {
-                    cum += expf(adjusted(a.logits, a.seen, st, i, false) - M) / S;
-                    if (r < cum) {
-                        pick = i;
-                        break;
-                    }
-                }
-            } else {
-                cum += pre[th];
-            }
+};
+
+// f(i, s, p) over this thread's ids, with s = sc[i] and p = pr[i] (0 when
+// pr is null) loaded eight ids at a time, so a pass keeps eight loads in
+// flight per lane instead of one.
+constexpr int kGenUnroll = 8;
+template <class F>
+__device__ __forceinline__ void gen_each(const GenLayout &L, const float *sc, const float *pr, F f) {
+    for (int i0 = L.base; i0 < L.end; i0 += 64 * kGenUnroll) {
+        float sv[kGenUnroll], pv[kGenUnroll];
+#pragma unroll
+        for (int u = 0; u < kGenUnroll; u++) {
+            const int i = i0 + 64 * u;
+            sv[u] = i < L.end ? sc[i] : 0.0f;
+            pv[u] = pr && i < L.end ? pr[i] : 0.0f;
         }
-        if (pick < 0) {
-            pick = 0;
-            for (int i = 0; i < a.V; i++)
-                if (expf(adjusted(a.logits, a.seen, st, i, false) - M) / S > 0.0f) {
-                    pick = i;
+#pragma unroll
+        for (int u = 0; u < kGenUnroll; u++) {
+            const int i = i0 + 64 * u;
+            if (i < L.end) f(i, sv[u], pv[u]);
+        }
+    }
+}
+
+__device__ __forceinline__ unsigned long long fx(float p) { return (unsigned long long)((double)p * kFx); }
+
+__device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += shfl_xor_u64(v, off);
+    return v;
+}
+
+__device__ __forceinline__ unsigned long long wave_incl_u64(unsigned long long v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t lo = __shfl_up((uint32_t)v, off, 64), hi = __shfl_up((uint32_t)(v >> 32), off, 64);
+        if (lane >= off) v += ((unsigned long long)hi << 32) | lo;
+    }
+    return v;
+}
+
+// Exclusive prefix over the workgroup's threads in thread order; *total gets
+// the sum.  Begins and ends with a barrier.
+__device__ unsigned long long block_excl_u64(unsigned long long v, GenShared &sh, unsigned long long *total) {
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const unsigned long long incl = wave_incl_u64(v);
+    __syncthreads();
+    if (lane == 63) sh.wtot[w] = incl;
+    __syncthreads();
+    unsigned long long before = 0, all = 0;
+    for (int i = 0; i < kGenWaves; i++) {
+        if (i < w) before += sh.wtot[i];
+        all += sh.wtot[i];
+    }
+    __syncthreads();
+    *total = all;
+    return before + incl - v;
+}
+
+__device__ float block_max_f(float v, GenShared &sh) {
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) sh.fred[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = -INFINITY;
+    for (int i = 0; i < kGenWaves; i++) m = fmaxf(m, sh.fred[i]);
+    __syncthreads();
+    return m;
+}
+
+__device__ float block_sum_f(float v, GenShared &sh) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) sh.fred[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = 0.0f;
+    for (int i = 0; i < kGenWaves; i++) m += sh.fred[i];
+    __syncthreads();
+    return m;
+}
+
+// A value one thread found (or ~0 if none did), broadcast to all.
+__device__ unsigned long long block_pick(bool mine, unsigned long long v, GenShared &sh) {
+    if (threadIdx.x == 0) sh.res[2] = ~0ull;
+    __syncthreads();
+    if (mine) sh.res[2] = v;
+    __syncthreads();
+    const unsigned long long r = sh.res[2];
+    __syncthreads();
+    return r;
+}
+
+// Threshold search in id order: the first id whose running total of wv(i)
+// (the weight of id i, 0 when not selected; any i < V) exceeds `rest`, or -1
+// when the total does not.  Row totals (thread w*64 + r holds row r of wave
+// w, so thread order is id order), a prefix scan over them, then one
+// wavefront scans the 256 ids of the crossing row.
+template <class Wv>
+__device__ int id_threshold(const GenLayout &L, Wv wv, unsigned long long rest, GenShared &sh) {
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    auto wb = [&](int i) { return i < L.V ? wv(i) : 0ull; };
+    for (int r = 0; r < L.nrow; r++) {
+        const int i = w * L.wsz + r * kGenRow + lane;
+        const unsigned long long v = wave_sum_u64(wb(i) + wb(i + 64) + wb(i + 128) + wb(i + 192));
+        if (lane == 0) sh.rowt[w][r] = v;
+    }
+    __syncthreads();
+    const unsigned long long c = lane < L.nrow ? sh.rowt[w][lane] : 0ull;
+    unsigned long long tot;
+    const unsigned long long cum = block_excl_u64(c, sh, &tot);
+    if (tot <= rest) return -1;
+    const unsigned long long hit =
+        block_pick(lane < L.nrow && cum <= rest && cum + c > rest, ((unsigned long long)t << 48) | cum, sh);
+    const int row = (int)(hit >> 48);
+    const unsigned long long left = rest - (hit & ((1ull << 48) - 1));
+    const int first = (row >> 6) * L.wsz + (row & 63) * kGenRow;  // lane l: ids first + 4l .. first + 4l + 3
+    if (t == 0) sh.res[2] = ~0ull;
+    __syncthreads();
+    if (w == 0) {
+        unsigned long long q[4], m = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            q[k] = wb(first + 4 * lane + k);
+            m += q[k];
+        }
+        const unsigned long long incl = wave_incl_u64(m);
+        unsigned long long cu = incl - m;
+        if (cu <= left && incl > left) {
+            for (int k = 0; k < 4; k++) {
+                cu += q[k];
+                if (cu > left) {
+                    sh.res[2] = (unsigned long long)(first + 4 * lane + k);
                     break;
                 }
+            }
         }
-        emit_token(a, pick);
     }
+    __syncthreads();
+    const unsigned long long r = sh.res[2];
+    __syncthreads();
+    return r == ~0ull ? -1 : (int)r;
+}
+
+// Threshold search in (key descending, id ascending) order.  kw(i, s, p, k,
+// w) says whether id i (scaled logit s, pr value p) is selected and sets its
+// key k (uint32, larger first) and weight w.  A radix search over the key
+// (12, 12, then 8 bits) finds the key at which the running total crosses
+// `target`; ties at that key go in id order.  Returns the id, or -1 when the
+// total of all selected ids does not exceed the target.  Ids of weight 0
+// can never be the answer and are skipped.
+template <class Kw>
+__device__ int desc_threshold(const GenLayout &L, const float *sc, const float *pr, Kw kw,
+                              unsigned long long target, GenShared &sh) {
+    const int t = threadIdx.x;
+    uint32_t pfx = 0;                  // key bits decided so far
+    unsigned long long rest = target;  // target left after the heavier bins
+    for (int lv = 0; lv < 3; lv++) {
+        const int shift = lv == 0 ? 20 : lv == 1 ? 8 : 0;
+        const uint32_t nb = lv == 2 ? 256u : 4096u;
+        const int above = lv == 0 ? 32 : lv == 1 ? 20 : 8;  // pfx holds key >> above
+        for (int i = t; i < kGenBins; i += kGenThreads) sh.bins[i] = 0;
+        __syncthreads();
+        gen_each(L, sc, pr, [&](int i, float s, float p) {
+            uint32_t k;
+            unsigned long long v;
+            if (!kw(i, s, p, k, v) || !v) return;
+            if (lv > 0 && (k >> above) != pfx) return;
+            atomicAdd(&sh.bins[(k >> shift) & (nb - 1)], v);
+        });
+        __syncthreads();
+        // thread t takes 4 bins from the top: nb-1-4t .. nb-4-4t
+        unsigned long long c[4], mine = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int bin = (int)nb - 1 - 4 * t - j;
+            c[j] = bin >= 0 ? sh.bins[bin] : 0ull;
+            mine += c[j];
+        }
+        unsigned long long total;
+        unsigned long long cum = block_excl_u64(mine, sh, &total);
+        if (total <= rest) return -1;  // only possible at level 0
+        int hit = -1;
+        unsigned long long before = 0;
+        if (cum <= rest && cum + mine > rest) {
+            for (int j = 0; j < 4; j++) {
+                if (cum + c[j] > rest) {
+                    hit = (int)nb - 1 - 4 * t - j;
+                    before = cum;
+                    break;
+                }
+                cum += c[j];
+            }
+        }
+        // the bin (12 bits) and the weight before it (< 2^52 for V <= 2^18)
+        const unsigned long long r = block_pick(hit >= 0, ((unsigned long long)hit << 52) | before, sh);
+        pfx = (pfx << (lv == 2 ? 8 : 12)) | (uint32_t)(r >> 52);
+        rest -= r & ((1ull << 52) - 1);
+    }
+    return id_threshold(
+        L,
+        [&](int i) {
+            uint32_t k;
+            unsigned long long v;
+            return kw(i, sc[i], pr ? pr[i] : 0.0f, k, v) && k == pfx ? v : 0ull;
+        },
+        rest, sh);
+}
+
+__global__ __launch_bounds__(kGenThreads) void sample_general_kernel(const SampleArgs a) {
+    __shared__ GenShared sh;
+    const DevState st = *a.st;
+    const GenLayout L(a.V);
+    const int V = a.V, t = threadIdx.x;
+    float *sc = a.scratch, *pr = a.scratch + V;
+    // scaled logits (penalty, temperature) and their maximum
+    float mx = -INFINITY;
+    for (int i0 = L.base; i0 < L.end; i0 += 64 * kGenUnroll) {
+        float lv[kGenUnroll];
+#pragma unroll
+        for (int u = 0; u < kGenUnroll; u++) {
+            const int i = i0 + 64 * u;
+            lv[u] = i < L.end ? a.logits[i] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kGenUnroll; u++) {
+            const int i = i0 + 64 * u;
+            if (i >= L.end) break;
+            float v = lv[u];
+            if (st.penalty != 1.0f && a.seen && ((a.seen[i >> 5] >> (i & 31)) & 1u))
+                v = v > 0.0f ? __fdiv_rn(v, st.penalty) : __fmul_rn(v, st.penalty);
+            v = __fdiv_rn(v, st.temperature);
+            sc[i] = v;
+            mx = fmaxf(mx, v);
+        }
+    }
+    const float M = block_max_f(mx, sh);
+    // Every order below is (scaled logit descending, id ascending): the
+    // reference's top-k sort, and a valid order for its probability sort,
+    // since the probability is a non-decreasing function of the scaled logit.
+    // the key of a cut id, read by its owner
+    auto cut_key = [&](int cut) {
+        const bool own = cut >= L.base && cut < L.end && ((cut - L.base) & 63) == 0;
+        return (uint32_t)block_pick(own, own ? f32_order(sc[cut]) : 0u, sh);
+    };
+    // top-k (0 < k < V): ids after the k-th best key get a scaled logit of
+    // -inf, so their probability is 0
+    const bool use_k = st.top_k > 0 && st.top_k < V;
+    if (use_k) {
+        const int kid = desc_threshold(
+            L, sc, nullptr,
+            [](int, float s, float, uint32_t &k, unsigned long long &w) {
+                k = f32_order(s);
+                w = 1;
+                return true;
+            },
+            (unsigned long long)(st.top_k - 1), sh);
+        if (kid >= 0) {
+            const uint32_t ck = cut_key(kid);
+            gen_each(L, sc, nullptr, [&](int i, float s, float) {
+                const uint32_t k = f32_order(s);
+                if (!(k > ck || (k == ck && i <= kid))) sc[i] = -INFINITY;
+            });
+        }
+    }
+    // softmax over the candidates (dropped ids contribute exp(-inf) = 0):
+    // pr holds exp(s - M), the probability is pr / S
+    float sum = 0.0f;
+    gen_each(L, sc, nullptr, [&](int i, float s, float) {
+        const float e = expf(s - M);
+        pr[i] = e;
+        sum += e;
+    });
+    const float S = block_sum_f(sum, sh);
+    // nucleus: keep through the first cumulative sum above top_p, then
+    // divide by the kept mass
+    bool renorm = false;
+    float sumk = 1.0f;
+    if (st.top_p < 1.0f) {
+        const int cut = desc_threshold(
+            L, sc, pr,
+            [&](int, float s, float p, uint32_t &k, unsigned long long &w) {
+                k = f32_order(s);
+                w = fx(p / S);
+                return true;
+            },
+            fx(st.top_p), sh);
+        if (cut >= 0) {
+            const uint32_t ck = cut_key(cut);
+            unsigned long long mk = 0;
+            gen_each(L, sc, pr, [&](int i, float s, float p) {
+                const uint32_t k = f32_order(s);
+                if (k > ck || (k == ck && i <= cut))
+                    mk += fx(p / S);
+                else
+                    pr[i] = 0.0f;
+            });
+            unsigned long long tot;
+            (void)block_excl_u64(mk, sh, &tot);
+            sumk = (float)((double)tot / kFx);
+            renorm = true;
+        }
+    }
+    auto prob = [&](float p) {
+        const float q = p / S;
+        return renorm ? q / sumk : q;
+    };
+    // the draw: inverse-CDF walk, in descending order with top-k (the
+    // candidates are the sorted ids), else in id order
+    const float r = uniform_f32(st.seed, (unsigned long long)st.step);
+    int pick;
+    if (use_k)
+        pick = desc_threshold(
+            L, sc, pr,
+            [&](int, float s, float p, uint32_t &k, unsigned long long &w) {
+                k = f32_order(s);
+                w = fx(prob(p));
+                return true;
+            },
+            fx(r), sh);
+    else
+        pick = id_threshold(L, [&](int i) { return fx(prob(pr[i])); }, fx(r), sh);
+    if (pick < 0) {
+        // past the last cumulative sum (rounding): the first id with p > 0 in
+        // walk order -- the best key with top-k, else the lowest id
+        unsigned long long best = ~0ull;
+        gen_each(L, sc, pr, [&](int i, float s, float p) {
+            if (!(prob(p) > 0.0f)) return;
+            const unsigned long long k =
+                use_k ? (((unsigned long long)~f32_order(s) << 32) | (uint32_t)i) : (unsigned long long)i;
+            best = k < best ? k : best;
+        });
+        if (t == 0) sh.res[2] = ~0ull;
+        __syncthreads();
+        atomicMin(&sh.res[2], best);
+        __syncthreads();
+        const unsigned long long k = sh.res[2];
+        pick = k == ~0ull ? 0 : (int)(uint32_t)k;
+    }
+    if (t == 0) emit_token(a, pick);
 }
 
 }  // namespace
 
 hipError_t launch_sample(const SampleArgs &a, hipStream_t s) {
+    if (a.V <= 0 || a.V > kSampleMaxVocab) return hipErrorInvalidValue;
     const int nslices = (a.V + kSampleSlice - 1) / kSampleSlice;
     if (a.greedy || a.cand) {
         // top-k (or greedy) path; the host only sets cand when top_k is usable
@@ -398,7 +715,8 @@ hipError_t launch_sample(const SampleArgs &a, hipStream_t s) {
         hipLaunchKernelGGL(sample_select_kernel, dim3(1), dim3(kSelectThreads), 0, s, a, nslices);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(sample_full_kernel, dim3(1), dim3(1024), 0, s, a);
+    if (!a.scratch) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(sample_general_kernel, dim3(1), dim3(kGenThreads), 0, s, a);
     return hipGetLastError();
 }
 
