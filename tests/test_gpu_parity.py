@@ -229,6 +229,37 @@ def test_sampling_teacher_forced(T, O, untied, temp, k, p, pen):
     assert mism <= 1, f"{mism} of 48 sampled ids differ"
 
 
+@pytest.fixture(scope="module")
+def odd_vocab(T, O, W):
+    import dataclasses
+    wl = dataclasses.replace(W.TINY, name="tiny-llama-v777-s13", vocab_size=777, weight_seed=13)
+    p = W.ensure_model(wl, model_root())
+    return T.Model.load(p), O.OracleModel.load(p), wl
+
+
+# a vocabulary that is not a multiple of the sampler's slices, rows or
+# wavefronts; top_p = 0 keeps only the most likely id; top_k = V - 1; a tiny
+# temperature (nearly one-hot probabilities)
+@pytest.mark.parametrize("temp,k,p,pen", [(0.7, 0, 0.0, 1.0), (1.0, 776, 1.0, 1.0), (1.3, 100, 0.5, 1.2),
+                                          (0.05, 0, 0.95, 1.0), (0.9, 30, 0.9, 1.1), (1.0, 0, 1.0, 1.4)])
+def test_sampling_odd_vocab(T, O, odd_vocab, temp, k, p, pen):
+    g, o, wl = odd_vocab
+    prompt = [int(t) for t in T.synth_tokens(29, 9, wl.vocab_size)]
+    out = T.generate(g, prompt, T.GenParams(max_tokens=40, temperature=temp, top_k=k, top_p=p,
+                                            repetition_penalty=pen, seed=5))
+    assert len(out.tokens) == 40
+    assert all(0 <= t < wl.vocab_size for t in out.tokens)
+    ref = O.generate(o, prompt, 40, forced=out.tokens, repetition_penalty=pen, keep_logits=True)
+    mism = 0
+    for i, (tok, lg) in enumerate(zip(out.tokens, ref.step_logits)):
+        tr = O.sample(lg, temp, k, p, device_draw(5, i))
+        mism += tr.token != tok
+        assert tok in set(int(c) for c, pr in zip(tr.cand_ids, tr.cand_probs) if pr > 0), f"step {i}"
+        if p == 0.0:
+            assert tok == int(np.argmax(lg)), f"step {i}: top_p = 0 keeps the most likely id"
+    assert mism <= 1, f"{mism} of 40 sampled ids differ"
+
+
 # --- C2: the 1B-class model, prefill 64 + greedy decode -----------------------
 
 @pytest.fixture(scope="module")
