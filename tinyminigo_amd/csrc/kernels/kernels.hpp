@@ -308,7 +308,7 @@ struct SampleArgs {
     int greedy;       // temperature <= 0: argmax of the penalized logits
     int advance_pos;  // 1 after a decode step, 0 after prefill
     // whole-vocabulary path (cand null, not greedy): [2V] floats (scaled
-    // logits, then unnormalized probabilities)
+    // logits, then probabilities)
     float *scratch;
 };
 

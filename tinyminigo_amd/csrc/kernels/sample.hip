@@ -322,8 +322,8 @@ __global__ __launch_bounds__(kSelectThreads) void sample_select_kernel(const Sam
 // above kSampleMaxK.  One workgroup of kGenThreads.  Wave w owns the ids
 // [w*wsz, (w+1)*wsz) (wsz a multiple of 256), lane l of it the ids
 // w*wsz + 64*j + l, so every pass is coalesced; rows of 256 ids are the
-// units of the id-order searches.  a.scratch holds the scaled logits [V],
-// then the unnormalized probabilities [V].  The orders the reference gets by
+// units of the id-order searches.  a.scratch holds the scaled logits [V]
+// and the probabilities [V].  The orders the reference gets by
 // sorting are found by threshold searches instead: among the selected ids,
 // in a given order, the first at which a running total of weights exceeds
 // a target.  Weight 1 in (scaled logit descending, id ascending) order gives
@@ -364,9 +364,9 @@ struct GenLayout {
 };
 
 // f(i, s, p) over this thread's ids, with s = sc[i] and p = pr[i] (0 when
-// pr is null) loaded eight ids at a time, so a pass keeps eight loads in
-// flight per lane instead of one.
-constexpr int kGenUnroll = 8;
+// pr is null) loaded kGenUnroll ids at a time, so one memory round trip
+// covers 16 ids per lane.
+constexpr int kGenUnroll = 16;
 template <class F>
 __device__ __forceinline__ void gen_each(const GenLayout &L, const float *sc, const float *pr, F f) {
     for (int i0 = L.base; i0 < L.end; i0 += 64 * kGenUnroll) {
@@ -385,7 +385,16 @@ __device__ __forceinline__ void gen_each(const GenLayout &L, const float *sc, co
     }
 }
 
-__device__ __forceinline__ unsigned long long fx(float p) { return (unsigned long long)((double)p * kFx); }
+// floor(p * 2^40) for 0 <= p < 2 (exact: p's 24-bit significand shifted by
+// its exponent); 0 for subnormals, negatives, NaN and p >= 2.
+__device__ __forceinline__ unsigned long long fx(float p) {
+    const uint32_t u = __float_as_uint(p);
+    const int e = (int)(u >> 23);  // with the sign bit set e > 255
+    if (e == 0 || e > 127) return 0ull;
+    const unsigned long long m = (u & 0x7fffffu) | 0x800000u;
+    const int sh = e - 110;  // value = m * 2^(e - 150), times 2^40
+    return sh >= 0 ? m << sh : (sh > -24 ? m >> -sh : 0ull);
+}
 
 __device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
 #pragma unroll
@@ -452,19 +461,38 @@ __device__ unsigned long long block_pick(bool mine, unsigned long long v, GenSha
     return r;
 }
 
-// Threshold search in id order: the first id whose running total of wv(i)
-// (the weight of id i, 0 when not selected; any i < V) exceeds `rest`, or -1
-// when the total does not.  Row totals (thread w*64 + r holds row r of wave
-// w, so thread order is id order), a prefix scan over them, then one
-// wavefront scans the 256 ids of the crossing row.
-template <class Wv>
-__device__ int id_threshold(const GenLayout &L, Wv wv, unsigned long long rest, GenShared &sh) {
+// Threshold search in id order: the first id whose running total of
+// wf(i, s, p) (the weight of id i with s = sc[i], p = pr[i]; 0 when not
+// selected) exceeds `rest`, or -1 when the total does not; *through gets the
+// running total through that id.  Row totals (row
+// r of wave w = its ids w*wsz + 256 r .. +255, i.e. lane l's ids for j =
+// 4r .. 4r+3; thread w*64 + r then holds row r, so thread order is id
+// order), a prefix scan over them, then one wavefront scans the 256 ids of
+// the crossing row.
+template <class Wf>
+__device__ int id_threshold(const GenLayout &L, const float *sc, const float *pr, Wf wf, unsigned long long rest,
+                            GenShared &sh, unsigned long long *through = nullptr) {
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    auto wb = [&](int i) { return i < L.V ? wv(i) : 0ull; };
-    for (int r = 0; r < L.nrow; r++) {
-        const int i = w * L.wsz + r * kGenRow + lane;
-        const unsigned long long v = wave_sum_u64(wb(i) + wb(i + 64) + wb(i + 128) + wb(i + 192));
-        if (lane == 0) sh.rowt[w][r] = v;
+    constexpr int RB = kGenUnroll / 4;  // rows per batch
+    for (int r0 = 0; r0 < L.nrow; r0 += RB) {
+        float sv[kGenUnroll], pv[kGenUnroll];
+#pragma unroll
+        for (int u = 0; u < kGenUnroll; u++) {
+            const int i = L.base + (r0 * 4 + u) * 64;
+            sv[u] = i < L.end ? sc[i] : 0.0f;
+            pv[u] = pr && i < L.end ? pr[i] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < RB; q++) {
+            unsigned long long v = 0;
+#pragma unroll
+            for (int u = 4 * q; u < 4 * q + 4; u++) {
+                const int i = L.base + (r0 * 4 + u) * 64;
+                if (i < L.end) v += wf(i, sv[u], pv[u]);
+            }
+            v = wave_sum_u64(v);
+            if (lane == 0 && r0 + q < L.nrow) sh.rowt[w][r0 + q] = v;
+        }
     }
     __syncthreads();
     const unsigned long long c = lane < L.nrow ? sh.rowt[w][lane] : 0ull;
@@ -482,7 +510,8 @@ __device__ int id_threshold(const GenLayout &L, Wv wv, unsigned long long rest, 
         unsigned long long q[4], m = 0;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            q[k] = wb(first + 4 * lane + k);
+            const int i = first + 4 * lane + k;
+            q[k] = i < L.V ? wf(i, sc[i], pr ? pr[i] : 0.0f) : 0ull;
             m += q[k];
         }
         const unsigned long long incl = wave_incl_u64(m);
@@ -492,6 +521,7 @@ __device__ int id_threshold(const GenLayout &L, Wv wv, unsigned long long rest, 
                 cu += q[k];
                 if (cu > left) {
                     sh.res[2] = (unsigned long long)(first + 4 * lane + k);
+                    sh.res[3] = rest - left + cu;  // running total through this id
                     break;
                 }
             }
@@ -499,6 +529,7 @@ __device__ int id_threshold(const GenLayout &L, Wv wv, unsigned long long rest, 
     }
     __syncthreads();
     const unsigned long long r = sh.res[2];
+    if (through) *through = sh.res[3];
     __syncthreads();
     return r == ~0ull ? -1 : (int)r;
 }
@@ -508,11 +539,12 @@ __device__ int id_threshold(const GenLayout &L, Wv wv, unsigned long long rest, 
 // key k (uint32, larger first) and weight w.  A radix search over the key
 // (12, 12, then 8 bits) finds the key at which the running total crosses
 // `target`; ties at that key go in id order.  Returns the id, or -1 when the
-// total of all selected ids does not exceed the target.  Ids of weight 0
-// can never be the answer and are skipped.
+// total of all selected ids does not exceed the target; *through gets the
+// running total through the returned id.  Ids of weight 0 can never be the
+// answer and are skipped.
 template <class Kw>
 __device__ int desc_threshold(const GenLayout &L, const float *sc, const float *pr, Kw kw,
-                              unsigned long long target, GenShared &sh) {
+                              unsigned long long target, GenShared &sh, unsigned long long *through = nullptr) {
     const int t = threadIdx.x;
     uint32_t pfx = 0;                  // key bits decided so far
     unsigned long long rest = target;  // target left after the heavier bins
@@ -558,14 +590,17 @@ __device__ int desc_threshold(const GenLayout &L, const float *sc, const float *
         pfx = (pfx << (lv == 2 ? 8 : 12)) | (uint32_t)(r >> 52);
         rest -= r & ((1ull << 52) - 1);
     }
-    return id_threshold(
-        L,
-        [&](int i) {
+    const int id = id_threshold(
+        L, sc, pr,
+        [&](int i, float s, float p) {
             uint32_t k;
             unsigned long long v;
-            return kw(i, sc[i], pr ? pr[i] : 0.0f, k, v) && k == pfx ? v : 0ull;
+            return kw(i, s, p, k, v) && k == pfx ? v : 0ull;
         },
-        rest, sh);
+        rest, sh, through);
+    // the ties' running total starts after the heavier keys' target - rest
+    if (id >= 0 && through) *through += target - rest;
+    return id;
 }
 
 __global__ __launch_bounds__(kGenThreads) void sample_general_kernel(const SampleArgs a) {
@@ -596,19 +631,22 @@ __global__ __launch_bounds__(kGenThreads) void sample_general_kernel(const Sampl
         }
     }
     const float M = block_max_f(mx, sh);
-    // Every order below is (scaled logit descending, id ascending): the
-    // reference's top-k sort, and a valid order for its probability sort,
-    // since the probability is a non-decreasing function of the scaled logit.
-    // the key of a cut id, read by its owner
-    auto cut_key = [&](int cut) {
+    // The orders below are (key descending, id ascending) with the scaled
+    // logit as key for top-k and the walk after it -- the reference's sort --
+    // and the probability for the nucleus, whose sort leaves ties
+    // unspecified.
+    // the key of a cut id (read by its owner), from array v
+    auto cut_key = [&](const float *v, int cut) {
         const bool own = cut >= L.base && cut < L.end && ((cut - L.base) & 63) == 0;
-        return (uint32_t)block_pick(own, own ? f32_order(sc[cut]) : 0u, sh);
+        return (uint32_t)block_pick(own, own ? f32_order(v[cut]) : 0u, sh);
     };
-    // top-k (0 < k < V): ids after the k-th best key get a scaled logit of
-    // -inf, so their probability is 0
+    // top-k (0 < k < V): the k-th best scaled logit (kk, id kid); ids after
+    // it in the order are not candidates
     const bool use_k = st.top_k > 0 && st.top_k < V;
+    uint32_t kk = 0;
+    int kid = V;
     if (use_k) {
-        const int kid = desc_threshold(
+        kid = desc_threshold(
             L, sc, nullptr,
             [](int, float s, float, uint32_t &k, unsigned long long &w) {
                 k = f32_order(s);
@@ -616,58 +654,43 @@ __global__ __launch_bounds__(kGenThreads) void sample_general_kernel(const Sampl
                 return true;
             },
             (unsigned long long)(st.top_k - 1), sh);
-        if (kid >= 0) {
-            const uint32_t ck = cut_key(kid);
-            gen_each(L, sc, nullptr, [&](int i, float s, float) {
-                const uint32_t k = f32_order(s);
-                if (!(k > ck || (k == ck && i <= kid))) sc[i] = -INFINITY;
-            });
-        }
+        if (kid < 0) kid = V;  // unreachable: the count always exceeds k - 1
+        kk = kid < V ? cut_key(sc, kid) : 0u;
     }
-    // softmax over the candidates (dropped ids contribute exp(-inf) = 0):
-    // pr holds exp(s - M), the probability is pr / S
+    // softmax over the candidates: pr = exp(s - M) (0 for non-candidates),
+    // S their sum, then pr = pr / S, the reference's probabilities
     float sum = 0.0f;
     gen_each(L, sc, nullptr, [&](int i, float s, float) {
-        const float e = expf(s - M);
+        const uint32_t k = f32_order(s);
+        const float e = (!use_k || k > kk || (k == kk && i <= kid)) ? expf(s - M) : 0.0f;
         pr[i] = e;
         sum += e;
     });
     const float S = block_sum_f(sum, sh);
-    // nucleus: keep through the first cumulative sum above top_p, then
-    // divide by the kept mass
-    bool renorm = false;
-    float sumk = 1.0f;
+    gen_each(L, pr, nullptr, [&](int i, float e, float) { pr[i] = e / S; });
+    // nucleus: keep through the first cumulative probability above top_p (in
+    // probability order), then divide the kept probabilities by their sum
     if (st.top_p < 1.0f) {
+        unsigned long long kept = 0;
         const int cut = desc_threshold(
-            L, sc, pr,
-            [&](int, float s, float p, uint32_t &k, unsigned long long &w) {
-                k = f32_order(s);
-                w = fx(p / S);
+            L, pr, nullptr,
+            [&](int, float p, float, uint32_t &k, unsigned long long &w) {
+                k = f32_order(p);
+                w = fx(p);
                 return true;
             },
-            fx(st.top_p), sh);
+            fx(st.top_p), sh, &kept);
         if (cut >= 0) {
-            const uint32_t ck = cut_key(cut);
-            unsigned long long mk = 0;
-            gen_each(L, sc, pr, [&](int i, float s, float p) {
-                const uint32_t k = f32_order(s);
-                if (k > ck || (k == ck && i <= cut))
-                    mk += fx(p / S);
-                else
-                    pr[i] = 0.0f;
+            const uint32_t ck = cut_key(pr, cut);
+            const float sumk = (float)((double)kept / kFx);
+            gen_each(L, pr, nullptr, [&](int i, float p, float) {
+                const uint32_t k = f32_order(p);
+                pr[i] = (k > ck || (k == ck && i <= cut)) ? p / sumk : 0.0f;
             });
-            unsigned long long tot;
-            (void)block_excl_u64(mk, sh, &tot);
-            sumk = (float)((double)tot / kFx);
-            renorm = true;
         }
     }
-    auto prob = [&](float p) {
-        const float q = p / S;
-        return renorm ? q / sumk : q;
-    };
-    // the draw: inverse-CDF walk, in descending order with top-k (the
-    // candidates are the sorted ids), else in id order
+    // the draw: inverse-CDF walk, in descending scaled-logit order with top-k
+    // (the candidates are the sorted ids), else in id order
     const float r = uniform_f32(st.seed, (unsigned long long)st.step);
     int pick;
     if (use_k)
@@ -675,18 +698,18 @@ __global__ __launch_bounds__(kGenThreads) void sample_general_kernel(const Sampl
             L, sc, pr,
             [&](int, float s, float p, uint32_t &k, unsigned long long &w) {
                 k = f32_order(s);
-                w = fx(prob(p));
+                w = fx(p);
                 return true;
             },
             fx(r), sh);
     else
-        pick = id_threshold(L, [&](int i) { return fx(prob(pr[i])); }, fx(r), sh);
+        pick = id_threshold(L, pr, nullptr, [&](int, float p, float) { return fx(p); }, fx(r), sh);
     if (pick < 0) {
         // past the last cumulative sum (rounding): the first id with p > 0 in
         // walk order -- the best key with top-k, else the lowest id
         unsigned long long best = ~0ull;
         gen_each(L, sc, pr, [&](int i, float s, float p) {
-            if (!(prob(p) > 0.0f)) return;
+            if (!(p > 0.0f)) return;
             const unsigned long long k =
                 use_k ? (((unsigned long long)~f32_order(s) << 32) | (uint32_t)i) : (unsigned long long)i;
             best = k < best ? k : best;
