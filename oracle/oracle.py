@@ -58,6 +58,10 @@ def _load_lib():
         "om_attention_batch": (None, [PF, PF, PF, S, S, S, S, S, PF]),
         "om_apply_repetition_penalty": (None, [PF, S, PU32, S, F]),
         "om_sample": (S, [PF, S, F, S, F, F, PU32, PF, C.POINTER(S)]),
+        "om_chacha_block": (None, [PU32, C.c_uint64, C.c_uint64, C.c_int, PU32]),
+        "om_pcg_xsh_rr": (C.c_uint32, [C.c_uint64]),
+        "om_stdrng_key": (None, [C.c_uint64, PU32]),
+        "om_stdrng_uniform": (None, [C.c_uint64, S, PF]),
         "om_model_new": (C.c_void_p, [C.c_void_p]),
         "om_model_free": (None, [C.c_void_p]),
         "om_cache_new": (C.c_void_p, [C.c_int, S]),
@@ -258,6 +262,31 @@ class SampleTrace:
     token: int
     cand_ids: np.ndarray  # candidate ids in walk order
     cand_probs: np.ndarray  # final probabilities (after the nucleus cut)
+
+
+def chacha_block(key, counter: int, stream: int, rounds: int) -> np.ndarray:
+    k = np.ascontiguousarray(key, np.uint32)
+    out = np.empty(16, np.uint32)
+    lib.om_chacha_block(u32p(k), counter, stream, rounds, u32p(out))
+    return out
+
+
+def pcg_xsh_rr(state: int) -> int:
+    return int(lib.om_pcg_xsh_rr(state))
+
+
+def stdrng_key(seed: int) -> np.ndarray:
+    out = np.empty(8, np.uint32)
+    lib.om_stdrng_key(seed, u32p(out))
+    return out
+
+
+def stdrng_uniform(seed: int, n: int) -> np.ndarray:
+    """The first n `StandardUniform` f32 draws of `StdRng::seed_from_u64(seed)`
+    (src/model.rs:629, src/tensor.rs:1204), restated."""
+    out = np.empty(max(n, 1), np.float32)
+    lib.om_stdrng_uniform(seed, n, fp(out))
+    return out[:n]
 
 
 def sample(logits, temperature: float, top_k: int, top_p: float, r: float) -> SampleTrace:
@@ -627,9 +656,10 @@ class OracleGen:
 def generate(model: OracleModel, prompt: Sequence[int], max_tokens: int, temperature: float = 0.0,
              top_k: int = 0, top_p: float = 1.0, repetition_penalty: float = 1.0,
              draws: Optional[Callable[[int], float]] = None, forced: Optional[Sequence[int]] = None,
-             keep_logits: bool = False) -> OracleGen:
-    """generate (src/model.rs:614-663).  `draws(i)` supplies the uniform of
-    step i when sampling; `forced` replays given ids (teacher forcing) while
+             keep_logits: bool = False, seed: int = 0) -> OracleGen:
+    """generate (src/model.rs:614-663).  When sampling, step i's uniform is
+    `draws(i)` if given, else draw i of StdRng::seed_from_u64(seed)
+    (stdrng_uniform); `forced` replays given ids (teacher forcing) while
     still recording the logits each one was chosen from."""
     if len(prompt) == 0:
         raise OracleError("empty prompt")
@@ -649,7 +679,10 @@ def generate(model: OracleModel, prompt: Sequence[int], max_tokens: int, tempera
         elif temperature <= 0.0:
             nxt = argmax(logits)
         else:
-            nxt = sample(logits, temperature, top_k, top_p, draws(i) if draws else 0.5).token
+            if draws is None:
+                stream = stdrng_uniform(seed, max_tokens)
+                draws = lambda j: float(stream[j])  # noqa: E731
+            nxt = sample(logits, temperature, top_k, top_p, draws(i)).token
         generated.append(nxt)
         if nxt in eos:
             break

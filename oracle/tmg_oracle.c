@@ -749,6 +749,81 @@ static int cmp_desc(const void *a, const void *b) {
     return ia < ib ? -1 : (ia > ib ? 1 : 0);
 }
 
+/* ---- the reference's RNG: StdRng::seed_from_u64 + StandardUniform f32 ----
+ * generate (src/model.rs:629) makes StdRng::seed_from_u64(params.seed) and
+ * sample (src/tensor.rs:1204) draws one StandardUniform f32 per sampled
+ * step.  Those live in the crates rand 0.10.2, rand_core 0.10.1 and
+ * chacha20 0.10.2 (Cargo.lock:744-752, :774-777, :140-143), whose sources
+ * are not in the reference tree; this restates their published algorithms:
+ *   - seed_from_u64 (rand_core): the 32-byte seed is eight outputs of a
+ *     PCG32 stream, each little-endian -- per output the 64-bit state first
+ *     advances (state * 6364136223846793005 + 11634580027462260723), then the
+ *     XSH-RR output function of the new state;
+ *   - StdRng = ChaCha12Rng (chacha20): key = the seed, 64-bit block counter
+ *     from 0 in words 12-13, stream 0 in words 14-15, 12 rounds; next_u32
+ *     returns the blocks' 16 words in order;
+ *   - StandardUniform f32 (rand): (next_u32 >> 8) * 2^-24.
+ * The ChaCha block function is pinned by the RFC 7539 vectors at 20 rounds,
+ * the XSH-RR output function by the PCG reference demo sequence; the
+ * constants specific to the crates are restated, not pinned (no vectors of
+ * theirs are available offline). */
+
+static uint32_t om_rotl32(uint32_t x, int n) { return (x << n) | (x >> (32 - n)); }
+
+#define OM_QR(a, b, c, d)                   \
+    do {                                    \
+        x[a] += x[b]; x[d] = om_rotl32(x[d] ^ x[a], 16); \
+        x[c] += x[d]; x[b] = om_rotl32(x[b] ^ x[c], 12); \
+        x[a] += x[b]; x[d] = om_rotl32(x[d] ^ x[a], 8);  \
+        x[c] += x[d]; x[b] = om_rotl32(x[b] ^ x[c], 7);  \
+    } while (0)
+
+/* One ChaCha block: constants, key[8], counter (words 12-13), stream
+ * (words 14-15); `rounds` even. */
+OM_API void om_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, int rounds,
+                            uint32_t out[16]) {
+    uint32_t s[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u};
+    for (int i = 0; i < 8; i++) s[4 + i] = key[i];
+    s[12] = (uint32_t)counter;
+    s[13] = (uint32_t)(counter >> 32);
+    s[14] = (uint32_t)stream;
+    s[15] = (uint32_t)(stream >> 32);
+    uint32_t x[16];
+    memcpy(x, s, sizeof(x));
+    for (int r = 0; r < rounds; r += 2) {
+        OM_QR(0, 4, 8, 12); OM_QR(1, 5, 9, 13); OM_QR(2, 6, 10, 14); OM_QR(3, 7, 11, 15);
+        OM_QR(0, 5, 10, 15); OM_QR(1, 6, 11, 12); OM_QR(2, 7, 8, 13); OM_QR(3, 4, 9, 14);
+    }
+    for (int i = 0; i < 16; i++) out[i] = x[i] + s[i];
+}
+
+/* PCG XSH-RR output function of a 64-bit state. */
+OM_API uint32_t om_pcg_xsh_rr(uint64_t state) {
+    const uint32_t xorshifted = (uint32_t)(((state >> 18) ^ state) >> 27);
+    const unsigned rot = (unsigned)(state >> 59);
+    return (xorshifted >> rot) | (xorshifted << ((32 - rot) & 31));
+}
+
+/* seed_from_u64: the eight key words. */
+OM_API void om_stdrng_key(uint64_t seed, uint32_t key[8]) {
+    uint64_t state = seed;
+    for (int i = 0; i < 8; i++) {
+        state = state * 6364136223846793005ull + 11634580027462260723ull;
+        key[i] = om_pcg_xsh_rr(state);
+    }
+}
+
+/* The first n StandardUniform f32 draws of StdRng::seed_from_u64(seed). */
+OM_API void om_stdrng_uniform(uint64_t seed, size_t n, float *out) {
+    uint32_t key[8], blk[16];
+    om_stdrng_key(seed, key);
+    for (size_t j = 0; j < n; j++) {
+        if (j % 16 == 0) om_chacha_block(key, (uint64_t)(j / 16), 0, 12, blk);
+        out[j] = (float)(blk[j % 16] >> 8) * (1.0f / 16777216.0f);
+    }
+}
+
+
 /* sample (src/tensor.rs:1157-1213) with the uniform draw r supplied by the
  * caller (the reference draws it from rand's StdRng, which cannot run here).
  * Optional outputs: the candidate ids in walk order (cand_ids, n_cand) and

@@ -1,0 +1,75 @@
+"""The reference's sampling draws (StdRng::seed_from_u64 + StandardUniform
+f32, src/model.rs:629 and src/tensor.rs:1204): the oracle's restatement
+against published vectors, and the library's own copy against the oracle.
+
+rand 0.10.2 / rand_core 0.10.1 / chacha20 0.10.2 are not in the reference
+tree.  The ChaCha block function is pinned by RFC 7539 (20 rounds; the
+12-round StdRng runs the same double round six times), the PCG XSH-RR output
+function by the PCG reference demo; the crates' own constants (seed
+expansion increment, 12 rounds, the f32 conversion) are restated and
+unpinned."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+
+def test_chacha_block_rfc7539():
+    # RFC 7539 section 2.3.2: key 00..1f, nonce 00:00:00:09:00:00:00:4a:00:00:00:00,
+    # block count 1 (words 12..15 = 1, 0x09000000, 0x4a000000, 0)
+    key = np.array([int.from_bytes(bytes(range(4 * i, 4 * i + 4)), "little") for i in range(8)], np.uint32)
+    out = O.chacha_block(key, (0x09000000 << 32) | 1, 0x4a000000, 20)
+    assert [int(x) for x in out] == [
+        0xe4e7f110, 0x15593bd1, 0x1fdd0f50, 0xc47120a3, 0xc7f4d1c7, 0x0368c033, 0x9aaa2204, 0x4e6cd4c3,
+        0x466482d2, 0x09aa9f07, 0x05d7c214, 0xa2028bd9, 0xd19c12b5, 0xb94e16de, 0xe883d0cb, 0x4e3c50a2]
+    # RFC 7539 appendix A.1, test vector 1: all-zero key, nonce and counter
+    z = O.chacha_block(np.zeros(8, np.uint32), 0, 0, 20)
+    assert b"".join(int(x).to_bytes(4, "little") for x in z).hex() == (
+        "76b8e0ada0f13d90405d6ae55386bd28bdd219b8a08ded1aa836efcc8b770dc7"
+        "da41597c5157488d7724e03fb8d84a376a43b8f41518a11cc387b669b2ee6586")
+
+
+def test_chacha_rounds_and_counter():
+    key = O.stdrng_key(5)
+    # fewer rounds give a different block; the counter and stream words move it
+    assert not np.array_equal(O.chacha_block(key, 0, 0, 12), O.chacha_block(key, 0, 0, 20))
+    assert not np.array_equal(O.chacha_block(key, 0, 0, 12), O.chacha_block(key, 1, 0, 12))
+    assert not np.array_equal(O.chacha_block(key, 0, 0, 12), O.chacha_block(key, 0, 1, 12))
+
+
+def test_pcg_output_function_demo_sequence():
+    # pcg32 reference demo (srandom(42, 54)): output of the state before each
+    # advance, increment (54 << 1) | 1
+    M, MASK, inc = 6364136223846793005, 2**64 - 1, (54 << 1) | 1
+    st = ((0 * M + inc) & MASK) + 42
+    st = (st * M + inc) & MASK
+    outs = []
+    for _ in range(6):
+        old, st = st, (st * M + inc) & MASK
+        outs.append(O.pcg_xsh_rr(old))
+    assert outs == [0xa15c02b7, 0x7b47f409, 0xba1d3330, 0x83d2f293, 0xbfa4784b, 0xcbed606e]
+
+
+def test_stdrng_stream_structure():
+    seed = 987654321
+    key = O.stdrng_key(seed)
+    # seed expansion: eight PCG32 outputs, the state advanced before each
+    M, INC, MASK = 6364136223846793005, 11634580027462260723, 2**64 - 1
+    st, exp = seed, []
+    for _ in range(8):
+        st = (st * M + INC) & MASK
+        exp.append(O.pcg_xsh_rr(st))
+    assert [int(x) for x in key] == exp
+    # draws: the ChaCha12 words of blocks 0, 1, ... in order, top 24 bits
+    u = O.stdrng_uniform(seed, 40)
+    words = np.concatenate([O.chacha_block(key, b, 0, 12) for b in range(3)])[:40]
+    assert np.array_equal(u, ((words >> 8).astype(np.float64) * 2.0**-24).astype(np.float32))
+    assert u.min() >= 0.0 and u.max() < 1.0
+
+
+def test_library_stdrng_matches_oracle():
+    T = pytest.importorskip("tinyminigo_amd")
+    for seed in (0, 1, 42, 2**64 - 1, 1234567890123):
+        assert np.array_equal(T.stdrng_uniform(seed, 300), O.stdrng_uniform(seed, 300)), seed
+    big = T.stdrng_uniform(42, 20000)
+    assert abs(float(big.mean()) - 0.5) < 0.01

@@ -15,6 +15,9 @@ namespace tmg {
 // Sets the thread-local error text and returns `code`.
 int set_error(int code, const std::string &msg);
 void clear_error();
+// The first n draws of the reference's StdRng::seed_from_u64(seed) +
+// StandardUniform f32 (stdrng.cpp).
+void stdrng_uniform(uint64_t seed, size_t n, float *out);
 
 // ---- safetensors (reference src/safetensors_loader.rs:103-147) ----------
 

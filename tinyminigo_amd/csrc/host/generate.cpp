@@ -20,21 +20,6 @@ namespace {
 
 constexpr int kWindow = 4;
 
-uint64_t fnv1a64(const char *s) {
-    uint64_t h = 0xcbf29ce484222325ull;
-    for (; *s; s++) {
-        h ^= (unsigned char)*s;
-        h *= 0x100000001b3ull;
-    }
-    return h;
-}
-
-uint64_t mix64(uint64_t z) {
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    return z ^ (z >> 31);
-}
-
 struct CacheGuard {
     tmg_cache *c = nullptr;
     ~CacheGuard() { tmg_cache_free(c); }
@@ -102,8 +87,15 @@ extern "C" int tmg_generate(tmg_model *m, const uint32_t *prompt, size_t n_promp
     st.top_k = use_k ? (int)p->top_k : 0;
     st.top_p = p->top_p;
     st.penalty = p->repetition_penalty;
-    st.seed = mix64((p->seed * 0x9E3779B97F4A7C15ull) ^ fnv1a64("sample"));
     TMG_HIPG(hipMemcpy(c->st, &st, sizeof(st), hipMemcpyHostToDevice));
+    if (!greedy && p->max_tokens > 0) {
+        // the reference's StdRng::seed_from_u64(seed) stream: one
+        // StandardUniform f32 per sampled step (src/model.rs:629,
+        // src/tensor.rs:1204)
+        std::vector<float> draws(p->max_tokens);
+        stdrng_uniform(p->seed, draws.size(), draws.data());
+        TMG_HIPG(hipMemcpy(c->draws, draws.data(), draws.size() * 4, hipMemcpyHostToDevice));
+    }
     if (step_graphs_enabled() && (rc = get_step_graph(m, c, mode))) return rc;
 
     // prefill (timed like the reference, src/model.rs:622-624)

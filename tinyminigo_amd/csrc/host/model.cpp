@@ -502,6 +502,8 @@ int enqueue_select(tmg_model *m, tmg_cache *c, int mode, int advance_pos) {
     sa.seen_rw = c->seen;
     sa.cand = mode == SEL_FULL ? nullptr : c->cand;
     sa.scratch = c->gsc;
+    sa.draws = c->draws;
+    sa.n_draws = (int)c->max_pos + 2;
     sa.history = c->history;
     sa.hist_cap = (int)c->max_pos + 2;
     sa.greedy = mode == SEL_PENALTY_ARGMAX;
@@ -979,14 +981,18 @@ extern "C" int tmg_cache_new(tmg_model *m, uint32_t max_pos, tmg_cache **out) {
     c->history = (int *)hist;
     const size_t seen_words = ((size_t)m->V + 31) / 32;
     const size_t nslices = ((size_t)m->V + kSampleSlice - 1) / kSampleSlice;
-    void *seen = nullptr, *cand = nullptr, *gsc = nullptr;
+    void *seen = nullptr, *cand = nullptr, *gsc = nullptr, *draws = nullptr;
     if (!rc && (hipMalloc(&seen, seen_words * 4) != hipSuccess ||
                 hipMalloc(&cand, nslices * kSampleMaxK * 8) != hipSuccess ||
-                hipMalloc(&gsc, (size_t)m->V * 8) != hipSuccess))
+                hipMalloc(&gsc, (size_t)m->V * 8) != hipSuccess ||
+                hipMalloc(&draws, ((size_t)max_pos + 2) * 4) != hipSuccess))
         rc = set_error(TMG_E_NOMEM, "sampler buffer allocation failed");
     c->seen = (unsigned *)seen;
     c->cand = (unsigned long long *)cand;
     c->gsc = (float *)gsc;
+    c->draws = (float *)draws;
+    if (!rc && hipMemset(c->draws, 0, ((size_t)max_pos + 2) * 4) != hipSuccess)
+        rc = set_error(TMG_E_DEVICE, "hipMemset failed");
     if (!rc && hipMemset(c->seen, 0, seen_words * 4) != hipSuccess) rc = set_error(TMG_E_DEVICE, "hipMemset failed");
     if (!rc) {
         DevState init{};
@@ -1028,6 +1034,7 @@ extern "C" void tmg_cache_free(tmg_cache *c) {
     (void)hipFree(c->seen);
     (void)hipFree(c->cand);
     (void)hipFree(c->gsc);
+    (void)hipFree(c->draws);
     (void)hipFree(c->bar);
     (void)hipFree(c->plan);
     (void)hipFree(c->k);

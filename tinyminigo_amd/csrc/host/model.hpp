@@ -84,6 +84,7 @@ struct tmg_cache {
     int attn_nsplit = 1;               // split-K width of decode attention for this cache
     unsigned *seen = nullptr;          // bitmap of generated ids (repetition penalty)
     unsigned long long *cand = nullptr;  // sampler candidates
+    float *draws = nullptr;              // [max_pos + 2] uniform draw per step (sampling)
     float *gsc = nullptr;                // [2V] scratch of the whole-vocabulary sampler
     tmg::GridBar *bar = nullptr;       // persistent-kernel barrier counters
     tmg::PersistPlan *plan = nullptr;  // persistent-kernel argument blocks

@@ -27,7 +27,6 @@ struct DevState {
     int top_k;   // 0 or >= vocab: no top-k
     float top_p;
     float penalty;
-    unsigned long long seed;
 };
 
 enum GemvPro { PRO_PLAIN = 0, PRO_NORM = 1, PRO_NORM_BATCH = 2, PRO_EMBED_NORM = 3, PRO_ATTN_COMBINE = 4 };
@@ -310,6 +309,10 @@ struct SampleArgs {
     // whole-vocabulary path (cand null, not greedy): [2V] floats (scaled
     // logits, then probabilities)
     float *scratch;
+    // uniform draw of each step (the reference's StdRng stream), indexed by
+    // st->step; steps at or past n_draws use 0
+    const float *draws;
+    int n_draws;
 };
 
 hipError_t launch_sample(const SampleArgs &a, hipStream_t s);

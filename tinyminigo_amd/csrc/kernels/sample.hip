@@ -26,17 +26,10 @@
 namespace tmg {
 namespace {
 
-constexpr unsigned long long kGamma = 0x9E3779B97F4A7C15ull;
-
-__device__ __forceinline__ unsigned long long mix64(unsigned long long z) {
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    return z ^ (z >> 31);
-}
-
-// Uniform f32 in [0, 1) with 24 random bits, draw `i` of stream `key`.
-__device__ __forceinline__ float uniform_f32(unsigned long long key, unsigned long long i) {
-    return (float)(mix64(key + (i + 1) * kGamma) >> 40) * 0x1.0p-24f;
+// The uniform draw of the running step (the reference's StdRng stream,
+// computed on the host).
+__device__ __forceinline__ float step_draw(const SampleArgs &a, int step) {
+    return step >= 0 && step < a.n_draws ? a.draws[step] : 0.0f;
 }
 
 __device__ __forceinline__ float key_value(unsigned long long key) {
@@ -298,7 +291,7 @@ __global__ __launch_bounds__(kSelectThreads) void sample_select_kernel(const Sam
         p = lane < cutoff ? p / s2 : 0.0f;
     }
     // inverse-CDF walk in candidate order (src/tensor.rs:1203-1212)
-    const float r = uniform_f32(st.seed, (unsigned long long)st.step);
+    const float r = step_draw(a, st.step);
     float cum = 0.0f;
     int pick = -1;
     for (int i = 0; i < K; i++) {
@@ -691,7 +684,7 @@ __global__ __launch_bounds__(kGenThreads) void sample_general_kernel(const Sampl
     }
     // the draw: inverse-CDF walk, in descending scaled-logit order with top-k
     // (the candidates are the sorted ids), else in id order
-    const float r = uniform_f32(st.seed, (unsigned long long)st.step);
+    const float r = step_draw(a, st.step);
     int pick;
     if (use_k)
         pick = desc_threshold(

@@ -245,6 +245,14 @@ def generate(model: Model, prompt_tokens: Sequence[int], params: GenParams,
                      prefill_secs=secs.value)
 
 
+def stdrng_uniform(seed: int, n: int) -> np.ndarray:
+    """The uniform draws `generate` samples with: StdRng::seed_from_u64(seed)
+    (src/model.rs:629), one StandardUniform f32 per step (src/tensor.rs:1204)."""
+    out = np.empty(max(n, 1), np.float32)
+    check(lib.tmg_stdrng_uniform(seed, n, _fptr(out)))
+    return out[:n]
+
+
 def gemv_bf16(w_dev: int, x_dev: int, y_dev: int, out: int, in_: int, stream: int = 0) -> None:
     """tensor::matmul_w (src/tensor.rs:315-338) on device pointers."""
     check(lib.tmg_gemv_bf16(C.c_void_p(w_dev), C.c_void_p(x_dev), C.c_void_p(y_dev), out, in_,
