@@ -984,7 +984,7 @@ extern "C" int tmg_cache_new(tmg_model *m, uint32_t max_pos, tmg_cache **out) {
     void *seen = nullptr, *cand = nullptr, *gsc = nullptr, *draws = nullptr;
     if (!rc && (hipMalloc(&seen, seen_words * 4) != hipSuccess ||
                 hipMalloc(&cand, nslices * kSampleMaxK * 8) != hipSuccess ||
-                hipMalloc(&gsc, (size_t)m->V * 8) != hipSuccess ||
+                hipMalloc(&gsc, (size_t)m->V * 8 + 4 * 128 * 4) != hipSuccess ||
                 hipMalloc(&draws, ((size_t)max_pos + 2) * 4) != hipSuccess))
         rc = set_error(TMG_E_NOMEM, "sampler buffer allocation failed");
     c->seen = (unsigned *)seen;

@@ -85,7 +85,7 @@ struct tmg_cache {
     unsigned *seen = nullptr;          // bitmap of generated ids (repetition penalty)
     unsigned long long *cand = nullptr;  // sampler candidates
     float *draws = nullptr;              // [max_pos + 2] uniform draw per step (sampling)
-    float *gsc = nullptr;                // [2V] scratch of the whole-vocabulary sampler
+    float *gsc = nullptr;                // [2V + 512] scratch of the whole-vocabulary sampler
     tmg::GridBar *bar = nullptr;       // persistent-kernel barrier counters
     tmg::PersistPlan *plan = nullptr;  // persistent-kernel argument blocks
     bool persist_broken = false;       // a barrier timed out: use the graph path

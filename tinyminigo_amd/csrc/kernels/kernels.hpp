@@ -306,8 +306,9 @@ struct SampleArgs {
     int hist_cap;
     int greedy;       // temperature <= 0: argmax of the penalized logits
     int advance_pos;  // 1 after a decode step, 0 after prefill
-    // whole-vocabulary path (cand null, not greedy): [2V] floats (scaled
-    // logits, then probabilities)
+    // whole-vocabulary path (cand null, not greedy): [2V + 512] floats
+    // (scaled logits, probabilities, 128 partial maxima, 128 partial sums,
+    // 128 u64 partial masses)
     float *scratch;
     // uniform draw of each step (the reference's StdRng stream), indexed by
     // st->step; steps at or past n_draws use 0

@@ -316,7 +316,8 @@ __global__ __launch_bounds__(kSelectThreads) void sample_select_kernel(const Sam
 // [w*wsz, (w+1)*wsz) (wsz a multiple of 256), lane l of it the ids
 // w*wsz + 64*j + l, so every pass is coalesced; rows of 256 ids are the
 // units of the id-order searches.  a.scratch holds the scaled logits [V]
-// and the probabilities [V].  The orders the reference gets by
+// and the probabilities [V]; three wide kernels before it compute them (the
+// probabilities only without top-k).  The orders the reference gets by
 // sorting are found by threshold searches instead: among the selected ids,
 // in a given order, the first at which a running total of weights exceeds
 // a target.  Weight 1 in (scaled logit descending, id ascending) order gives
@@ -596,34 +597,115 @@ __device__ int desc_threshold(const GenLayout &L, const float *sc, const float *
     return id;
 }
 
+// The elementwise front of the whole-vocabulary path, over many workgroups:
+// each workgroup of 256 threads takes 2048 ids (thread t: ids g*2048 +
+// 256 j + t).  a.scratch: sc [V] | pr [V] | part [kGenParts] maxima |
+// part [kGenParts] sums | u64 part [kGenParts] walk masses.
+constexpr int kGenWide = 2048;
+constexpr int kGenParts = kSampleMaxVocab / kGenWide;
+static_assert(kGenParts == 128 && kGenParts <= kBlock, "the scratch layout reserves 128 partials of each kind");
+
+__device__ __forceinline__ float wg_reduce(float v, bool is_max, float *red4) {
+    v = is_max ? wave_max(v) : wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return is_max ? fmaxf(fmaxf(red4[0], red4[1]), fmaxf(red4[2], red4[3])) : (red4[0] + red4[1]) + (red4[2] + red4[3]);
+}
+
+// The maximum of the first n partials (every workgroup reads the same
+// values in the same order, so all get the same result).
+__device__ __forceinline__ float parts_max(const float *part, int n, float *red4) {
+    float m = -INFINITY;
+    for (int i = threadIdx.x; i < n; i += kBlock) m = fmaxf(m, part[i]);
+    const float r = wg_reduce(m, true, red4);
+    __syncthreads();
+    return r;
+}
+
+// pass 1: scaled logits (penalty, temperature; src/tensor.rs:1142-1154,
+// :1168) and the workgroup maximum
+__global__ __launch_bounds__(kBlock) void sample_scale_kernel(const SampleArgs a) {
+    __shared__ float red4[4];
+    const DevState st = *a.st;
+    const int base = blockIdx.x * kGenWide + threadIdx.x;
+    float lv[kGenWide / kBlock];
+#pragma unroll
+    for (int j = 0; j < kGenWide / kBlock; j++) {
+        const int i = base + j * kBlock;
+        lv[j] = i < a.V ? a.logits[i] : 0.0f;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kGenWide / kBlock; j++) {
+        const int i = base + j * kBlock;
+        if (i < a.V) {
+            float v = lv[j];
+            if (st.penalty != 1.0f && a.seen && ((a.seen[i >> 5] >> (i & 31)) & 1u))
+                v = v > 0.0f ? __fdiv_rn(v, st.penalty) : __fmul_rn(v, st.penalty);
+            v = __fdiv_rn(v, st.temperature);
+            a.scratch[i] = v;
+            mx = fmaxf(mx, v);
+        }
+    }
+    const float m = wg_reduce(mx, true, red4);
+    if (threadIdx.x == 0) a.scratch[2 * (size_t)a.V + blockIdx.x] = m;
+}
+
+// pass 2 (no top-k): pr = exp(s - M) and the workgroup sum
+__global__ __launch_bounds__(kBlock) void sample_exp_kernel(const SampleArgs a) {
+    __shared__ float red4[4];
+    const DevState st = *a.st;
+    if (st.top_k > 0 && st.top_k < a.V) return;  // top-k: the candidates come first
+    const int nparts = (a.V + kGenWide - 1) / kGenWide;
+    const float M = parts_max(a.scratch + 2 * (size_t)a.V, nparts, red4);
+    const int base = blockIdx.x * kGenWide + threadIdx.x;
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kGenWide / kBlock; j++) {
+        const int i = base + j * kBlock;
+        if (i < a.V) {
+            const float e = expf(a.scratch[i] - M);
+            a.scratch[a.V + i] = e;
+            sum += e;
+        }
+    }
+    const float S = wg_reduce(sum, false, red4);
+    if (threadIdx.x == 0) a.scratch[2 * (size_t)a.V + kGenParts + blockIdx.x] = S;
+}
+
+// pass 3 (no top-k): pr = pr / S, S the partial sums added in order
+__global__ __launch_bounds__(kBlock) void sample_norm_kernel(const SampleArgs a) {
+    __shared__ float Ssh;
+    const DevState st = *a.st;
+    if (st.top_k > 0 && st.top_k < a.V) return;
+    const int nparts = (a.V + kGenWide - 1) / kGenWide;
+    if (threadIdx.x == 0) {
+        const float *ps = a.scratch + 2 * (size_t)a.V + kGenParts;
+        float S = 0.0f;
+        for (int i = 0; i < nparts; i++) S += ps[i];
+        Ssh = S;
+    }
+    __syncthreads();
+    const float S = Ssh;
+    const int base = blockIdx.x * kGenWide + threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < kGenWide / kBlock; j++) {
+        const int i = base + j * kBlock;
+        if (i < a.V) a.scratch[a.V + i] = a.scratch[a.V + i] / S;
+    }
+}
+
 __global__ __launch_bounds__(kGenThreads) void sample_general_kernel(const SampleArgs a) {
     __shared__ GenShared sh;
     const DevState st = *a.st;
     const GenLayout L(a.V);
     const int V = a.V, t = threadIdx.x;
     float *sc = a.scratch, *pr = a.scratch + V;
-    // scaled logits (penalty, temperature) and their maximum
-    float mx = -INFINITY;
-    for (int i0 = L.base; i0 < L.end; i0 += 64 * kGenUnroll) {
-        float lv[kGenUnroll];
-#pragma unroll
-        for (int u = 0; u < kGenUnroll; u++) {
-            const int i = i0 + 64 * u;
-            lv[u] = i < L.end ? a.logits[i] : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < kGenUnroll; u++) {
-            const int i = i0 + 64 * u;
-            if (i >= L.end) break;
-            float v = lv[u];
-            if (st.penalty != 1.0f && a.seen && ((a.seen[i >> 5] >> (i & 31)) & 1u))
-                v = v > 0.0f ? __fdiv_rn(v, st.penalty) : __fmul_rn(v, st.penalty);
-            v = __fdiv_rn(v, st.temperature);
-            sc[i] = v;
-            mx = fmaxf(mx, v);
-        }
-    }
-    const float M = block_max_f(mx, sh);
+    // sc holds the scaled logits (sample_scale_kernel); without top-k pr
+    // already holds the probabilities (sample_exp_kernel, sample_norm_kernel)
+    // and the draw is sample_walk_kernel's, so only a nucleus cut is left
+    if (!(st.top_k > 0 && st.top_k < V) && !(st.top_p < 1.0f)) return;
+
     // The orders below are (key descending, id ascending) with the scaled
     // logit as key for top-k and the walk after it -- the reference's sort --
     // and the probability for the nucleus, whose sort leaves ties
@@ -650,17 +732,24 @@ __global__ __launch_bounds__(kGenThreads) void sample_general_kernel(const Sampl
         if (kid < 0) kid = V;  // unreachable: the count always exceeds k - 1
         kk = kid < V ? cut_key(sc, kid) : 0u;
     }
-    // softmax over the candidates: pr = exp(s - M) (0 for non-candidates),
-    // S their sum, then pr = pr / S, the reference's probabilities
-    float sum = 0.0f;
-    gen_each(L, sc, nullptr, [&](int i, float s, float) {
-        const uint32_t k = f32_order(s);
-        const float e = (!use_k || k > kk || (k == kk && i <= kid)) ? expf(s - M) : 0.0f;
-        pr[i] = e;
-        sum += e;
-    });
-    const float S = block_sum_f(sum, sh);
-    gen_each(L, pr, nullptr, [&](int i, float e, float) { pr[i] = e / S; });
+    if (use_k) {
+        // softmax over the candidates: pr = exp(s - M) (0 for the others), S
+        // their sum, then pr = pr / S, the reference's probabilities; M is
+        // the overall maximum (the best id is always a candidate)
+        float m = -INFINITY;
+        const int nparts = (V + kGenWide - 1) / kGenWide;
+        for (int i = t; i < nparts; i += kGenThreads) m = fmaxf(m, sc[2 * (size_t)V + i]);
+        const float M = block_max_f(m, sh);
+        float sum = 0.0f;
+        gen_each(L, sc, nullptr, [&](int i, float s, float) {
+            const uint32_t k = f32_order(s);
+            const float e = (k > kk || (k == kk && i <= kid)) ? expf(s - M) : 0.0f;
+            pr[i] = e;
+            sum += e;
+        });
+        const float S = block_sum_f(sum, sh);
+        gen_each(L, pr, nullptr, [&](int i, float e, float) { pr[i] = e / S; });
+    }
     // nucleus: keep through the first cumulative probability above top_p (in
     // probability order), then divide the kept probabilities by their sum
     if (st.top_p < 1.0f) {
@@ -682,29 +771,26 @@ __global__ __launch_bounds__(kGenThreads) void sample_general_kernel(const Sampl
             });
         }
     }
-    // the draw: inverse-CDF walk, in descending scaled-logit order with top-k
-    // (the candidates are the sorted ids), else in id order
+    // without top-k the draw walks the ids in order: sample_walk_kernel
+    if (!use_k) return;
+    // the draw: inverse-CDF walk in descending scaled-logit order (the
+    // top-k candidates are the sorted ids)
     const float r = step_draw(a, st.step);
-    int pick;
-    if (use_k)
-        pick = desc_threshold(
-            L, sc, pr,
-            [&](int, float s, float p, uint32_t &k, unsigned long long &w) {
-                k = f32_order(s);
-                w = fx(p);
-                return true;
-            },
-            fx(r), sh);
-    else
-        pick = id_threshold(L, pr, nullptr, [&](int, float p, float) { return fx(p); }, fx(r), sh);
+    int pick = desc_threshold(
+        L, sc, pr,
+        [&](int, float s, float p, uint32_t &k, unsigned long long &w) {
+            k = f32_order(s);
+            w = fx(p);
+            return true;
+        },
+        fx(r), sh);
     if (pick < 0) {
-        // past the last cumulative sum (rounding): the first id with p > 0 in
-        // walk order -- the best key with top-k, else the lowest id
+        // past the last cumulative sum (rounding): the first candidate with
+        // p > 0 in walk order, i.e. the best key
         unsigned long long best = ~0ull;
         gen_each(L, sc, pr, [&](int i, float s, float p) {
             if (!(p > 0.0f)) return;
-            const unsigned long long k =
-                use_k ? (((unsigned long long)~f32_order(s) << 32) | (uint32_t)i) : (unsigned long long)i;
+            const unsigned long long k = ((unsigned long long)~f32_order(s) << 32) | (uint32_t)i;
             best = k < best ? k : best;
         });
         if (t == 0) sh.res[2] = ~0ull;
@@ -713,6 +799,106 @@ __global__ __launch_bounds__(kGenThreads) void sample_general_kernel(const Sampl
         __syncthreads();
         const unsigned long long k = sh.res[2];
         pick = k == ~0ull ? 0 : (int)(uint32_t)k;
+    }
+    if (t == 0) emit_token(a, pick);
+}
+
+// Without top-k: the inverse-CDF walk in id order (src/tensor.rs:1203-1212)
+// over the probabilities in pr (after any nucleus cut), in 2^-40 fixed
+// point.  Pass 1, one workgroup per 2048 ids: the chunk's mass.
+__global__ __launch_bounds__(kBlock) void sample_walk_sums_kernel(const SampleArgs a) {
+    __shared__ unsigned long long red4[4];
+    const DevState st = *a.st;
+    if (st.top_k > 0 && st.top_k < a.V) return;
+    const int base = blockIdx.x * kGenWide + threadIdx.x;
+    unsigned long long m = 0;
+#pragma unroll
+    for (int j = 0; j < kGenWide / kBlock; j++) {
+        const int i = base + j * kBlock;
+        if (i < a.V) m += fx(a.scratch[a.V + i]);
+    }
+    m = wave_sum_u64(m);
+    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0)
+        reinterpret_cast<unsigned long long *>(a.scratch + 2 * (size_t)a.V + 2 * kGenParts)[blockIdx.x] =
+            (red4[0] + red4[1]) + (red4[2] + red4[3]);
+}
+
+// Pass 2, one workgroup: the chunk where the running mass first exceeds the
+// draw (a prefix over the chunk masses), then the id inside it (thread t
+// holds ids 8t .. 8t+7 of the chunk, so thread order is id order).
+__global__ __launch_bounds__(kBlock) void sample_walk_kernel(const SampleArgs a) {
+    __shared__ unsigned long long wt[4];
+    __shared__ unsigned long long pick_sh;
+    const DevState st = *a.st;
+    if (st.top_k > 0 && st.top_k < a.V) return;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const float *pr = a.scratch + a.V;
+    const unsigned long long *parts =
+        reinterpret_cast<const unsigned long long *>(a.scratch + 2 * (size_t)a.V + 2 * kGenParts);
+    const int nparts = (a.V + kGenWide - 1) / kGenWide;  // <= kGenParts <= kBlock
+    const unsigned long long rf = fx(step_draw(a, st.step));
+    auto block_excl = [&](unsigned long long v, unsigned long long *tot) {
+        const unsigned long long incl = wave_incl_u64(v);
+        __syncthreads();
+        if (lane == 63) wt[w] = incl;
+        __syncthreads();
+        unsigned long long before = 0;
+        for (int i = 0; i < w; i++) before += wt[i];
+        *tot = (wt[0] + wt[1]) + (wt[2] + wt[3]);
+        return before + incl - v;
+    };
+    if (t == 0) pick_sh = ~0ull;
+    const unsigned long long c = t < nparts ? parts[t] : 0ull;
+    unsigned long long tot;
+    const unsigned long long cum = block_excl(c, &tot);
+    __syncthreads();
+    if (t < nparts && cum <= rf && cum + c > rf) pick_sh = ((unsigned long long)t << 48) | cum;
+    __syncthreads();
+    const unsigned long long hit = pick_sh;
+    __syncthreads();
+    int pick = -1;
+    if (hit != ~0ull) {
+        const int g = (int)(hit >> 48);
+        const unsigned long long left = rf - (hit & ((1ull << 48) - 1));
+        const int i0 = g * kGenWide + 8 * t;
+        unsigned long long q[8], m = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            q[k] = i0 + k < a.V ? fx(pr[i0 + k]) : 0ull;
+            m += q[k];
+        }
+        unsigned long long t2;
+        unsigned long long cu = block_excl(m, &t2);
+        if (t == 0) pick_sh = ~0ull;
+        __syncthreads();
+        if (cu <= left && cu + m > left) {
+            for (int k = 0; k < 8; k++) {
+                cu += q[k];
+                if (cu > left) {
+                    pick_sh = (unsigned long long)(i0 + k);
+                    break;
+                }
+            }
+        }
+        __syncthreads();
+        pick = pick_sh == ~0ull ? -1 : (int)pick_sh;
+    }
+    if (pick < 0) {
+        // past the last cumulative sum (rounding): the lowest id with p > 0
+        unsigned long long best = ~0ull;
+        for (int i = t; i < a.V; i += kBlock)
+            if (pr[i] > 0.0f) {
+                best = (unsigned long long)i;
+                break;
+            }
+        __syncthreads();
+        if (t == 0) pick_sh = ~0ull;
+        __syncthreads();
+        atomicMin(&pick_sh, best);
+        __syncthreads();
+        pick = pick_sh == ~0ull ? 0 : (int)pick_sh;
     }
     if (t == 0) emit_token(a, pick);
 }
@@ -732,7 +918,13 @@ hipError_t launch_sample(const SampleArgs &a, hipStream_t s) {
         return hipGetLastError();
     }
     if (!a.scratch) return hipErrorInvalidValue;
+    const dim3 wide((a.V + kGenWide - 1) / kGenWide);
+    hipLaunchKernelGGL(sample_scale_kernel, wide, dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(sample_exp_kernel, wide, dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(sample_norm_kernel, wide, dim3(kBlock), 0, s, a);
     hipLaunchKernelGGL(sample_general_kernel, dim3(1), dim3(kGenThreads), 0, s, a);
+    hipLaunchKernelGGL(sample_walk_sums_kernel, wide, dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(sample_walk_kernel, dim3(1), dim3(kBlock), 0, s, a);
     return hipGetLastError();
 }
 
