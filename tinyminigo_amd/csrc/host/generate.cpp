@@ -88,6 +88,8 @@ extern "C" int tmg_generate(tmg_model *m, const uint32_t *prompt, size_t n_promp
     st.top_p = p->top_p;
     st.penalty = p->repetition_penalty;
     TMG_HIPG(hipMemcpy(c->st, &st, sizeof(st), hipMemcpyHostToDevice));
+    c->samp_use_k = use_k;
+    c->samp_use_p = p->top_p < 1.0f;
     if (!greedy && p->max_tokens > 0) {
         // the reference's StdRng::seed_from_u64(seed) stream: one
         // StandardUniform f32 per sampled step (src/model.rs:629,

@@ -502,6 +502,8 @@ int enqueue_select(tmg_model *m, tmg_cache *c, int mode, int advance_pos) {
     sa.seen_rw = c->seen;
     sa.cand = mode == SEL_FULL ? nullptr : c->cand;
     sa.scratch = c->gsc;
+    sa.use_k = c->samp_use_k;
+    sa.use_p = c->samp_use_p;
     sa.draws = c->draws;
     sa.n_draws = (int)c->max_pos + 2;
     sa.history = c->history;
@@ -984,14 +986,15 @@ extern "C" int tmg_cache_new(tmg_model *m, uint32_t max_pos, tmg_cache **out) {
     void *seen = nullptr, *cand = nullptr, *gsc = nullptr, *draws = nullptr;
     if (!rc && (hipMalloc(&seen, seen_words * 4) != hipSuccess ||
                 hipMalloc(&cand, nslices * kSampleMaxK * 8) != hipSuccess ||
-                hipMalloc(&gsc, (size_t)m->V * 8 + 4 * 128 * 4) != hipSuccess ||
+                hipMalloc(&gsc, kSampleScratchBytes(m->V)) != hipSuccess ||
                 hipMalloc(&draws, ((size_t)max_pos + 2) * 4) != hipSuccess))
         rc = set_error(TMG_E_NOMEM, "sampler buffer allocation failed");
     c->seen = (unsigned *)seen;
     c->cand = (unsigned long long *)cand;
     c->gsc = (float *)gsc;
     c->draws = (float *)draws;
-    if (!rc && hipMemset(c->draws, 0, ((size_t)max_pos + 2) * 4) != hipSuccess)
+    if (!rc && (hipMemset(c->draws, 0, ((size_t)max_pos + 2) * 4) != hipSuccess ||
+                hipMemset(c->gsc, 0, kSampleScratchBytes(m->V)) != hipSuccess))
         rc = set_error(TMG_E_DEVICE, "hipMemset failed");
     if (!rc && hipMemset(c->seen, 0, seen_words * 4) != hipSuccess) rc = set_error(TMG_E_DEVICE, "hipMemset failed");
     if (!rc) {

@@ -85,7 +85,8 @@ struct tmg_cache {
     unsigned *seen = nullptr;          // bitmap of generated ids (repetition penalty)
     unsigned long long *cand = nullptr;  // sampler candidates
     float *draws = nullptr;              // [max_pos + 2] uniform draw per step (sampling)
-    float *gsc = nullptr;                // [2V + 512] scratch of the whole-vocabulary sampler
+    float *gsc = nullptr;                // kSampleScratchBytes(V) of the whole-vocabulary sampler
+    int samp_use_k = 0, samp_use_p = 0;  // the running generate call's top-k / nucleus
     tmg::GridBar *bar = nullptr;       // persistent-kernel barrier counters
     tmg::PersistPlan *plan = nullptr;  // persistent-kernel argument blocks
     bool persist_broken = false;       // a barrier timed out: use the graph path

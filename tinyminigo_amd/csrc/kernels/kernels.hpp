@@ -294,6 +294,8 @@ constexpr int kSampleSlice = 2048;
 constexpr int kSampleSelectKeys = 8192;
 // Largest vocabulary either sampling path takes.
 constexpr int kSampleMaxVocab = 262144;
+// Scratch bytes of the whole-vocabulary sampler for a vocabulary of V ids.
+constexpr size_t kSampleScratchBytes(size_t V) { return V * 8 + 40960; }
 
 struct SampleArgs {
     float *logits;  // [V]; penalized in place like the reference
@@ -306,10 +308,13 @@ struct SampleArgs {
     int hist_cap;
     int greedy;       // temperature <= 0: argmax of the penalized logits
     int advance_pos;  // 1 after a decode step, 0 after prefill
-    // whole-vocabulary path (cand null, not greedy): [2V + 512] floats
-    // (scaled logits, probabilities, 128 partial maxima, 128 partial sums,
-    // 128 u64 partial masses)
+    // whole-vocabulary path (cand null, not greedy): kSampleScratchBytes(V)
+    // of zero-initialized device memory (scaled logits, probabilities,
+    // partials, a 4096-bin histogram, search states), and whether the
+    // running generate call uses top-k (top_k > kSampleMaxK here) and a
+    // nucleus cut
     float *scratch;
+    int use_k, use_p;
     // uniform draw of each step (the reference's StdRng stream), indexed by
     // st->step; steps at or past n_draws use 0
     const float *draws;

@@ -12,9 +12,9 @@
 //   lane runs the reference's sequential tail over the k candidates in
 //   order: softmax (max, exp, sequential sum, divide), nucleus cut at the
 //   first cumulative sum > top_p, renormalization, and the inverse-CDF walk.
-// Whole-vocabulary path (no top-k, or top_k > kSampleMaxK): one workgroup
-// replaces each of the reference's sorts with a threshold search over the
-// whole vocabulary (sample_general_kernel below).
+// Whole-vocabulary path (no top-k, or top_k > kSampleMaxK): each of the
+// reference's sorts becomes a threshold search over the whole vocabulary,
+// run as wide histogram launches (search_hist_kernel and the others below).
 //
 // Keys order by value descending, then id ascending, which is the reference
 // argmax tie rule; the reference's sort_unstable_by leaves equal-value order
@@ -312,71 +312,66 @@ __global__ __launch_bounds__(kSelectThreads) void sample_select_kernel(const Sam
 
 // ---------------------------------------------------------------------------
 // Whole-vocabulary path: no top-k (with or without a nucleus cut), or top_k
-// above kSampleMaxK.  One workgroup of kGenThreads.  Wave w owns the ids
-// [w*wsz, (w+1)*wsz) (wsz a multiple of 256), lane l of it the ids
-// w*wsz + 64*j + l, so every pass is coalesced; rows of 256 ids are the
-// units of the id-order searches.  a.scratch holds the scaled logits [V]
-// and the probabilities [V]; three wide kernels before it compute them (the
-// probabilities only without top-k).  The orders the reference gets by
-// sorting are found by threshold searches instead: among the selected ids,
-// in a given order, the first at which a running total of weights exceeds
-// a target.  Weight 1 in (scaled logit descending, id ascending) order gives
-// the k-th largest logit; the probability as weight gives the nucleus cut
-// (first cumulative sum > top_p) and the inverse-CDF walk.  Probability
-// masses are summed in 2^-40 fixed point, so every sum is exact and
-// independent of summation order.
+// above kSampleMaxK.  Every pass is a launch over many workgroups; only the
+// bin and chunk selections run in one workgroup.
+//
+// The orders the reference gets by sorting are found by threshold searches:
+// among the selected ids, in (key descending, id ascending) order, the first
+// at which a running total of weights exceeds a target.
+//   SK_COUNT   key = scaled logit, weight 1, target k - 1: the k-th best
+//              logit (the reference's top-k sort);
+//   SK_NUCLEUS key = probability, weight = probability, target top_p: the
+//              nucleus cut (the reference sorts by probability, ties
+//              unspecified); the kept mass is the running total at the cut;
+//   SK_WALK    key = scaled logit, weight = probability, target = the draw:
+//              the inverse-CDF walk over the sorted top-k candidates.
+// A search is a radix search over the 32-bit key (12, 12, then 8 bits): per
+// level a histogram launch (LDS bins, then global bins) and a pick launch
+// (the bin where the running total crosses what is left of the target);
+// ties at the final key go in id order (chunk masses, then one chunk
+// scanned).  Without top-k the draw walks the ids in order (chunk masses,
+// then one chunk).  Probability masses are summed in 2^-40 fixed point, so
+// every sum is exact and independent of order.
 // ---------------------------------------------------------------------------
 
-constexpr int kGenThreads = 1024;
-constexpr int kGenWaves = kGenThreads / 64;
-constexpr int kGenRow = 256;       // ids per row of an id-order search
-constexpr int kGenMaxRows = 64;    // rows per wave: one per lane
-constexpr int kGenBins = 4096;     // 12-bit digits: key bits 31..20, 19..8, then 7..0
+constexpr int kGenWide = 2048;  // ids per workgroup of the elementwise passes
+constexpr int kGenParts = kSampleMaxVocab / kGenWide;
+constexpr int kHistIds = 4096;  // ids per workgroup of a histogram pass
+constexpr int kGenBins = 4096;
+constexpr int kPickThreads = 1024;
 constexpr double kFx = 1099511627776.0;  // 2^40
-static_assert(kGenWaves * kGenMaxRows * kGenRow >= kSampleMaxVocab, "rows must cover the vocabulary");
+static_assert(kGenParts == 128 && kGenParts <= kBlock, "scratch layout: 128 partials of each kind");
+static_assert(kGenBins == 4 * kPickThreads, "the pick takes four bins per thread");
 
-struct GenShared {
-    union {
-        unsigned long long bins[kGenBins];                 // key histogram
-        unsigned long long rowt[kGenWaves][kGenMaxRows];   // row totals
-    };
-    unsigned long long wtot[kGenWaves];
-    unsigned long long res[4];
-    float fred[kGenWaves];
+enum SearchKind { SK_COUNT = 0, SK_NUCLEUS = 1, SK_WALK = 2 };
+constexpr int kSearchRunning = -2;  // SearchState::id while levels remain
+
+struct SearchState {
+    unsigned long long rest;     // target left after the heavier keys
+    unsigned long long through;  // running total through the found id
+    uint32_t pfx;                // key bits decided (the whole key after the last level)
+    int id;                      // the found id; -1: the total does not exceed the target
+    int pad[2];
 };
 
-// Which ids this thread owns: i = base + 64*j, i < end.
-struct GenLayout {
-    int V, wsz, nrow, base, end;
-    __device__ explicit GenLayout(int v) : V(v) {
-        nrow = (V + kGenWaves * kGenRow - 1) / (kGenWaves * kGenRow);
-        wsz = nrow * kGenRow;
-        const int w = (int)(threadIdx.x >> 6);
-        base = w * wsz + (int)(threadIdx.x & 63);
-        end = min(V, (w + 1) * wsz);
-    }
+// a.scratch: sc [V] | pr [V] | max partials [128] | sum partials [128] |
+// u64 mass partials [128] | u64 histogram [4096] | SearchState [3]
+struct GenBufs {
+    float *sc, *pr, *pmax, *psum;
+    unsigned long long *pmass, *hist;
+    SearchState *ss;
 };
 
-// f(i, s, p) over this thread's ids, with s = sc[i] and p = pr[i] (0 when
-// pr is null) loaded kGenUnroll ids at a time, so one memory round trip
-// covers 16 ids per lane.
-constexpr int kGenUnroll = 16;
-template <class F>
-__device__ __forceinline__ void gen_each(const GenLayout &L, const float *sc, const float *pr, F f) {
-    for (int i0 = L.base; i0 < L.end; i0 += 64 * kGenUnroll) {
-        float sv[kGenUnroll], pv[kGenUnroll];
-#pragma unroll
-        for (int u = 0; u < kGenUnroll; u++) {
-            const int i = i0 + 64 * u;
-            sv[u] = i < L.end ? sc[i] : 0.0f;
-            pv[u] = pr && i < L.end ? pr[i] : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < kGenUnroll; u++) {
-            const int i = i0 + 64 * u;
-            if (i < L.end) f(i, sv[u], pv[u]);
-        }
-    }
+__device__ __forceinline__ GenBufs gen_bufs(const SampleArgs &a) {
+    GenBufs b;
+    b.sc = a.scratch;
+    b.pr = a.scratch + a.V;
+    b.pmax = a.scratch + 2 * (size_t)a.V;
+    b.psum = b.pmax + kGenParts;
+    b.pmass = reinterpret_cast<unsigned long long *>(b.psum + kGenParts);
+    b.hist = b.pmass + kGenParts;
+    b.ss = reinterpret_cast<SearchState *>(b.hist + kGenBins);
+    return b;
 }
 
 // floor(p * 2^40) for 0 <= p < 2 (exact: p's 24-bit significand shifted by
@@ -406,204 +401,24 @@ __device__ __forceinline__ unsigned long long wave_incl_u64(unsigned long long v
     return v;
 }
 
-// Exclusive prefix over the workgroup's threads in thread order; *total gets
-// the sum.  Begins and ends with a barrier.
-__device__ unsigned long long block_excl_u64(unsigned long long v, GenShared &sh, unsigned long long *total) {
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+// Exclusive prefix over the workgroup's threads in thread order (NW
+// wavefronts); *total gets the sum.  wt holds NW values of LDS.
+template <int NW>
+__device__ unsigned long long block_excl_u64(unsigned long long v, unsigned long long *wt, unsigned long long *total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const unsigned long long incl = wave_incl_u64(v);
     __syncthreads();
-    if (lane == 63) sh.wtot[w] = incl;
+    if (lane == 63) wt[w] = incl;
     __syncthreads();
     unsigned long long before = 0, all = 0;
-    for (int i = 0; i < kGenWaves; i++) {
-        if (i < w) before += sh.wtot[i];
-        all += sh.wtot[i];
+#pragma unroll
+    for (int i = 0; i < NW; i++) {
+        if (i < w) before += wt[i];
+        all += wt[i];
     }
-    __syncthreads();
     *total = all;
     return before + incl - v;
 }
-
-__device__ float block_max_f(float v, GenShared &sh) {
-    v = wave_max(v);
-    if ((threadIdx.x & 63) == 0) sh.fred[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float m = -INFINITY;
-    for (int i = 0; i < kGenWaves; i++) m = fmaxf(m, sh.fred[i]);
-    __syncthreads();
-    return m;
-}
-
-__device__ float block_sum_f(float v, GenShared &sh) {
-    v = wave_sum(v);
-    if ((threadIdx.x & 63) == 0) sh.fred[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float m = 0.0f;
-    for (int i = 0; i < kGenWaves; i++) m += sh.fred[i];
-    __syncthreads();
-    return m;
-}
-
-// A value one thread found (or ~0 if none did), broadcast to all.
-__device__ unsigned long long block_pick(bool mine, unsigned long long v, GenShared &sh) {
-    if (threadIdx.x == 0) sh.res[2] = ~0ull;
-    __syncthreads();
-    if (mine) sh.res[2] = v;
-    __syncthreads();
-    const unsigned long long r = sh.res[2];
-    __syncthreads();
-    return r;
-}
-
-// Threshold search in id order: the first id whose running total of
-// wf(i, s, p) (the weight of id i with s = sc[i], p = pr[i]; 0 when not
-// selected) exceeds `rest`, or -1 when the total does not; *through gets the
-// running total through that id.  Row totals (row
-// r of wave w = its ids w*wsz + 256 r .. +255, i.e. lane l's ids for j =
-// 4r .. 4r+3; thread w*64 + r then holds row r, so thread order is id
-// order), a prefix scan over them, then one wavefront scans the 256 ids of
-// the crossing row.
-template <class Wf>
-__device__ int id_threshold(const GenLayout &L, const float *sc, const float *pr, Wf wf, unsigned long long rest,
-                            GenShared &sh, unsigned long long *through = nullptr) {
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    constexpr int RB = kGenUnroll / 4;  // rows per batch
-    for (int r0 = 0; r0 < L.nrow; r0 += RB) {
-        float sv[kGenUnroll], pv[kGenUnroll];
-#pragma unroll
-        for (int u = 0; u < kGenUnroll; u++) {
-            const int i = L.base + (r0 * 4 + u) * 64;
-            sv[u] = i < L.end ? sc[i] : 0.0f;
-            pv[u] = pr && i < L.end ? pr[i] : 0.0f;
-        }
-#pragma unroll
-        for (int q = 0; q < RB; q++) {
-            unsigned long long v = 0;
-#pragma unroll
-            for (int u = 4 * q; u < 4 * q + 4; u++) {
-                const int i = L.base + (r0 * 4 + u) * 64;
-                if (i < L.end) v += wf(i, sv[u], pv[u]);
-            }
-            v = wave_sum_u64(v);
-            if (lane == 0 && r0 + q < L.nrow) sh.rowt[w][r0 + q] = v;
-        }
-    }
-    __syncthreads();
-    const unsigned long long c = lane < L.nrow ? sh.rowt[w][lane] : 0ull;
-    unsigned long long tot;
-    const unsigned long long cum = block_excl_u64(c, sh, &tot);
-    if (tot <= rest) return -1;
-    const unsigned long long hit =
-        block_pick(lane < L.nrow && cum <= rest && cum + c > rest, ((unsigned long long)t << 48) | cum, sh);
-    const int row = (int)(hit >> 48);
-    const unsigned long long left = rest - (hit & ((1ull << 48) - 1));
-    const int first = (row >> 6) * L.wsz + (row & 63) * kGenRow;  // lane l: ids first + 4l .. first + 4l + 3
-    if (t == 0) sh.res[2] = ~0ull;
-    __syncthreads();
-    if (w == 0) {
-        unsigned long long q[4], m = 0;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int i = first + 4 * lane + k;
-            q[k] = i < L.V ? wf(i, sc[i], pr ? pr[i] : 0.0f) : 0ull;
-            m += q[k];
-        }
-        const unsigned long long incl = wave_incl_u64(m);
-        unsigned long long cu = incl - m;
-        if (cu <= left && incl > left) {
-            for (int k = 0; k < 4; k++) {
-                cu += q[k];
-                if (cu > left) {
-                    sh.res[2] = (unsigned long long)(first + 4 * lane + k);
-                    sh.res[3] = rest - left + cu;  // running total through this id
-                    break;
-                }
-            }
-        }
-    }
-    __syncthreads();
-    const unsigned long long r = sh.res[2];
-    if (through) *through = sh.res[3];
-    __syncthreads();
-    return r == ~0ull ? -1 : (int)r;
-}
-
-// Threshold search in (key descending, id ascending) order.  kw(i, s, p, k,
-// w) says whether id i (scaled logit s, pr value p) is selected and sets its
-// key k (uint32, larger first) and weight w.  A radix search over the key
-// (12, 12, then 8 bits) finds the key at which the running total crosses
-// `target`; ties at that key go in id order.  Returns the id, or -1 when the
-// total of all selected ids does not exceed the target; *through gets the
-// running total through the returned id.  Ids of weight 0 can never be the
-// answer and are skipped.
-template <class Kw>
-__device__ int desc_threshold(const GenLayout &L, const float *sc, const float *pr, Kw kw,
-                              unsigned long long target, GenShared &sh, unsigned long long *through = nullptr) {
-    const int t = threadIdx.x;
-    uint32_t pfx = 0;                  // key bits decided so far
-    unsigned long long rest = target;  // target left after the heavier bins
-    for (int lv = 0; lv < 3; lv++) {
-        const int shift = lv == 0 ? 20 : lv == 1 ? 8 : 0;
-        const uint32_t nb = lv == 2 ? 256u : 4096u;
-        const int above = lv == 0 ? 32 : lv == 1 ? 20 : 8;  // pfx holds key >> above
-        for (int i = t; i < kGenBins; i += kGenThreads) sh.bins[i] = 0;
-        __syncthreads();
-        gen_each(L, sc, pr, [&](int i, float s, float p) {
-            uint32_t k;
-            unsigned long long v;
-            if (!kw(i, s, p, k, v) || !v) return;
-            if (lv > 0 && (k >> above) != pfx) return;
-            atomicAdd(&sh.bins[(k >> shift) & (nb - 1)], v);
-        });
-        __syncthreads();
-        // thread t takes 4 bins from the top: nb-1-4t .. nb-4-4t
-        unsigned long long c[4], mine = 0;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int bin = (int)nb - 1 - 4 * t - j;
-            c[j] = bin >= 0 ? sh.bins[bin] : 0ull;
-            mine += c[j];
-        }
-        unsigned long long total;
-        unsigned long long cum = block_excl_u64(mine, sh, &total);
-        if (total <= rest) return -1;  // only possible at level 0
-        int hit = -1;
-        unsigned long long before = 0;
-        if (cum <= rest && cum + mine > rest) {
-            for (int j = 0; j < 4; j++) {
-                if (cum + c[j] > rest) {
-                    hit = (int)nb - 1 - 4 * t - j;
-                    before = cum;
-                    break;
-                }
-                cum += c[j];
-            }
-        }
-        // the bin (12 bits) and the weight before it (< 2^52 for V <= 2^18)
-        const unsigned long long r = block_pick(hit >= 0, ((unsigned long long)hit << 52) | before, sh);
-        pfx = (pfx << (lv == 2 ? 8 : 12)) | (uint32_t)(r >> 52);
-        rest -= r & ((1ull << 52) - 1);
-    }
-    const int id = id_threshold(
-        L, sc, pr,
-        [&](int i, float s, float p) {
-            uint32_t k;
-            unsigned long long v;
-            return kw(i, s, p, k, v) && k == pfx ? v : 0ull;
-        },
-        rest, sh, through);
-    // the ties' running total starts after the heavier keys' target - rest
-    if (id >= 0 && through) *through += target - rest;
-    return id;
-}
-
-// The elementwise front of the whole-vocabulary path, over many workgroups:
-// each workgroup of 256 threads takes 2048 ids (thread t: ids g*2048 +
-// 256 j + t).  a.scratch: sc [V] | pr [V] | part [kGenParts] maxima |
-// part [kGenParts] sums | u64 part [kGenParts] walk masses.
-constexpr int kGenWide = 2048;
-constexpr int kGenParts = kSampleMaxVocab / kGenWide;
-static_assert(kGenParts == 128 && kGenParts <= kBlock, "the scratch layout reserves 128 partials of each kind");
 
 __device__ __forceinline__ float wg_reduce(float v, bool is_max, float *red4) {
     v = is_max ? wave_max(v) : wave_sum(v);
@@ -612,14 +427,27 @@ __device__ __forceinline__ float wg_reduce(float v, bool is_max, float *red4) {
     return is_max ? fmaxf(fmaxf(red4[0], red4[1]), fmaxf(red4[2], red4[3])) : (red4[0] + red4[1]) + (red4[2] + red4[3]);
 }
 
-// The maximum of the first n partials (every workgroup reads the same
-// values in the same order, so all get the same result).
-__device__ __forceinline__ float parts_max(const float *part, int n, float *red4) {
-    float m = -INFINITY;
-    for (int i = threadIdx.x; i < n; i += kBlock) m = fmaxf(m, part[i]);
-    const float r = wg_reduce(m, true, red4);
-    __syncthreads();
-    return r;
+__device__ __forceinline__ bool use_topk(const DevState &st, int V) { return st.top_k > 0 && st.top_k < V; }
+
+// Key and weight of id i for a search; false when the weight is 0 (such an
+// id can never be where the running total crosses the target).
+__device__ __forceinline__ bool kind_kw(int kind, float s, float p, uint32_t &k, unsigned long long &w) {
+    if (kind == SK_COUNT) {
+        k = f32_order(s);
+        w = 1;
+    } else if (kind == SK_NUCLEUS) {
+        k = f32_order(p);
+        w = fx(p);
+    } else {
+        k = f32_order(s);
+        w = fx(p);
+    }
+    return w != 0;
+}
+
+__device__ __forceinline__ unsigned long long kind_target(int kind, const SampleArgs &a, const DevState &st) {
+    return kind == SK_COUNT ? (unsigned long long)(st.top_k - 1)
+                            : kind == SK_NUCLEUS ? fx(st.top_p) : fx(step_draw(a, st.step));
 }
 
 // pass 1: scaled logits (penalty, temperature; src/tensor.rs:1142-1154,
@@ -627,6 +455,7 @@ __device__ __forceinline__ float parts_max(const float *part, int n, float *red4
 __global__ __launch_bounds__(kBlock) void sample_scale_kernel(const SampleArgs a) {
     __shared__ float red4[4];
     const DevState st = *a.st;
+    const GenBufs b = gen_bufs(a);
     const int base = blockIdx.x * kGenWide + threadIdx.x;
     float lv[kGenWide / kBlock];
 #pragma unroll
@@ -643,46 +472,58 @@ __global__ __launch_bounds__(kBlock) void sample_scale_kernel(const SampleArgs a
             if (st.penalty != 1.0f && a.seen && ((a.seen[i >> 5] >> (i & 31)) & 1u))
                 v = v > 0.0f ? __fdiv_rn(v, st.penalty) : __fmul_rn(v, st.penalty);
             v = __fdiv_rn(v, st.temperature);
-            a.scratch[i] = v;
+            b.sc[i] = v;
             mx = fmaxf(mx, v);
         }
     }
     const float m = wg_reduce(mx, true, red4);
-    if (threadIdx.x == 0) a.scratch[2 * (size_t)a.V + blockIdx.x] = m;
+    if (threadIdx.x == 0) b.pmax[blockIdx.x] = m;
 }
 
-// pass 2 (no top-k): pr = exp(s - M) and the workgroup sum
+// pass 2: softmax numerators over the candidates (src/tensor.rs:1177-1179):
+// pr = exp(s - M) for candidates (all ids, or the top-k found by SK_COUNT),
+// 0 for the others; M the overall maximum (always a candidate); workgroup sum
 __global__ __launch_bounds__(kBlock) void sample_exp_kernel(const SampleArgs a) {
     __shared__ float red4[4];
     const DevState st = *a.st;
-    if (st.top_k > 0 && st.top_k < a.V) return;  // top-k: the candidates come first
+    const GenBufs b = gen_bufs(a);
     const int nparts = (a.V + kGenWide - 1) / kGenWide;
-    const float M = parts_max(a.scratch + 2 * (size_t)a.V, nparts, red4);
+    float m = -INFINITY;
+    for (int i = threadIdx.x; i < nparts; i += kBlock) m = fmaxf(m, b.pmax[i]);
+    const float M = wg_reduce(m, true, red4);
+    __syncthreads();
+    const bool k_on = use_topk(st, a.V);
+    uint32_t kk = 0;
+    int kid = a.V;
+    if (k_on) {
+        kk = b.ss[SK_COUNT].pfx;
+        kid = b.ss[SK_COUNT].id;
+    }
     const int base = blockIdx.x * kGenWide + threadIdx.x;
     float sum = 0.0f;
 #pragma unroll
     for (int j = 0; j < kGenWide / kBlock; j++) {
         const int i = base + j * kBlock;
         if (i < a.V) {
-            const float e = expf(a.scratch[i] - M);
-            a.scratch[a.V + i] = e;
+            const float s = b.sc[i];
+            const uint32_t k = f32_order(s);
+            const float e = (!k_on || k > kk || (k == kk && i <= kid)) ? expf(s - M) : 0.0f;
+            b.pr[i] = e;
             sum += e;
         }
     }
     const float S = wg_reduce(sum, false, red4);
-    if (threadIdx.x == 0) a.scratch[2 * (size_t)a.V + kGenParts + blockIdx.x] = S;
+    if (threadIdx.x == 0) b.psum[blockIdx.x] = S;
 }
 
-// pass 3 (no top-k): pr = pr / S, S the partial sums added in order
+// pass 3: pr = pr / S, S the partial sums added in order
 __global__ __launch_bounds__(kBlock) void sample_norm_kernel(const SampleArgs a) {
     __shared__ float Ssh;
-    const DevState st = *a.st;
-    if (st.top_k > 0 && st.top_k < a.V) return;
+    const GenBufs b = gen_bufs(a);
     const int nparts = (a.V + kGenWide - 1) / kGenWide;
     if (threadIdx.x == 0) {
-        const float *ps = a.scratch + 2 * (size_t)a.V + kGenParts;
         float S = 0.0f;
-        for (int i = 0; i < nparts; i++) S += ps[i];
+        for (int i = 0; i < nparts; i++) S += b.psum[i];
         Ssh = S;
     }
     __syncthreads();
@@ -691,214 +532,280 @@ __global__ __launch_bounds__(kBlock) void sample_norm_kernel(const SampleArgs a)
 #pragma unroll
     for (int j = 0; j < kGenWide / kBlock; j++) {
         const int i = base + j * kBlock;
-        if (i < a.V) a.scratch[a.V + i] = a.scratch[a.V + i] / S;
+        if (i < a.V) b.pr[i] = b.pr[i] / S;
     }
 }
 
-__global__ __launch_bounds__(kGenThreads) void sample_general_kernel(const SampleArgs a) {
-    __shared__ GenShared sh;
-    const DevState st = *a.st;
-    const GenLayout L(a.V);
-    const int V = a.V, t = threadIdx.x;
-    float *sc = a.scratch, *pr = a.scratch + V;
-    // sc holds the scaled logits (sample_scale_kernel); without top-k pr
-    // already holds the probabilities (sample_exp_kernel, sample_norm_kernel)
-    // and the draw is sample_walk_kernel's, so only a nucleus cut is left
-    if (!(st.top_k > 0 && st.top_k < V) && !(st.top_p < 1.0f)) return;
+// A search level's histogram: key digit `level` of the selected ids whose
+// higher digits equal the prefix picked so far, weights into LDS bins, then
+// the non-zero bins into the global histogram.
+__global__ __launch_bounds__(kBlock) void search_hist_kernel(const SampleArgs a, int kind, int level) {
+    __shared__ unsigned long long h[kGenBins];
+    const GenBufs b = gen_bufs(a);
+    const SearchState s = b.ss[kind];
+    if (level > 0 && s.id != kSearchRunning) return;
+    const int shift = level == 0 ? 20 : level == 1 ? 8 : 0;
+    const uint32_t nb = level == 2 ? 256u : 4096u;
+    const int above = level == 1 ? 20 : 8;  // levels 1, 2: the prefix is key >> above
+    for (int i = threadIdx.x; i < (int)nb; i += kBlock) h[i] = 0;
+    __syncthreads();
+    constexpr int PER = kHistIds / kBlock;
+    const int base = blockIdx.x * kHistIds + threadIdx.x;
+    float sv[PER], pv[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int i = base + j * kBlock;
+        sv[j] = (kind != SK_NUCLEUS && i < a.V) ? b.sc[i] : 0.0f;
+        pv[j] = (kind != SK_COUNT && i < a.V) ? b.pr[i] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int i = base + j * kBlock;
+        uint32_t k;
+        unsigned long long w;
+        if (i >= a.V || !kind_kw(kind, sv[j], pv[j], k, w)) continue;
+        if (level > 0 && (k >> above) != s.pfx) continue;
+        atomicAdd(&h[(k >> shift) & (nb - 1)], w);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < (int)nb; i += kBlock)
+        if (h[i]) __hip_atomic_fetch_add(&b.hist[i], h[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
-    // The orders below are (key descending, id ascending) with the scaled
-    // logit as key for top-k and the walk after it -- the reference's sort --
-    // and the probability for the nucleus, whose sort leaves ties
-    // unspecified.
-    // the key of a cut id (read by its owner), from array v
-    auto cut_key = [&](const float *v, int cut) {
-        const bool own = cut >= L.base && cut < L.end && ((cut - L.base) & 63) == 0;
-        return (uint32_t)block_pick(own, own ? f32_order(v[cut]) : 0u, sh);
-    };
-    // top-k (0 < k < V): the k-th best scaled logit (kk, id kid); ids after
-    // it in the order are not candidates
-    const bool use_k = st.top_k > 0 && st.top_k < V;
-    uint32_t kk = 0;
-    int kid = V;
-    if (use_k) {
-        kid = desc_threshold(
-            L, sc, nullptr,
-            [](int, float s, float, uint32_t &k, unsigned long long &w) {
-                k = f32_order(s);
-                w = 1;
-                return true;
-            },
-            (unsigned long long)(st.top_k - 1), sh);
-        if (kid < 0) kid = V;  // unreachable: the count always exceeds k - 1
-        kk = kid < V ? cut_key(sc, kid) : 0u;
+// A search level's pick: the bin (from the top) where the running total
+// first exceeds what is left of the target; clears the global histogram for
+// the next level.  At level 0 a total that does not exceed the target ends
+// the search (id -1).
+__global__ __launch_bounds__(kPickThreads) void search_pick_kernel(const SampleArgs a, int kind, int level) {
+    __shared__ unsigned long long wt[kPickThreads / 64];
+    __shared__ unsigned long long pk;
+    const DevState st = *a.st;
+    const GenBufs b = gen_bufs(a);
+    const SearchState s = b.ss[kind];
+    if (level > 0 && s.id != kSearchRunning) return;
+    const int t = threadIdx.x;
+    const unsigned long long rest = level == 0 ? kind_target(kind, a, st) : s.rest;
+    const int nb = level == 2 ? 256 : 4096;
+    unsigned long long c[4], mine = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int bin = nb - 1 - 4 * t - j;
+        c[j] = bin >= 0 ? b.hist[bin] : 0ull;
+        mine += c[j];
     }
-    if (use_k) {
-        // softmax over the candidates: pr = exp(s - M) (0 for the others), S
-        // their sum, then pr = pr / S, the reference's probabilities; M is
-        // the overall maximum (the best id is always a candidate)
-        float m = -INFINITY;
-        const int nparts = (V + kGenWide - 1) / kGenWide;
-        for (int i = t; i < nparts; i += kGenThreads) m = fmaxf(m, sc[2 * (size_t)V + i]);
-        const float M = block_max_f(m, sh);
-        float sum = 0.0f;
-        gen_each(L, sc, nullptr, [&](int i, float s, float) {
-            const uint32_t k = f32_order(s);
-            const float e = (k > kk || (k == kk && i <= kid)) ? expf(s - M) : 0.0f;
-            pr[i] = e;
-            sum += e;
-        });
-        const float S = block_sum_f(sum, sh);
-        gen_each(L, pr, nullptr, [&](int i, float e, float) { pr[i] = e / S; });
-    }
-    // nucleus: keep through the first cumulative probability above top_p (in
-    // probability order), then divide the kept probabilities by their sum
-    if (st.top_p < 1.0f) {
-        unsigned long long kept = 0;
-        const int cut = desc_threshold(
-            L, pr, nullptr,
-            [&](int, float p, float, uint32_t &k, unsigned long long &w) {
-                k = f32_order(p);
-                w = fx(p);
-                return true;
-            },
-            fx(st.top_p), sh, &kept);
-        if (cut >= 0) {
-            const uint32_t ck = cut_key(pr, cut);
-            const float sumk = (float)((double)kept / kFx);
-            gen_each(L, pr, nullptr, [&](int i, float p, float) {
-                const uint32_t k = f32_order(p);
-                pr[i] = (k > ck || (k == ck && i <= cut)) ? p / sumk : 0.0f;
-            });
+    if (t == 0) pk = ~0ull;
+    unsigned long long total;
+    unsigned long long cum = block_excl_u64<kPickThreads / 64>(mine, wt, &total);
+    if (cum <= rest && cum + mine > rest) {
+        for (int j = 0; j < 4; j++) {
+            if (cum + c[j] > rest) {
+                // the bin (12 bits) and the weight before it (< 2^52)
+                pk = ((unsigned long long)(nb - 1 - 4 * t - j) << 52) | cum;
+                break;
+            }
+            cum += c[j];
         }
     }
-    // without top-k the draw walks the ids in order: sample_walk_kernel
-    if (!use_k) return;
-    // the draw: inverse-CDF walk in descending scaled-logit order (the
-    // top-k candidates are the sorted ids)
-    const float r = step_draw(a, st.step);
-    int pick = desc_threshold(
-        L, sc, pr,
-        [&](int, float s, float p, uint32_t &k, unsigned long long &w) {
-            k = f32_order(s);
-            w = fx(p);
-            return true;
-        },
-        fx(r), sh);
-    if (pick < 0) {
-        // past the last cumulative sum (rounding): the first candidate with
-        // p > 0 in walk order, i.e. the best key
-        unsigned long long best = ~0ull;
-        gen_each(L, sc, pr, [&](int i, float s, float p) {
-            if (!(p > 0.0f)) return;
-            const unsigned long long k = ((unsigned long long)~f32_order(s) << 32) | (uint32_t)i;
-            best = k < best ? k : best;
-        });
-        if (t == 0) sh.res[2] = ~0ull;
-        __syncthreads();
-        atomicMin(&sh.res[2], best);
-        __syncthreads();
-        const unsigned long long k = sh.res[2];
-        pick = k == ~0ull ? 0 : (int)(uint32_t)k;
+    __syncthreads();
+    const unsigned long long hit = pk;
+    // every thread has read its bins: clear them for the next level
+#pragma unroll
+    for (int j = 0; j < 4; j++) b.hist[4 * t + j] = 0ull;
+    if (t == 0) {
+        SearchState n = s;
+        if (total <= rest || hit == ~0ull) {
+            n.id = -1;
+        } else {
+            n.pfx = ((level == 0 ? 0u : s.pfx) << (level == 2 ? 8 : 12)) | (uint32_t)(hit >> 52);
+            n.rest = rest - (hit & ((1ull << 52) - 1));
+            n.id = kSearchRunning;
+        }
+        b.ss[kind] = n;
     }
-    if (t == 0) emit_token(a, pick);
 }
 
-// Without top-k: the inverse-CDF walk in id order (src/tensor.rs:1203-1212)
-// over the probabilities in pr (after any nucleus cut), in 2^-40 fixed
-// point.  Pass 1, one workgroup per 2048 ids: the chunk's mass.
+// Ties at the final key, in id order: pass 1, the mass of the tied ids per
+// 2048-id chunk.
+__global__ __launch_bounds__(kBlock) void search_tie_sums_kernel(const SampleArgs a, int kind) {
+    __shared__ unsigned long long red4[4];
+    const GenBufs b = gen_bufs(a);
+    const SearchState s = b.ss[kind];
+    if (s.id != kSearchRunning) return;
+    const int i0 = blockIdx.x * kGenWide + 8 * threadIdx.x;
+    unsigned long long m = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int i = i0 + j;
+        if (i >= a.V) break;
+        uint32_t k;
+        unsigned long long w;
+        if (kind_kw(kind, b.sc[i], b.pr[i], k, w) && k == s.pfx) m += w;
+    }
+    m = wave_sum_u64(m);
+    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) b.pmass[blockIdx.x] = (red4[0] + red4[1]) + (red4[2] + red4[3]);
+}
+
+// The first id, in id order, where the running mass of wv(i) (any i < V)
+// exceeds `rest`, given each 2048-id chunk's mass in pmass: the chunk by a
+// prefix over the chunk masses, then the id within it (thread t holds ids
+// 8t .. 8t+7 of the chunk, so thread order is id order).  Returns -1 when
+// the total does not exceed `rest`; *through gets the running mass through
+// the id.  One workgroup of kBlock threads.
+template <class Wv>
+__device__ int chunk_threshold(const SampleArgs &a, const unsigned long long *pmass, Wv wv, unsigned long long rest,
+                               unsigned long long *through) {
+    __shared__ unsigned long long wt[4];
+    __shared__ unsigned long long pk, pth;
+    const int t = threadIdx.x;
+    const int nparts = (a.V + kGenWide - 1) / kGenWide;  // <= kGenParts <= kBlock
+    if (t == 0) pk = ~0ull;
+    const unsigned long long c = t < nparts ? pmass[t] : 0ull;
+    unsigned long long tot;
+    const unsigned long long cum = block_excl_u64<4>(c, wt, &tot);
+    if (t < nparts && cum <= rest && cum + c > rest) pk = ((unsigned long long)t << 48) | cum;
+    __syncthreads();
+    const unsigned long long hit = pk;
+    __syncthreads();
+    if (hit == ~0ull) return -1;
+    const int g = (int)(hit >> 48);
+    const unsigned long long before = hit & ((1ull << 48) - 1), left = rest - before;
+    const int i0 = g * kGenWide + 8 * t;
+    unsigned long long q[8], m = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        q[k] = i0 + k < a.V ? wv(i0 + k) : 0ull;
+        m += q[k];
+    }
+    if (t == 0) pk = ~0ull;
+    unsigned long long t2;
+    unsigned long long cu = block_excl_u64<4>(m, wt, &t2);
+    if (cu <= left && cu + m > left) {
+        for (int k = 0; k < 8; k++) {
+            cu += q[k];
+            if (cu > left) {
+                pk = (unsigned long long)(i0 + k);
+                pth = before + cu;
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    const unsigned long long r = pk;
+    if (through) *through = pth;
+    __syncthreads();
+    return r == ~0ull ? -1 : (int)r;
+}
+
+// Ties, pass 2: the id; SK_WALK then emits the token (with the reference's
+// fallback when the draw lies past the last cumulative sum: the first
+// candidate with p > 0 in walk order, i.e. the best key).
+__global__ __launch_bounds__(kBlock) void search_tie_pick_kernel(const SampleArgs a, int kind) {
+    __shared__ unsigned long long best_sh;
+    const DevState st = *a.st;
+    const GenBufs b = gen_bufs(a);
+    const SearchState s = b.ss[kind];
+    const int t = threadIdx.x;
+    int id = -1;
+    unsigned long long through = 0;
+    if (s.id == kSearchRunning) {
+        id = chunk_threshold(
+            a, b.pmass,
+            [&](int i) -> unsigned long long {
+                uint32_t k;
+                unsigned long long w;
+                return kind_kw(kind, b.sc[i], b.pr[i], k, w) && k == s.pfx ? w : 0ull;
+            },
+            s.rest, &through);
+        // the running total from the search's start: the heavier keys'
+        // target - rest, then the ties'
+        through += kind_target(kind, a, st) - s.rest;
+    }
+    if (kind != SK_WALK) {
+        if (t == 0) {
+            SearchState n = s;
+            n.id = s.id == kSearchRunning ? id : -1;
+            n.through = through;
+            b.ss[kind] = n;
+        }
+        return;
+    }
+    if (id < 0) {
+        unsigned long long best = ~0ull;
+        for (int i = t; i < a.V; i += kBlock) {
+            const float p = b.pr[i];
+            if (!(p > 0.0f)) continue;
+            const unsigned long long k = ((unsigned long long)~f32_order(b.sc[i]) << 32) | (uint32_t)i;
+            best = k < best ? k : best;
+        }
+        if (t == 0) best_sh = ~0ull;
+        __syncthreads();
+        atomicMin(&best_sh, best);
+        __syncthreads();
+        id = best_sh == ~0ull ? 0 : (int)(uint32_t)best_sh;
+    }
+    if (t == 0) emit_token(a, id);
+}
+
+// The nucleus cut (src/tensor.rs:1182-1201): ids after the cut in
+// probability order get 0, the kept ones p / (kept mass).
+__global__ __launch_bounds__(kBlock) void sample_renorm_kernel(const SampleArgs a) {
+    const GenBufs b = gen_bufs(a);
+    const SearchState s = b.ss[SK_NUCLEUS];
+    if (s.id < 0) return;
+    const float sumk = (float)((double)s.through / kFx);
+    const int base = blockIdx.x * kGenWide + threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < kGenWide / kBlock; j++) {
+        const int i = base + j * kBlock;
+        if (i < a.V) {
+            const float p = b.pr[i];
+            const uint32_t k = f32_order(p);
+            b.pr[i] = (k > s.pfx || (k == s.pfx && i <= s.id)) ? p / sumk : 0.0f;
+        }
+    }
+}
+
+// Without top-k: the inverse-CDF walk in id order (src/tensor.rs:1203-1212),
+// pass 1: each 2048-id chunk's probability mass.
 __global__ __launch_bounds__(kBlock) void sample_walk_sums_kernel(const SampleArgs a) {
     __shared__ unsigned long long red4[4];
-    const DevState st = *a.st;
-    if (st.top_k > 0 && st.top_k < a.V) return;
+    const GenBufs b = gen_bufs(a);
     const int base = blockIdx.x * kGenWide + threadIdx.x;
     unsigned long long m = 0;
 #pragma unroll
     for (int j = 0; j < kGenWide / kBlock; j++) {
         const int i = base + j * kBlock;
-        if (i < a.V) m += fx(a.scratch[a.V + i]);
+        if (i < a.V) m += fx(b.pr[i]);
     }
     m = wave_sum_u64(m);
     if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = m;
     __syncthreads();
-    if (threadIdx.x == 0)
-        reinterpret_cast<unsigned long long *>(a.scratch + 2 * (size_t)a.V + 2 * kGenParts)[blockIdx.x] =
-            (red4[0] + red4[1]) + (red4[2] + red4[3]);
+    if (threadIdx.x == 0) b.pmass[blockIdx.x] = (red4[0] + red4[1]) + (red4[2] + red4[3]);
 }
 
-// Pass 2, one workgroup: the chunk where the running mass first exceeds the
-// draw (a prefix over the chunk masses), then the id inside it (thread t
-// holds ids 8t .. 8t+7 of the chunk, so thread order is id order).
+// pass 2: the id where the running mass first exceeds the draw, emitted
+// (past the last cumulative sum: the lowest id with p > 0).
 __global__ __launch_bounds__(kBlock) void sample_walk_kernel(const SampleArgs a) {
-    __shared__ unsigned long long wt[4];
-    __shared__ unsigned long long pick_sh;
+    __shared__ unsigned long long best_sh;
     const DevState st = *a.st;
-    if (st.top_k > 0 && st.top_k < a.V) return;
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const float *pr = a.scratch + a.V;
-    const unsigned long long *parts =
-        reinterpret_cast<const unsigned long long *>(a.scratch + 2 * (size_t)a.V + 2 * kGenParts);
-    const int nparts = (a.V + kGenWide - 1) / kGenWide;  // <= kGenParts <= kBlock
-    const unsigned long long rf = fx(step_draw(a, st.step));
-    auto block_excl = [&](unsigned long long v, unsigned long long *tot) {
-        const unsigned long long incl = wave_incl_u64(v);
-        __syncthreads();
-        if (lane == 63) wt[w] = incl;
-        __syncthreads();
-        unsigned long long before = 0;
-        for (int i = 0; i < w; i++) before += wt[i];
-        *tot = (wt[0] + wt[1]) + (wt[2] + wt[3]);
-        return before + incl - v;
-    };
-    if (t == 0) pick_sh = ~0ull;
-    const unsigned long long c = t < nparts ? parts[t] : 0ull;
-    unsigned long long tot;
-    const unsigned long long cum = block_excl(c, &tot);
-    __syncthreads();
-    if (t < nparts && cum <= rf && cum + c > rf) pick_sh = ((unsigned long long)t << 48) | cum;
-    __syncthreads();
-    const unsigned long long hit = pick_sh;
-    __syncthreads();
-    int pick = -1;
-    if (hit != ~0ull) {
-        const int g = (int)(hit >> 48);
-        const unsigned long long left = rf - (hit & ((1ull << 48) - 1));
-        const int i0 = g * kGenWide + 8 * t;
-        unsigned long long q[8], m = 0;
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            q[k] = i0 + k < a.V ? fx(pr[i0 + k]) : 0ull;
-            m += q[k];
-        }
-        unsigned long long t2;
-        unsigned long long cu = block_excl(m, &t2);
-        if (t == 0) pick_sh = ~0ull;
-        __syncthreads();
-        if (cu <= left && cu + m > left) {
-            for (int k = 0; k < 8; k++) {
-                cu += q[k];
-                if (cu > left) {
-                    pick_sh = (unsigned long long)(i0 + k);
-                    break;
-                }
-            }
-        }
-        __syncthreads();
-        pick = pick_sh == ~0ull ? -1 : (int)pick_sh;
-    }
+    const GenBufs b = gen_bufs(a);
+    const int t = threadIdx.x;
+    int pick = chunk_threshold(
+        a, b.pmass, [&](int i) { return fx(b.pr[i]); }, fx(step_draw(a, st.step)), nullptr);
     if (pick < 0) {
-        // past the last cumulative sum (rounding): the lowest id with p > 0
         unsigned long long best = ~0ull;
         for (int i = t; i < a.V; i += kBlock)
-            if (pr[i] > 0.0f) {
+            if (b.pr[i] > 0.0f) {
                 best = (unsigned long long)i;
                 break;
             }
+        if (t == 0) best_sh = ~0ull;
         __syncthreads();
-        if (t == 0) pick_sh = ~0ull;
+        atomicMin(&best_sh, best);
         __syncthreads();
-        atomicMin(&pick_sh, best);
-        __syncthreads();
-        pick = pick_sh == ~0ull ? 0 : (int)pick_sh;
+        pick = best_sh == ~0ull ? 0 : (int)best_sh;
     }
     if (t == 0) emit_token(a, pick);
 }
@@ -918,13 +825,29 @@ hipError_t launch_sample(const SampleArgs &a, hipStream_t s) {
         return hipGetLastError();
     }
     if (!a.scratch) return hipErrorInvalidValue;
-    const dim3 wide((a.V + kGenWide - 1) / kGenWide);
+    const dim3 wide((a.V + kGenWide - 1) / kGenWide), hist((a.V + kHistIds - 1) / kHistIds);
+    auto search = [&](int kind) {
+        for (int level = 0; level < 3; level++) {
+            hipLaunchKernelGGL(search_hist_kernel, hist, dim3(kBlock), 0, s, a, kind, level);
+            hipLaunchKernelGGL(search_pick_kernel, dim3(1), dim3(kPickThreads), 0, s, a, kind, level);
+        }
+        hipLaunchKernelGGL(search_tie_sums_kernel, wide, dim3(kBlock), 0, s, a, kind);
+        hipLaunchKernelGGL(search_tie_pick_kernel, dim3(1), dim3(kBlock), 0, s, a, kind);
+    };
     hipLaunchKernelGGL(sample_scale_kernel, wide, dim3(kBlock), 0, s, a);
+    if (a.use_k) search(SK_COUNT);
     hipLaunchKernelGGL(sample_exp_kernel, wide, dim3(kBlock), 0, s, a);
     hipLaunchKernelGGL(sample_norm_kernel, wide, dim3(kBlock), 0, s, a);
-    hipLaunchKernelGGL(sample_general_kernel, dim3(1), dim3(kGenThreads), 0, s, a);
-    hipLaunchKernelGGL(sample_walk_sums_kernel, wide, dim3(kBlock), 0, s, a);
-    hipLaunchKernelGGL(sample_walk_kernel, dim3(1), dim3(kBlock), 0, s, a);
+    if (a.use_p) {
+        search(SK_NUCLEUS);
+        hipLaunchKernelGGL(sample_renorm_kernel, wide, dim3(kBlock), 0, s, a);
+    }
+    if (a.use_k) {
+        search(SK_WALK);
+    } else {
+        hipLaunchKernelGGL(sample_walk_sums_kernel, wide, dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL(sample_walk_kernel, dim3(1), dim3(kBlock), 0, s, a);
+    }
     return hipGetLastError();
 }
 
