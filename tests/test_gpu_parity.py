@@ -274,6 +274,76 @@ def test_sampling_odd_vocab(T, O, odd_vocab, temp, k, p, pen):
     assert mism <= 1, f"{mism} of 40 sampled ids differ"
 
 
+@pytest.fixture(scope="module")
+def big_vocab(T, O, W):
+    import dataclasses
+    wl = dataclasses.replace(W.TINY, name="tiny-llama-v200003-s17", vocab_size=200003, weight_seed=17,
+                             tied_lm_head=False)
+    p = W.ensure_model(wl, model_root())
+    return T.Model.load(p), O.OracleModel.load(p), wl
+
+
+def exact_sum_sample(lg, temp, k, p, r):
+    """The reference's sample() (src/tensor.rs:1157-1213) with its running
+    sums taken exactly (2^-40 fixed point), as the device computes them.  The
+    reference adds in f32, one term at a time; over a near-flat distribution
+    of 2e5 ids that running sum drifts from the exact one by about one
+    median probability, which moves the cut and the draw by about one id."""
+    s = (np.asarray(lg, np.float32) / np.float32(temp)).astype(np.float32)
+    V = s.size
+    ids = np.arange(V)
+    FX = lambda x: np.floor(np.asarray(x, np.float64) * 2.0**40).astype(np.int64)  # noqa: E731
+    cand = np.lexsort((ids, -s.astype(np.float64)))[:k] if 0 < k < V else ids
+    e = np.exp((s[cand] - s.max()).astype(np.float32)).astype(np.float32)
+    pr = (e / np.float32(e.sum(dtype=np.float64))).astype(np.float32)
+    if p < 1.0:
+        o2 = np.lexsort((cand, -pr.astype(np.float64)))
+        cum = np.cumsum(FX(pr[o2]))
+        cut = int(np.searchsorted(cum, FX(np.float32(p)), side="right"))
+        if cut < cum.size:
+            kept = o2[:cut + 1]
+            sumk = np.float32(cum[cut] / 2.0**40)
+            q = np.zeros_like(pr)
+            q[kept] = (pr[kept] / sumk).astype(np.float32)
+            pr = q
+    cum = np.cumsum(FX(pr))
+    j = int(np.searchsorted(cum, FX(np.float32(r)), side="right"))
+    if j < cum.size:
+        return int(cand[j])
+    nz = np.nonzero(pr > 0)[0]
+    return int(cand[nz[0]]) if nz.size else int(cand[0])
+
+
+# 200003 ids (odd, 98 sampler slices, 98 chunks, 49 histogram workgroups):
+# the sampler on the GPU's own logits (those checked against the oracle's)
+# against the reference's algorithm with exact running sums; the chosen id
+# is in the oracle's candidate set with p > 0
+@pytest.mark.parametrize("temp,k,p,pen", [(0.9, 0, 0.9, 1.1), (1.0, 50, 0.9, 1.0), (1.1, 300, 0.95, 1.2),
+                                          (0.8, 0, 1.0, 1.0), (0.0, 0, 1.0, 1.3)])
+def test_sampling_big_vocab(T, O, big_vocab, temp, k, p, pen):
+    g, o, wl = big_vocab
+    prompt = [int(t) for t in T.synth_tokens(37, 11, wl.vocab_size)]
+    n = 24
+    out = T.generate(g, prompt, T.GenParams(max_tokens=n, temperature=temp, top_k=k, top_p=p,
+                                            repetition_penalty=pen, seed=11))
+    assert len(out.tokens) == n and all(0 <= t < wl.vocab_size for t in out.tokens)
+    ref = O.generate(o, prompt, n, forced=out.tokens, repetition_penalty=pen, keep_logits=True)
+    gc = T.KvCache(g, len(prompt) + n + 2)
+    lg = g.forward_seq(prompt, gc)
+    mism = 0
+    for i, tok in enumerate(out.tokens):
+        lp = O.apply_repetition_penalty(lg, out.tokens[:i], pen) if i else np.asarray(lg, np.float32)
+        close_logits(lp, ref.step_logits[i], f"V=200003 step {i}")
+        if temp <= 0.0:
+            mism += O.sample(lp, temp, k, p, 0.0).token != tok
+        else:
+            mism += exact_sum_sample(lp, temp, k, p, device_draw(11, i)) != tok
+            tr = O.sample(ref.step_logits[i], temp, k, p, device_draw(11, i))
+            assert tok in set(int(c) for c, pr in zip(tr.cand_ids, tr.cand_probs) if pr > 0), f"step {i}"
+        lg = g.forward_token(tok, gc)
+    assert mism <= 1, f"{mism} of {n} sampled ids differ"
+
+
 # --- C2: the 1B-class model, prefill 64 + greedy decode -----------------------
 
 @pytest.fixture(scope="module")
