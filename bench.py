@@ -227,6 +227,13 @@ def main():
                          "decode tok/s over the B sequences")
     ap.add_argument("--format", choices=["safetensors", "tmb"], default="safetensors",
                     help="tmb: repack the model into a TMB1 file once (the reference's --repack) and load that")
+    ap.add_argument("--temperature", type=float, default=None,
+                    help="sample through generate with these parameters (the rest default to the 4b workload's: "
+                         "T=0.8, top-k 50, top-p 0.9, penalty 1.1, seed 42); top-k 0 or above 64 and top-p < 1 "
+                         "without top-k take the whole-vocabulary sampler")
+    ap.add_argument("--top-k", type=int, default=None)
+    ap.add_argument("--top-p", type=float, default=None)
+    ap.add_argument("--repetition-penalty", type=float, default=None)
     ap.add_argument("--model-dir", default=os.environ.get("TMG_MODEL_DIR",
                                                            os.path.join(tempfile.gettempdir(), "tmg_models")))
     args = ap.parse_args()
@@ -244,7 +251,12 @@ def main():
     from tinyminigo_amd.hip import synchronize as sync
 
     wl = {"1b": W.ONE_B, "4b": W.FOUR_B, "8k": W.LONG_CTX}[args.workload]
-    sampled = args.workload == "4b"
+    samp = dict(SAMPLED) if args.workload == "4b" else None
+    over = {k: v for k, v in (("temperature", args.temperature), ("top_k", args.top_k), ("top_p", args.top_p),
+                              ("repetition_penalty", args.repetition_penalty)) if v is not None}
+    if over:
+        samp = dict(SAMPLED if samp is None else samp, **over)
+    sampled = samp is not None and samp["temperature"] > 0
     t0 = time.perf_counter()
     path = W.ensure_model(wl, args.model_dir)
     log(f"model ready at {path} ({time.perf_counter() - t0:.1f}s)")
@@ -291,10 +303,10 @@ def main():
         # the product path: generate (prefill, device sampling, one id per
         # step to the host); decode tok/s as the reference's main.rs reports
         # it, (n - 1) / (elapsed - prefill)
-        T.generate(m, prompt, T.GenParams(max_tokens=Wm, **SAMPLED))
+        T.generate(m, prompt, T.GenParams(max_tokens=Wm, **samp))
         sync()
         t = time.perf_counter()
-        gen = T.generate(m, prompt, T.GenParams(max_tokens=K, **SAMPLED))
+        gen = T.generate(m, prompt, T.GenParams(max_tokens=K, **samp))
         wall_all = time.perf_counter() - t
         wall = wall_all - gen.prefill_secs
         K_timed = len(gen.tokens) - 1
@@ -351,9 +363,10 @@ def main():
         log("timing the CPU baseline")
         cpu = cpu_baseline(path, prompt, args.cpu_seconds, wl if args.workload == "8k" else None,
                            m if args.workload == "8k" else None, cache if args.workload == "8k" else None,
-                           SAMPLED if sampled else None, i8)
+                           samp if sampled else None, i8)
 
-    kind = (f"{K} sampled tokens (T=0.8, top-k 50, top-p 0.9, penalty 1.1, seed 42) through generate"
+    kind = (f"{K} sampled tokens (T={samp['temperature']:g}, top-k {samp['top_k']}, top-p {samp['top_p']:g}, "
+             f"penalty {samp['repetition_penalty']:g}, seed {samp['seed']}) through generate"
             if sampled else f"{K} greedy decode steps")
     out = {
         "metric": METRIC,
