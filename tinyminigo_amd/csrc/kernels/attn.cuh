@@ -28,18 +28,18 @@ namespace tmg {
 // head_dim 128 halve the cross-lane reduction steps per score against one
 // (measured faster with two query heads per KV head, slower with four, where
 // the doubled accumulator registers cost more than the reductions saved).
-template <int HD, int GROUP>
+template <int HD, int GROUP, int NT = kBlock>
 struct AttnGeom {
     static constexpr int VPL = (HD >= 128 && GROUP <= 2) ? 2 : 1;
     static constexpr int TS = HD / (4 * VPL);
-    static constexpr int NTEAM = kBlock / TS;
+    static constexpr int NTEAM = NT / TS;
     static constexpr int J = NTEAM >= 64 ? 1 : 64 / NTEAM;
     static constexpr int CH = NTEAM * J;
 };
 
-template <int HD, int GROUP>
+template <int HD, int GROUP, int NT = kBlock>
 struct AttnShared {
-    static constexpr int NTEAM = AttnGeom<HD, GROUP>::NTEAM;
+    static constexpr int NTEAM = AttnGeom<HD, GROUP, NT>::NTEAM;
     float o[NTEAM][GROUP][HD];
     float m[NTEAM][GROUP];
     float l[NTEAM][GROUP];
@@ -64,10 +64,10 @@ __device__ __forceinline__ int active_splits(int n_ctx, int nsplit) {
 // capacity a.cap), so the K/V loads do not wait for it; qpos and active are
 // then computed here and the arguments ignored.  Splits found inactive
 // return at once.
-template <int HD, int GROUP, bool COH, bool PREFETCH = true, bool SPEC = false>
+template <int HD, int GROUP, bool COH, bool PREFETCH = true, bool SPEC = false, int NT = kBlock>
 __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, int ti, int qpos, int active,
-                                          AttnShared<HD, GROUP> &sm) {
-    using G = AttnGeom<HD, GROUP>;
+                                          AttnShared<HD, GROUP, NT> &sm) {
+    using G = AttnGeom<HD, GROUP, NT>;
     constexpr int VPL = G::VPL, TS = G::TS, NTEAM = G::NTEAM;
     constexpr int J = G::J;  // positions per team per chunk
     constexpr int CH = G::CH;
@@ -220,7 +220,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
     const size_t row_hd = (size_t)ti * qd + g * GROUP * HD;
     const size_t pbase = (((size_t)ti * a.nkv + g) * a.nsplit + split) * GROUP;
     const bool direct = active == 1 && (a.out_f32 || a.out_hi);
-    for (int idx = t; idx < GROUP * HD; idx += kBlock) {
+    for (int idx = t; idx < GROUP * HD; idx += NT) {
         const int h = idx / HD, d = idx % HD;
         float M = -INFINITY;
 #pragma unroll 8
