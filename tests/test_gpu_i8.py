@@ -152,6 +152,31 @@ def test_i8_generate_greedy_vs_oracle(T, O, untied_i8):
     assert list(toks) == ref.tokens[1:]
 
 
+@pytest.mark.parametrize("temp,k,p,pen,seed", [(0.8, 50, 0.9, 1.1, 42), (0.9, 0, 0.9, 1.0, 3), (1.2, 200, 1.0, 1.2, 9)])
+def test_i8_sampling_teacher_forced(T, O, untied_i8, temp, k, p, pen, seed):
+    # int8 weights with both sampling paths: replaying the sampled ids, each
+    # step's GPU logits are within tolerance of the int8 oracle's, and the
+    # oracle's sample() on the GPU's logits with the reference's StdRng draw
+    # picks the GPU's id (a free-running comparison would diverge for good
+    # after one draw boundary, which the int8 logit differences make likelier)
+    g, o, _, wl = untied_i8
+    prompt = [int(t) for t in T.synth_tokens(27, 12, wl.vocab_size)]
+    n = 32
+    out = T.generate(g, prompt, T.GenParams(max_tokens=n, temperature=temp, top_k=k, top_p=p,
+                                            repetition_penalty=pen, seed=seed))
+    ref = O.generate(o, prompt, n, forced=out.tokens, repetition_penalty=pen, keep_logits=True)
+    draws = O.stdrng_uniform(seed, n)
+    gc = T.KvCache(g, len(prompt) + n + 2)
+    lg = g.forward_seq(prompt, gc)
+    mism = 0
+    for i, tok in enumerate(out.tokens):
+        lp = O.apply_repetition_penalty(lg, out.tokens[:i], pen) if i else np.asarray(lg, np.float32)
+        close_logits(lp, ref.step_logits[i], f"i8 sampled step {i}")
+        mism += O.sample(lp, temp, k, p, float(draws[i])).token != tok
+        lg = g.forward_token(tok, gc)
+    assert mism <= 1, f"{mism} of {n} sampled ids differ"
+
+
 def test_i8_k_not_multiple_of_64(T, O, W):
     import dataclasses
     wl = dataclasses.replace(W.TINY, name="tiny-llama-h96-kv3-i160-s13", hidden_size=96, num_attention_heads=6,
