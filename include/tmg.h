@@ -106,6 +106,11 @@ int tmg_tmb_repack(const char *safetensors_path, const char *tmb_path);
  * reference's writer produced.  tied_lm_head is 1 when the file has no
  * lm_head.weight. */
 int tmg_tmb_config(const char *tmb_path, tmg_config *out);
+/* Drop of Model (src/model.rs:338-347).  May be called before the model's
+ * caches are freed (Rust drops struct fields in declaration order): the
+ * model's device memory and stream are then released by the last
+ * tmg_cache_free.  After this call the model handle itself must not be used
+ * again; its caches may still be read, reset and freed. */
 void tmg_model_free(tmg_model *model);
 int tmg_model_config(const tmg_model *model, tmg_config *out);
 

@@ -413,48 +413,6 @@ def test_decode_attention_split_modes(T, O, untied, max_pos):
     assert gc.total_len() == n
 
 
-# --- persistent decode kernel vs the per-kernel graph path --------------------
-
-def _with_mode(mode, fn):
-    old = os.environ.get("TMG_DECODE_MODE")
-    os.environ["TMG_DECODE_MODE"] = mode
-    try:
-        return fn()
-    finally:
-        if old is None:
-            del os.environ["TMG_DECODE_MODE"]
-        else:
-            os.environ["TMG_DECODE_MODE"] = old
-
-
-@pytest.mark.parametrize("which", ["untied", "one_b"])
-def test_persistent_matches_graph_bitwise(T, W, which, request):
-    # both paths run the same device functions in the same order: the logits
-    # and ids must be identical, not merely close
-    if which == "untied":
-        g = request.getfixturevalue("untied")[0]
-        prompt = [int(t) for t in T.synth_tokens(41, 24, g.config.vocab_size)]
-    else:
-        g = request.getfixturevalue("one_b")[0]
-        prompt = [int(t) for t in W.ONE_B.prompt()]
-    n = 40
-
-    def run(mode):
-        def body():
-            c = T.KvCache(g, len(prompt) + n + 8)
-            first = int(np.argmax(g.forward_seq(prompt, c)))
-            toks, _ = g.decode_greedy(first, n, c)
-            lg = g.forward_token(int(toks[-1]), c)
-            return list(toks), lg, c.keys_flat(g.config.num_hidden_layers - 1)
-        return _with_mode(mode, body)
-
-    tp, lp, kp = run("persistent")
-    tg, lgr, kg = run("graph")
-    assert tp == tg
-    assert np.array_equal(lp, lgr)
-    assert np.array_equal(kp, kg)
-
-
 # --- C4: the 4B-class model, 128-token prompt + 256 sampled tokens ------------
 
 @pytest.fixture(scope="module")

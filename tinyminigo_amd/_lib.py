@@ -5,8 +5,11 @@ when libtmg.so is missing, importing this module raises ImportError.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import os
+import sys
+import weakref
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtmg.so")
@@ -156,3 +159,43 @@ class TmgError(RuntimeError):
 def check(rc: int) -> None:
     if rc != TMG_OK:
         raise TmgError(rc, lib.tmg_last_error().decode(errors="replace"))
+
+
+# ---- native handle lifetime --------------------------------------------------
+#
+# Every Python object that owns a native handle (a model, a KV cache, a device
+# buffer, a stream, a graph, timing events) registers here.  At interpreter
+# exit they are released explicitly, in dependency order (graphs and events,
+# then caches, buffers, models, streams), while the HIP runtime is still whole;
+# after that no finalizer makes a HIP or libtmg call.
+
+_RANKS = 5
+_live = [weakref.WeakSet() for _ in range(_RANKS)]
+_released = False
+
+
+def register(obj, rank: int) -> None:
+    """Track `obj` (which has a close() method) for release at exit."""
+    _live[rank].add(obj)
+
+
+def finalizing() -> bool:
+    """True once native handles must no longer be touched from finalizers."""
+    return _released or sys.is_finalizing()
+
+
+def release_all() -> None:
+    """Close every live native handle (idempotent); called at exit."""
+    global _released
+    if _released:
+        return
+    for rank in range(_RANKS):
+        for obj in list(_live[rank]):
+            try:
+                obj.close()
+            except Exception:
+                pass
+    _released = True
+
+
+atexit.register(release_all)

@@ -327,20 +327,6 @@ static int load_model(tmg_model *m, const SafeTensorsFile &f) {
     if ((rc = ensure_rope(m, 64))) return rc;
     if ((rc = pinned(m, (size_t)std::max<uint64_t>(V * 4, 1 << 16)))) return rc;
 
-    // persistent decode: instantiated for this shape, cooperative launch
-    // supported, and at least 8 workgroups co-resident (at most 2 per CU)
-    const int kc_h = (m->H + 2047) / 2048, kc_q = (m->qd + 2047) / 2048, kc_i = (m->I + 2047) / 2048;
-    // (BF16 rows only: int8 models take the per-kernel step)
-    const void *pk = m->i8 ? nullptr : persistent_kernel(kc_h, kc_q, kc_i, m->hd, group);
-    int coop = 0, cus = 0, per_cu = 0;
-    if (pk && m->L <= kMaxPlanLayers &&
-        hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, m->device) == hipSuccess && coop &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->device) == hipSuccess &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, pk, 256, 0) == hipSuccess && per_cu > 0) {
-        m->pk = pk;
-        m->pk_grid = std::min(per_cu, 2) * cus;
-        if (m->pk_grid < kBarGroups) m->pk = nullptr;
-    }
     TMG_HIP(hipDeviceSynchronize());
     return TMG_OK;
 }
@@ -511,171 +497,6 @@ int enqueue_select(tmg_model *m, tmg_cache *c, int mode, int advance_pos) {
     sa.greedy = mode == SEL_PENALTY_ARGMAX;
     sa.advance_pos = advance_pos;
     TMG_HIP(launch_sample(sa, m->stream));
-    return TMG_OK;
-}
-
-// Argument blocks of the persistent decode kernel for cache c (the same
-// arguments enqueue_decode_step passes to the per-kernel launches).
-int build_plan(tmg_model *m, tmg_cache *c) {
-    std::unique_ptr<PersistPlan> pl(new PersistPlan());
-    memset(pl.get(), 0, sizeof(PersistPlan));
-    const int H = m->H, I = m->I, qd = m->qd, kvd = m->kvd;
-    for (int l = 0; l < m->L; l++) {
-        const tmg_model::Layer &ly = m->layers[l];
-        float *kc = c->k + (size_t)l * c->max_pos * kvd;
-        float *vc = c->v + (size_t)l * c->max_pos * kvd;
-        GemvArgs &q = pl->qkv[l];
-        q.W = ly.qkv;
-        q.out = m->qkv_rows;
-        q.in = H;
-        q.x = m->x;
-        q.norm_w = ly.in_norm;
-        q.eps = m->cfg.rms_norm_eps;
-        q.rope_cos = m->rope_cos;
-        q.rope_sin = m->rope_sin;
-        q.pos = &c->st->pos;
-        q.hd = m->hd;
-        q.nq = m->nq;
-        q.nkv = m->nkv;
-        q.q_out = m->q;
-        q.k_cache = kc;
-        q.v_cache = vc;
-        if (l == 0) {
-            q.token = &c->st->cur_token;
-            q.embed_bf16 = m->embed_bf16;
-            q.embed_f32 = m->embed_f32;
-            q.x_store = m->x;
-        }
-        GemvArgs &o = pl->o[l];
-        o.W = ly.o;
-        o.out = H;
-        o.in = qd;
-        o.x = m->attn_out;
-        o.y = m->x;
-        o.part = m->attn_part;
-        o.part_ml = m->attn_ml;
-        o.pos = &c->st->pos;
-        o.nsplit = c->attn_nsplit;
-        o.hd = m->hd;
-        o.group = m->nq / m->nkv;
-        GemvArgs &g = pl->gu[l];
-        g.W = ly.gu;
-        g.out = 2 * I;
-        g.in = H;
-        g.x = m->x;
-        g.norm_w = ly.post_norm;
-        g.eps = m->cfg.rms_norm_eps;
-        g.y = m->h;
-        GemvArgs &d = pl->down[l];
-        d.W = ly.down;
-        d.out = H;
-        d.in = I;
-        d.x = m->h;
-        d.y = m->x;
-        AttnArgs &a = pl->attn[l];
-        a.q = m->q;
-        a.k_cache = kc;
-        a.v_cache = vc;
-        a.nq = m->nq;
-        a.nkv = m->nkv;
-        a.hd = m->hd;
-        a.T = 1;
-        a.pos_dev = &c->st->pos;
-        a.scale = 1.0f / sqrtf((float)m->hd);
-        a.nsplit = c->attn_nsplit;
-        a.part = m->attn_part;
-        a.part_ml = m->attn_ml;
-    }
-    GemvArgs &lm = pl->lm;
-    lm.W = m->lm_head;
-    lm.out = m->V;
-    lm.in = H;
-    lm.x = m->x;
-    lm.norm_w = m->final_norm;
-    lm.eps = m->cfg.rms_norm_eps;
-    lm.y = m->logits;
-    lm.argmax_part = m->argmax_part;
-    TMG_HIP(hipMemcpy(c->plan, pl.get(), sizeof(PersistPlan), hipMemcpyHostToDevice));
-    return TMG_OK;
-}
-
-int enqueue_persistent(tmg_model *m, tmg_cache *c, int steps, bool *used) {
-    *used = false;
-    // opt-in (TMG_DECODE_MODE=persistent): on MI355X the per-phase chain of
-    // dependent memory round trips (arguments, activations, store completion,
-    // barrier) costs more than the captured graph's kernel boundaries
-    const char *mode = getenv("TMG_DECODE_MODE");
-    if (!m->pk || !c->plan || c->persist_broken || steps <= 0 || !mode || strcmp(mode, "persistent") != 0)
-        return TMG_OK;
-    PersistArgs a{};
-    a.plan = c->plan;
-    a.L = m->L;
-    a.V = m->V;
-    a.nq = m->nq;
-    a.nkv = m->nkv;
-    a.nsplit = c->attn_nsplit;
-    a.fused_merge = c->attn_nsplit == 1 || fused_merge(m, c);
-    a.nparts = m->argmax_nparts;
-    a.attn_out = m->attn_out;
-    a.part = m->attn_part;
-    a.part_ml = m->attn_ml;
-    a.argmax_part = m->argmax_part;
-    a.st = c->st;
-    a.history = c->history;
-    a.hist_cap = (int)c->max_pos + 2;
-    a.bar = c->bar;
-    a.steps = steps;
-    // TMG_PERSIST_TRACE=1: per-barrier timestamps of workgroup 0, summarized
-    // on stderr after the launch (diagnostics only)
-    const char *tr = getenv("TMG_PERSIST_TRACE");
-    unsigned long long *trace = nullptr;
-    const int per_step = 5 * m->L + 2 + (a.fused_merge ? 0 : m->L);
-    const size_t nrec = 2 * (size_t)per_step * steps + 2;
-    if (tr && tr[0] == '1') {
-        TMG_HIP(hipMalloc(&trace, nrec * 8));
-        TMG_HIP(hipMemsetAsync(trace, 0, nrec * 8, m->stream));
-    }
-    a.trace = trace;
-    TMG_HIP(launch_persistent(m->pk, m->pk_grid, a, m->stream));
-    *used = true;
-    if (trace) {
-        std::vector<unsigned long long> t(nrec);
-        TMG_HIP(hipMemcpyAsync(t.data(), trace, nrec * 8, hipMemcpyDeviceToHost, m->stream));
-        TMG_HIP(hipStreamSynchronize(m->stream));
-        (void)hipFree(trace);
-        // phase k of a step: work = arrive[k] - leave[k-1]; wait = leave[k] - arrive[k]
-        const char *names[] = {"qkv", "attn", "o_proj", "gate_up", "down"};
-        std::vector<double> work(per_step, 0.0), wait(per_step, 0.0);
-        for (int s = 0; s < steps; s++)
-            for (int k = 0; k < per_step; k++) {
-                const size_t i = (size_t)s * per_step + k;
-                const unsigned long long prev = i == 0 ? t[0] : t[1 + 2 * (i - 1) + 1];
-                work[k] += (double)(t[1 + 2 * i] - prev) * 0.01;
-                wait[k] += (double)(t[1 + 2 * i + 1] - t[1 + 2 * i]) * 0.01;
-            }
-        double tw[5] = {0}, tt[5] = {0};
-        for (int k = 0; k < 5 * m->L; k++) {
-            tw[k % 5] += work[k] / steps;
-            tt[k % 5] += wait[k] / steps;
-        }
-        fprintf(stderr, "[tmg trace] per step (us, workgroup 0): ");
-        for (int i = 0; i < 5; i++) fprintf(stderr, "%s work %.1f wait %.1f | ", names[i], tw[i], tt[i]);
-        fprintf(stderr, "lm_head work %.1f wait %.1f | final work %.1f wait %.1f\n", work[per_step - 2] / steps,
-                wait[per_step - 2] / steps, work[per_step - 1] / steps, wait[per_step - 1] / steps);
-    }
-    return TMG_OK;
-}
-
-// After a persistent launch has completed: a timed-out barrier is an error,
-// and the cache falls back to the graph path from then on.
-int check_persistent(tmg_model *m, tmg_cache *c) {
-    unsigned err = 0;
-    TMG_HIP(hipMemcpy(&err, &c->bar->err, sizeof(err), hipMemcpyDeviceToHost));
-    if (err) {
-        c->persist_broken = true;
-        return set_error(TMG_E_DEVICE, "persistent decode: a grid barrier timed out; this cache now uses the "
-                                       "per-kernel path");
-    }
     return TMG_OK;
 }
 
@@ -953,7 +774,14 @@ extern "C" int tmg_model_load(const char *path, int device, tmg_model **out) {
     return TMG_OK;
 }
 
-extern "C" void tmg_model_free(tmg_model *m) { model_release(m); }
+extern "C" void tmg_model_free(tmg_model *m) {
+    if (!m) return;
+    if (m->live_caches > 0) {
+        m->free_requested = true;  // released by the last tmg_cache_free
+        return;
+    }
+    model_release(m);
+}
 
 extern "C" int tmg_model_config(const tmg_model *m, tmg_config *out) {
     if (!m || !out) return set_error(TMG_E_INVALID, "null argument");
@@ -966,8 +794,10 @@ extern "C" int tmg_cache_new(tmg_model *m, uint32_t max_pos, tmg_cache **out) {
     if (!m || !out || max_pos == 0) return set_error(TMG_E_INVALID, "bad argument to tmg_cache_new");
     *out = nullptr;
     (void)hipSetDevice(m->device);
+    if (m->free_requested) return set_error(TMG_E_INVALID, "model handle already freed");
     tmg_cache *c = new tmg_cache();
     c->model = m;
+    m->live_caches++;
     c->max_pos = max_pos;
     c->attn_nsplit = (int)std::min<uint32_t>(kMaxSplits, (max_pos + kAttnBlock - 1) / kAttnBlock);
     const size_t n = (size_t)m->L * max_pos * m->kvd;
@@ -1007,15 +837,6 @@ extern "C" int tmg_cache_new(tmg_model *m, uint32_t max_pos, tmg_cache **out) {
             rc = set_error(TMG_E_DEVICE, "state upload failed");
     }
     if (!rc) rc = ensure_rope(m, (int)max_pos + 1);
-    if (!rc && m->pk) {
-        void *bar = nullptr, *plan = nullptr;
-        if (hipMalloc(&bar, sizeof(GridBar)) != hipSuccess || hipMalloc(&plan, sizeof(PersistPlan)) != hipSuccess ||
-            hipMemset(bar, 0, sizeof(GridBar)) != hipSuccess)
-            rc = set_error(TMG_E_NOMEM, "persistent decode buffers");
-        c->bar = (GridBar *)bar;
-        c->plan = (PersistPlan *)plan;
-        if (!rc) rc = build_plan(m, c);
-    }
     if (!rc) rc = set_state(m, c, 0, true);
     if (!rc && hipStreamSynchronize(m->stream) != hipSuccess) rc = set_error(TMG_E_DEVICE, "stream sync failed");
     if (rc) {
@@ -1038,13 +859,13 @@ extern "C" void tmg_cache_free(tmg_cache *c) {
     (void)hipFree(c->cand);
     (void)hipFree(c->gsc);
     (void)hipFree(c->draws);
-    (void)hipFree(c->bar);
-    (void)hipFree(c->plan);
     (void)hipFree(c->k);
     (void)hipFree(c->v);
     (void)hipFree(c->st);
     (void)hipHostFree(c->history);
+    tmg_model *m = c->model;
     delete c;
+    if (--m->live_caches == 0 && m->free_requested) model_release(m);
 }
 
 extern "C" int tmg_cache_len(const tmg_cache *c, uint32_t layer, uint32_t *len) {
@@ -1095,12 +916,9 @@ extern "C" int tmg_forward_token(tmg_model *m, tmg_cache *c, uint32_t token, flo
     (void)hipSetDevice(m->device);
     int rc;
     if ((rc = set_state(m, c, (int)token, false))) return rc;
-    bool used = false;
-    if ((rc = enqueue_persistent(m, c, 1, &used))) return rc;
-    if (!used && (rc = launch_step(m, c, SEL_ARGMAX))) return rc;
+    if ((rc = launch_step(m, c, SEL_ARGMAX))) return rc;
     c->len += 1;
-    if ((rc = fetch_logits(m, logits))) return rc;
-    return used ? check_persistent(m, c) : TMG_OK;
+    return fetch_logits(m, logits);
 }
 
 extern "C" int tmg_forward_seq(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n, float *last_logits) {
@@ -1171,30 +989,21 @@ extern "C" int tmg_decode_greedy(tmg_model *m, tmg_cache *c, uint32_t token, uin
     if ((uint64_t)c->len + n_steps > c->max_pos) return set_error(TMG_E_CAPACITY, "KV cache full");
     (void)hipSetDevice(m->device);
     int rc;
-    const bool eager = !step_graphs_enabled();
     if ((rc = set_state(m, c, (int)token, true))) return rc;
-    hipEvent_t e0, e1;
-    TMG_HIP(hipEventCreate(&e0));
-    TMG_HIP(hipEventCreate(&e1));
-    TMG_HIP(hipEventRecord(e0, m->stream));
-    bool used = false;
-    if (!eager && (rc = enqueue_persistent(m, c, (int)n_steps, &used))) return rc;
-    if (!used) {
-        for (uint32_t i = 0; i < n_steps; i++)
-            if ((rc = launch_step(m, c, SEL_ARGMAX))) return rc;
-    }
-    TMG_HIP(hipEventRecord(e1, m->stream));
-    TMG_HIP(hipEventSynchronize(e1));
+    // the step graph is captured before the first timing event
+    if (step_graphs_enabled() && (rc = get_step_graph(m, c, SEL_ARGMAX))) return rc;
+    EventPair ev;
+    TMG_HIP(ev.create());
+    TMG_HIP(hipEventRecord(ev.e0, m->stream));
+    for (uint32_t i = 0; i < n_steps; i++)
+        if ((rc = launch_step(m, c, SEL_ARGMAX))) return rc;
+    TMG_HIP(hipEventRecord(ev.e1, m->stream));
+    TMG_HIP(hipEventSynchronize(ev.e1));
     float el = 0.f;
-    TMG_HIP(hipEventElapsedTime(&el, e0, e1));
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
+    TMG_HIP(hipEventElapsedTime(&el, ev.e0, ev.e1));
     c->len += n_steps;
     if (ms) *ms = el;
-    if (used && (rc = check_persistent(m, c))) return rc;
-    if (tokens_out && n_steps) {
-        memcpy(tokens_out, (const void *)c->history, (size_t)n_steps * 4);
-    }
+    if (tokens_out && n_steps) memcpy(tokens_out, (const void *)c->history, (size_t)n_steps * 4);
     return TMG_OK;
 }
 
@@ -1217,9 +1026,9 @@ extern "C" int tmg_profile_decode_step(tmg_model *m, tmg_cache *c, uint32_t toke
     // to back between two events (kernels abut as in the step graph)
     constexpr int kReps = 8;
     size_t nrec = 0;
-    hipEvent_t e0, e1;
-    TMG_HIP(hipEventCreate(&e0));
-    TMG_HIP(hipEventCreate(&e1));
+    EventPair ev;
+    TMG_HIP(ev.create());
+    hipEvent_t e0 = ev.e0, e1 = ev.e1;
     // TMG_DECODE_GRAPH=0: the same launches enqueued one by one (profilers
     // that do not follow graph launches)
     const bool use_graph = step_graphs_enabled();
@@ -1250,12 +1059,19 @@ extern "C" int tmg_profile_decode_step(tmg_model *m, tmg_cache *c, uint32_t toke
             rc = enqueue();
             hipGraph_t g = nullptr;
             hipError_t e = hipStreamEndCapture(m->stream, &g);
+            if (!rc && e == hipSuccess) e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+            if (g) (void)hipGraphDestroy(g);
             if (rc) break;
             TMG_HIP(e);
-            e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
-            (void)hipGraphDestroy(g);
-            TMG_HIP(e);
         }
+        // destroys the replay graph on every path out of this iteration
+        struct ExecGuard {
+            hipGraphExec_t &x;
+            ~ExecGuard() {
+                if (x) (void)hipGraphExecDestroy(x);
+                x = nullptr;
+            }
+        } guard{ex};
         auto replay = [&]() -> int {
             if (use_graph)
                 return hipGraphLaunch(ex, m->stream) == hipSuccess ? TMG_OK
@@ -1270,7 +1086,6 @@ extern "C" int tmg_profile_decode_step(tmg_model *m, tmg_cache *c, uint32_t toke
             TMG_HIP(hipEventSynchronize(e1));
             TMG_HIP(hipEventElapsedTime(&el, e0, e1));
         }
-        if (ex) (void)hipGraphExecDestroy(ex);
         if (rc) break;
         if (nrec < cap && records) {
             tmg_kernel_record r{};
@@ -1282,8 +1097,6 @@ extern "C" int tmg_profile_decode_step(tmg_model *m, tmg_cache *c, uint32_t toke
         }
         nrec++;
     }
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
     // the replays touched only scratch, the KV row at the current position
     // (rewritten by the next step) and the step state, restored here
     if (!rc) rc = set_state(m, c, (int)token, true);

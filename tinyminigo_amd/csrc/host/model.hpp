@@ -60,15 +60,17 @@ struct tmg_model {
     int kv_cap = 0;
     uint16_t *pf_kh = nullptr, *pf_kl = nullptr, *pf_vth = nullptr, *pf_vtl = nullptr;
 
-    // persistent decode kernel for this model's shape (null: graph path only)
-    const void *pk = nullptr;
-    int pk_grid = 0;
-
     // pinned host staging
     void *pin = nullptr;
     size_t pin_bytes = 0;
 
     std::vector<void *> allocs;
+
+    // Caches created on this model and not yet freed.  tmg_model_free with
+    // live caches only marks the model; the last tmg_cache_free releases it
+    // (a cache uses the model's stream, device and weights until it is freed).
+    int live_caches = 0;
+    bool free_requested = false;
 };
 
 struct tmg_cache {
@@ -87,9 +89,6 @@ struct tmg_cache {
     float *draws = nullptr;              // [max_pos + 2] uniform draw per step (sampling)
     float *gsc = nullptr;                // kSampleScratchBytes(V) of the whole-vocabulary sampler
     int samp_use_k = 0, samp_use_p = 0;  // the running generate call's top-k / nucleus
-    tmg::GridBar *bar = nullptr;       // persistent-kernel barrier counters
-    tmg::PersistPlan *plan = nullptr;  // persistent-kernel argument blocks
-    bool persist_broken = false;       // a barrier timed out: use the graph path
     // one captured step graph per token-selection mode (tmg::SelectMode)
     hipGraphExec_t graphs[4] = {nullptr, nullptr, nullptr, nullptr};
     hipGraph_t graph_src[4] = {nullptr, nullptr, nullptr, nullptr};
@@ -118,6 +117,19 @@ struct LaunchRecorder {
 };
 
 // How a step turns logits into the next token.
+// Two timing events, destroyed on every return path.
+struct EventPair {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t create() {
+        hipError_t e = hipEventCreate(&e0);
+        return e == hipSuccess ? hipEventCreate(&e1) : e;
+    }
+    ~EventPair() {
+        if (e0) (void)hipEventDestroy(e0);
+        if (e1) (void)hipEventDestroy(e1);
+    }
+};
+
 enum SelectMode {
     SEL_ARGMAX = 0,          // greedy, argmax fused into the lm_head GEMV
     SEL_PENALTY_ARGMAX = 1,  // greedy after the repetition penalty
@@ -136,9 +148,5 @@ int set_state(tmg_model *m, tmg_cache *c, int token, bool reset_step);
 int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n);
 int ensure_rope(tmg_model *m, int npos);
 int pinned(tmg_model *m, size_t bytes);
-// Greedy decode steps in one persistent launch when the model and cache
-// allow it (*used = false otherwise, nothing enqueued).
-int enqueue_persistent(tmg_model *m, tmg_cache *c, int steps, bool *used);
-int check_persistent(tmg_model *m, tmg_cache *c);
 
 }  // namespace tmg

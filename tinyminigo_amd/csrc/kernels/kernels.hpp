@@ -225,9 +225,8 @@ inline size_t skinny_counters(int max_m) { return (size_t)((max_m + 63) / 64) * 
 // Copy row `row` of x[T,H] to dst[H] (last prefill row -> decode residual).
 hipError_t launch_copy_row(const float *x, int row, int H, float *dst, hipStream_t s);
 
-// ---- persistent decode ------------------------------------------------------
+// ---- decode attention -------------------------------------------------------
 
-constexpr int kBarGroups = 8;  // arrival groups of the grid barrier
 // Decode attention with at most this many splits is merged in the o_proj
 // GEMV prologue; with more, by attn_combine_kernel.
 constexpr int kFusedSplits = 8;
@@ -239,49 +238,6 @@ constexpr int kAttnBlock = 64;
 // others read it first, so a long cache at a short context does not stream
 // the blocks of its inactive splits.
 constexpr int kSpecSplits = 8;
-
-// Grid-barrier counters, each on its own 128-byte line.  Zeroed once at cache
-// creation; the counters only grow and each launch records where the next
-// one starts.
-struct GridBar {
-    unsigned top[32];
-    unsigned sub[kBarGroups][32];
-    unsigned err;  // set when a barrier wait timed out
-    unsigned base_top;
-    unsigned base_sub[kBarGroups];
-};
-
-// Per-cache launch plan of the persistent decode kernel, built on the host
-// and kept in device memory so the kernel reads argument blocks through the
-// scalar cache instead of holding them in registers.
-constexpr int kMaxPlanLayers = 64;
-struct PersistPlan {
-    GemvArgs qkv[kMaxPlanLayers];   // PRO_EMBED_NORM (layer 0) / PRO_NORM, EPI_QKV
-    GemvArgs o[kMaxPlanLayers];     // PRO_ATTN_COMBINE or PRO_PLAIN, EPI_RESID
-    GemvArgs gu[kMaxPlanLayers];    // PRO_NORM, EPI_SWIGLU
-    GemvArgs down[kMaxPlanLayers];  // PRO_PLAIN, EPI_RESID
-    AttnArgs attn[kMaxPlanLayers];  // decode attention, partials only
-    GemvArgs lm;                    // PRO_NORM, EPI_LOGITS
-};
-
-struct PersistArgs {
-    const PersistPlan *plan;
-    int L, V, nq, nkv, nsplit, fused_merge, nparts;
-    float *attn_out, *part, *part_ml;  // split merge (when not fused)
-    const unsigned long long *argmax_part;
-    DevState *st;
-    int *history;
-    int hist_cap;
-    GridBar *bar;
-    int steps;  // decode steps run by this launch
-    // optional: workgroup 0 records the 100 MHz realtime clock when it
-    // arrives at and leaves every grid barrier ([2k], [2k+1]); null = off
-    unsigned long long *trace;
-};
-
-// The persistent kernel instantiated for these dims, or null.
-const void *persistent_kernel(int kc_h, int kc_q, int kc_i, int hd, int group);
-hipError_t launch_persistent(const void *kernel, int grid, const PersistArgs &a, hipStream_t s);
 
 // ---- sampling --------------------------------------------------------------
 

@@ -12,7 +12,8 @@ import ctypes as C
 
 import numpy as np
 
-from . import _lib  # noqa: F401  (libtmg.so first, so the soname below is the one it loaded)
+from . import _lib  # libtmg.so first, so the soname below is the one it loaded
+from ._lib import finalizing, register
 
 _hip = C.CDLL("libamdhip64.so.7")
 _hip.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
@@ -63,6 +64,7 @@ class DeviceBuffer:
         self.nbytes = nbytes
         self.ptr = C.c_void_p()
         _ok(_hip.hipMalloc(C.byref(self.ptr), max(nbytes, 1)), "hipMalloc")
+        register(self, 2)
 
     @classmethod
     def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
@@ -83,10 +85,14 @@ class DeviceBuffer:
     def fill_byte(self, v: int) -> None:
         _ok(_hip.hipMemset(self.ptr, v, self.nbytes), "hipMemset")
 
-    def __del__(self):
+    def close(self) -> None:
         if getattr(self, "ptr", None) is not None and self.ptr.value:
             _hip.hipFree(self.ptr)
             self.ptr = C.c_void_p()
+
+    def __del__(self):
+        if not finalizing():
+            self.close()
 
 
 def copy_device(dst: "DeviceBuffer", src: "DeviceBuffer", nbytes: int) -> None:
@@ -99,6 +105,7 @@ class Stream:
     def __init__(self):
         self.ptr = C.c_void_p()
         _ok(_hip.hipStreamCreate(C.byref(self.ptr)), "hipStreamCreate")
+        register(self, 4)
 
     @property
     def addr(self) -> int:
@@ -107,10 +114,15 @@ class Stream:
     def synchronize(self) -> None:
         _ok(_hip.hipStreamSynchronize(self.ptr), "hipStreamSynchronize")
 
-    def __del__(self):
+    def close(self) -> None:
         if getattr(self, "ptr", None) is not None and self.ptr.value:
+            _hip.hipStreamSynchronize(self.ptr)
             _hip.hipStreamDestroy(self.ptr)
             self.ptr = C.c_void_p()
+
+    def __del__(self):
+        if not finalizing():
+            self.close()
 
 
 class Graph:
@@ -128,14 +140,20 @@ class Graph:
         rc = _hip.hipGraphInstantiate(C.byref(self.exec), g, None, None, 0)
         _hip.hipGraphDestroy(g)
         _ok(rc, "hipGraphInstantiate")
+        register(self, 0)
 
     def launch(self) -> None:
         _ok(_hip.hipGraphLaunch(self.exec, self.stream.ptr), "hipGraphLaunch")
 
-    def __del__(self):
+    def close(self) -> None:
         if getattr(self, "exec", None) is not None and self.exec.value:
+            _hip.hipStreamSynchronize(self.stream.ptr)
             _hip.hipGraphExecDestroy(self.exec)
             self.exec = C.c_void_p()
+
+    def __del__(self):
+        if not finalizing():
+            self.close()
 
 
 class Timer:
@@ -146,6 +164,7 @@ class Timer:
         self.a, self.b = C.c_void_p(), C.c_void_p()
         _ok(_hip.hipEventCreate(C.byref(self.a)), "hipEventCreate")
         _ok(_hip.hipEventCreate(C.byref(self.b)), "hipEventCreate")
+        register(self, 0)
 
     def start(self):
         _ok(_hip.hipEventRecord(self.a, self.s), "hipEventRecord")
@@ -157,7 +176,12 @@ class Timer:
         _ok(_hip.hipEventElapsedTime(C.byref(ms), self.a, self.b), "hipEventElapsedTime")
         return ms.value
 
-    def __del__(self):
+    def close(self) -> None:
         for e in (self.a, self.b):
             if e.value:
                 _hip.hipEventDestroy(e)
+                e.value = None
+
+    def __del__(self):
+        if not finalizing():
+            self.close()

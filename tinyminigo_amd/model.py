@@ -14,8 +14,11 @@ from typing import Callable, List, Optional, Sequence
 
 import numpy as np
 
+import weakref
+
 from ._lib import (
-    ON_TOKEN, TmgError, check, lib, tmg_config, tmg_gen_params, tmg_kernel_record, tmg_synth_spec,
+    ON_TOKEN, TmgError, check, finalizing, lib, register, tmg_config, tmg_gen_params, tmg_kernel_record,
+    tmg_synth_spec,
 )
 
 __all__ = [
@@ -81,6 +84,8 @@ class Model:
 
     def __init__(self, handle: C.c_void_p):
         self._h = handle
+        self._caches = weakref.WeakSet()
+        register(self, 3)
         c = tmg_config()
         check(lib.tmg_model_config(self._h, C.byref(c)))
         self.config = ModelConfig._from_c(c)
@@ -93,11 +98,16 @@ class Model:
         return cls(h)
 
     def close(self) -> None:
+        """Free the model and every cache made on it (tmg_model_free)."""
+        for cache in list(self._caches):
+            cache.close()
         if self._h:
             lib.tmg_model_free(self._h)
             self._h = None
 
     def __del__(self):
+        if finalizing():
+            return
         try:
             self.close()
         except Exception:
@@ -153,9 +163,12 @@ class KvCache:
     def __init__(self, model: Model, max_pos: int):
         self.model = model
         self.max_pos = max_pos
+        self._h = None
         h = C.c_void_p()
         check(lib.tmg_cache_new(model._h, int(max_pos), C.byref(h)))
         self._h = h
+        model._caches.add(self)
+        register(self, 1)
 
     def close(self) -> None:
         if self._h:
@@ -163,6 +176,8 @@ class KvCache:
             self._h = None
 
     def __del__(self):
+        if finalizing():
+            return
         try:
             self.close()
         except Exception:
