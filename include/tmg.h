@@ -175,6 +175,15 @@ int tmg_stdrng_uniform(uint64_t seed, size_t n, float *out);
 int tmg_gemv_bf16(const uint16_t *w_dev, const float *x_dev, float *y_dev, uint32_t out, uint32_t in,
                   void *stream);
 
+/* Kernel level: tensor::argmax (src/tensor.rs:1063-1073) of x[0, n), a DEVICE
+ * f32 vector, written to *out_dev (a DEVICE uint32): the index of the first
+ * maximum.  NaN entries are skipped, -0.0 and +0.0 count as equal, and the
+ * result is 0 when every entry is -inf or NaN or n is 0 -- the reference's
+ * `v > best_val` scan from (0, -inf).  Two passes on `stream` (NULL = the
+ * default stream); the per-4096-element chunk keys of the first pass live in
+ * a buffer allocated and freed on that stream for the call. */
+int tmg_argmax_f32(const float *x_dev, uint32_t n, uint32_t *out_dev, void *stream);
+
 /* Kernel level, int8 weight-only mode (TMG_I8=1): y[out] = the reference's
  * matmul_w_into over WMat::I8 (src/tensor.rs:341-364): x is quantized with
  * one symmetric scale (quantize_row_i8, src/tensor.rs:125-139), each row dot

@@ -152,6 +152,20 @@ def test_argmax_basic_and_ties():
     assert O.argmax([np.nan, 1.0, np.nan]) == 1
 
 
+def test_argmax_edge_values():
+    # `v > best` from (0, -inf) (src/tensor.rs:1063-1073): -0.0 == +0.0, so
+    # the first zero wins; +inf is taken once; NaN never; empty -> 0
+    assert O.argmax([-0.0, 0.0]) == 0
+    assert O.argmax([0.0, -0.0]) == 0
+    assert O.argmax([-1.0, -0.0, 0.0]) == 1
+    assert O.argmax([1.0, np.inf, np.inf]) == 1
+    assert O.argmax([np.nan, np.inf]) == 1
+    assert O.argmax([np.nan, -np.inf, np.nan]) == 0
+    assert O.argmax([-np.inf, -3.0, -np.inf]) == 1
+    assert O.argmax([]) == 0
+    assert O.argmax([1e-45, 0.0]) == 0 and O.argmax([0.0, 1e-45]) == 1
+
+
 def test_attention_row_shapes():
     q = [1.0, 0.0]
     keys = [1.0, 0.0, 0.0, 1.0]

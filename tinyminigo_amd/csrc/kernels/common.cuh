@@ -199,8 +199,11 @@ __device__ __forceinline__ uint32_t f32_order(float v) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Argmax key of a non-NaN value: -0.0 and +0.0 share one key, since the
+// reference's `v > best` treats them as equal (the first one wins).
 __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
-    return ((unsigned long long)f32_order(v) << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
+    const uint32_t o = v == 0.0f ? 0x80000000u : f32_order(v);
+    return ((unsigned long long)o << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
 }
 
 __device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int off) {

@@ -74,6 +74,11 @@ struct GemvArgs {
 };
 
 hipError_t launch_gemv(int pro, int epi, const GemvArgs &a, hipStream_t s);
+
+// argmax of x[0, n) into *out (argmax.hip): argmax_parts(n) chunk keys in
+// `part`, then one reduction.
+uint32_t argmax_parts(uint32_t n);
+hipError_t launch_argmax(const float *x, uint32_t n, uint32_t *out, unsigned long long *part, hipStream_t s);
 // The decode GEMV over a.nb <= kMtMaxSeq activation rows at once (batched
 // decode of several sequences): every weight row is read once and dotted
 // with all rows.  PRO_NORM or PRO_PLAIN; EPI_QKV, EPI_RESID, EPI_SWIGLU or

@@ -23,6 +23,7 @@ from ._lib import (
 
 __all__ = [
     "ModelConfig", "Model", "KvCache", "GenParams", "GenOutput", "generate", "gemv_bf16", "gemv_i8", "quantize_i8", "repack_tmb",
+    "argmax_f32",
     "generate_batch",
     "synth_model", "synth_tokens", "synth_normal_bf16", "synth_normal_f32", "TmgError",
 ]
@@ -272,6 +273,12 @@ def gemv_bf16(w_dev: int, x_dev: int, y_dev: int, out: int, in_: int, stream: in
     """tensor::matmul_w (src/tensor.rs:315-338) on device pointers."""
     check(lib.tmg_gemv_bf16(C.c_void_p(w_dev), C.c_void_p(x_dev), C.c_void_p(y_dev), out, in_,
                             C.c_void_p(stream)))
+
+
+def argmax_f32(x_dev: int, n: int, out_dev: int, stream: int = 0) -> None:
+    """tensor::argmax (src/tensor.rs:1063-1073) of n device floats into a
+    device uint32."""
+    check(lib.tmg_argmax_f32(C.c_void_p(x_dev), int(n), C.c_void_p(out_dev), C.c_void_p(stream)))
 
 
 def generate_batch(model: Model, prompts: Sequence[Sequence[int]], max_tokens: int):
