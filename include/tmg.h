@@ -184,6 +184,17 @@ int tmg_gemv_bf16(const uint16_t *w_dev, const float *x_dev, float *y_dev, uint3
  * a buffer allocated and freed on that stream for the call. */
 int tmg_argmax_f32(const float *x_dev, uint32_t n, uint32_t *out_dev, void *stream);
 
+/* tmg_argmax_f32 for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  Same arguments and result; no hipMalloc,
+ * hipFree or allocating call is made: the chunk keys live in a fixed 32 KiB
+ * array per GPU, held until the process ends, so n is limited to
+ * 16,777,216 elements (larger n: TMG_E_INVALID, nothing launched).  The
+ * current device must be the stream's device.  Calls that overlap on one GPU
+ * (on different streams, or from different threads) share that array and
+ * race; calls in one stream order are safe. */
+int tmg_argmax_f32_noalloc(const float *x_dev, uint32_t n, uint32_t *out_dev, void *stream);
+
 /* Kernel level, int8 weight-only mode (TMG_I8=1): y[out] = the reference's
  * matmul_w_into over WMat::I8 (src/tensor.rs:341-364): x is quantized with
  * one symmetric scale (quantize_row_i8, src/tensor.rs:125-139), each row dot

@@ -121,6 +121,7 @@ SIGNATURES = {
     "tmg_tmb_config": (C.c_int, [C.c_char_p, C.POINTER(tmg_config)]),
     "tmg_gemv_bf16": (C.c_int, [P, P, P, C.c_uint32, C.c_uint32, P]),
     "tmg_argmax_f32": (C.c_int, [P, C.c_uint32, P, P]),
+    "tmg_argmax_f32_noalloc": (C.c_int, [P, C.c_uint32, P, P]),
     "tmg_stdrng_uniform": (C.c_int, [C.c_uint64, C.c_size_t, PF]),
     "tmg_gemv_i8": (C.c_int, [P, P, P, P, C.c_uint32, C.c_uint32, P]),
     "tmg_quantize_i8": (C.c_int, [P, C.c_uint32, C.c_uint32, P, P, P]),

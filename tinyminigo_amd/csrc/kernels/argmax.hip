@@ -11,6 +11,7 @@
 // key (common.cuh).
 #include <hip/hip_runtime.h>
 
+#include <mutex>
 #include <string>
 
 #include "../host/common.hpp"
@@ -68,6 +69,11 @@ __global__ __launch_bounds__(kBlock) void argmax_final_kernel(const unsigned lon
 
 }  // namespace
 
+// Chunk keys of tmg_argmax_f32_noalloc: one array per GPU, held until the
+// process ends (32 KiB: 4096 keys cover n <= 4096 * 4096 = 16,777,216).
+constexpr uint32_t kNoAllocParts = 4096;
+static __device__ __align__(256) unsigned long long scratch[kNoAllocParts];
+
 uint32_t argmax_parts(uint32_t n) { return (uint32_t)(((uint64_t)n + kArgmaxChunk - 1) / kArgmaxChunk); }
 
 hipError_t launch_argmax(const float *x, uint32_t n, uint32_t *out, unsigned long long *part, hipStream_t s) {
@@ -101,5 +107,48 @@ extern "C" int tmg_argmax_f32(const float *x_dev, uint32_t n, uint32_t *out_dev,
         if (e == hipSuccess) e = f;
     }
     if (e != hipSuccess) return set_error(TMG_E_DEVICE, std::string("tmg_argmax_f32: ") + hipGetErrorString(e));
+    return TMG_OK;
+}
+
+// tmg_argmax_f32 without any allocation: the chunk keys go to this GPU's
+// `scratch` array.  Its device address is looked up once per device, with
+// that device current, on the first call there (host code never passes the
+// array's name itself: on the host it is only a stand-in symbol).
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned long long *g_scratch[kMaxDevices] = {};
+
+int noalloc_scratch(unsigned long long **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(TMG_E_DEVICE, std::string("hipGetDevice: ") + hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return set_error(TMG_E_DEVICE, "device index beyond the no-alloc table");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_error(TMG_E_DEVICE, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+        g_scratch[dev] = (unsigned long long *)p;
+    }
+    *out = g_scratch[dev];
+    return TMG_OK;
+}
+}  // namespace
+
+extern "C" int tmg_argmax_f32_noalloc(const float *x_dev, uint32_t n, uint32_t *out_dev, void *stream) {
+    clear_error();
+    if (!out_dev || (n && !x_dev)) return set_error(TMG_E_INVALID, "null argument to tmg_argmax_f32_noalloc");
+    if (argmax_parts(n) > kNoAllocParts)
+        return set_error(TMG_E_INVALID, "tmg_argmax_f32_noalloc: n = " + std::to_string(n) + " exceeds its maximum of " +
+                                            std::to_string((uint64_t)kNoAllocParts * kArgmaxChunk) + " elements");
+    unsigned long long *part = nullptr;
+    int rc = noalloc_scratch(&part);
+    if (rc) return rc;
+    // every key the final pass reads is written by this call's first pass,
+    // so the array needs no clearing between calls
+    const hipError_t e = launch_argmax(x_dev, n, out_dev, part, (hipStream_t)stream);
+    if (e != hipSuccess) return set_error(TMG_E_DEVICE, std::string("tmg_argmax_f32_noalloc: ") + hipGetErrorString(e));
     return TMG_OK;
 }
