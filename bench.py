@@ -113,6 +113,8 @@ def gemv_sweep(T):
     MALL-hot: the same number of launches on one copy.  Bytes per launch =
     2*out*in + 4*in + 4*out; each figure is the per-launch average over
     graph replays (HIP events on the launch stream)."""
+    import numpy as np
+
     from tinyminigo_amd import hip as H
     stream = H.Stream()
     res = []
@@ -129,6 +131,14 @@ def gemv_sweep(T):
         H.synchronize()
         nbytes = 2 * out * inp + 4 * inp + 4 * out
         row = {"shape": f"{out}x{inp}", "bytes": nbytes, "copies": ncopy}
+        # max-abs error of the device result against the oracle's matmul_w
+        # (the reference's 8-lane dot order), computed before any timing
+        from oracle import oracle as O
+        T.gemv_bf16(w0.addr, xd.addr, yd.addr, out, inp, stream.addr)
+        stream.synchronize()
+        y = yd.to_array(np.float32, out)
+        ref = O.matmul_w(x, w, out, inp)
+        row["max_abs_err"] = float(np.abs(y.astype(np.float64) - ref.astype(np.float64)).max())
         for kind, pick in (("cold", lambda i: ws[i]), ("hot", lambda i: w0)):
             g = H.Graph(stream, lambda st: [T.gemv_bf16(pick(i).addr, xd.addr, yd.addr, out, inp, st.addr)
                                             for i in range(ncopy)])
@@ -146,7 +156,7 @@ def gemv_sweep(T):
         res.append(row)
         del ws, w0, xd, yd
         log(f"gemv {out}x{inp}: cold {row['cold_us']} us ({row['cold_GB_s']} GB/s), "
-            f"hot {row['hot_us']} us ({row['hot_GB_s']} GB/s)")
+            f"hot {row['hot_us']} us ({row['hot_GB_s']} GB/s), max abs err vs oracle {row['max_abs_err']:.2e}")
     return res
 
 
@@ -170,6 +180,93 @@ def pmc_traffic(kernel, weights="bf16"):
 
 
 SAMPLED = dict(temperature=0.8, top_k=50, top_p=0.9, repetition_penalty=1.1, seed=42)
+
+
+def kernel_table(m, cache, tok, reps=3):
+    """Per-kernel-kind timing of one decode step at the cache's position:
+    {name: (launches per step, algorithmic bytes per launch, ms per launch)}."""
+    import numpy as np
+    per = {}
+    for _ in range(reps):
+        for name, nbytes, ms, launches in m.profile_decode_step(tok, cache):
+            per.setdefault(name, [launches, nbytes, []])[2].append(ms)
+    return {k: (v[0], v[1], float(np.median(v[2]))) for k, v in per.items()}
+
+
+def extra_long_context(T, W, m, sync):
+    """The long-context workload (C3) on the already loaded 1B model: an
+    8192-token prefill, then 128 greedy decode steps from the captured step
+    graph (warmed on the same cache, which is reset and refilled before the
+    timed steps).  Reports the step rate, the KV share of the step bytes and
+    the decode attention kernel's rate at that context."""
+    import numpy as np
+    wl = W.LONG_CTX
+    prompt = [int(t) for t in wl.prompt()]
+    P, K = wl.prompt_len, wl.gen_tokens
+    c = T.KvCache(m, P + K + 8)
+    sync()
+    t = time.perf_counter()
+    lg = m.forward_seq(prompt, c)
+    sync()
+    prefill_s = time.perf_counter() - t
+    first = int(np.argmax(lg))
+    m.decode_greedy(first, 4, c)
+    c.reset()
+    m.forward_seq(prompt, c, want_logits=False)
+    sync()
+    t = time.perf_counter()
+    toks, ev_ms = m.decode_greedy(first, K, c)
+    sync()
+    wall = time.perf_counter() - t
+    ms_step = wall * 1e3 / K
+    n_ctx = P + (K + 1) / 2.0
+    step_bytes = wl.decode_bytes(int(round(n_ctx)))
+    per = kernel_table(m, c, int(toks[-1]))
+    attn = per.get("attn_decode")
+    c.close()
+    log(f"8k: prefill {prefill_s * 1e3:.1f} ms, decode {ms_step:.4f} ms/step")
+    return {
+        "workload": f"{wl.name}: {P}-token prompt, batched prefill, {K} greedy decode steps",
+        "ms_per_step": round(ms_step, 4), "tok_s": round(K / wall, 1), "decode_ms_events": round(ev_ms, 3),
+        "step_hbm": {"bytes_per_token": step_bytes, "kv_bytes_per_token": wl.kv_bytes(int(round(n_ctx))),
+                     "n_ctx_avg": n_ctx, "frac": round(step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "attn_decode": ({"avg_us": round(attn[2] * 1e3, 2), "bytes_per_launch": attn[1],
+                         "GB_s": round(attn[1] / (attn[2] * 1e-3) / 1e9, 1)} if attn else None),
+        "prefill_ms": round(prefill_s * 1e3, 2), "prefill_tok_s": round(P / prefill_s, 1),
+        "prefill_tflops": round(wl.prefill_flops(P) / prefill_s / 1e12, 1),
+    }
+
+
+def extra_four_b(T, W, model_dir, sync):
+    """The 4B sampled workload (C4): 128-token prompt, 256 tokens with
+    T=0.8, top-k 50, top-p 0.9, penalty 1.1, seed 42 through generate (the
+    product path: device sampling, one id per step to the host), rate as the
+    reference's main.rs reports it, (n - 1) / (elapsed - prefill)."""
+    wl = W.FOUR_B
+    path = W.ensure_model(wl, model_dir)
+    m = T.Model.load(path)
+    prompt = [int(t) for t in wl.prompt()]
+    K = wl.gen_tokens
+    T.generate(m, prompt, T.GenParams(max_tokens=16, **SAMPLED))
+    sync()
+    t = time.perf_counter()
+    gen = T.generate(m, prompt, T.GenParams(max_tokens=K, **SAMPLED))
+    wall_all = time.perf_counter() - t
+    wall = wall_all - gen.prefill_secs
+    n = len(gen.tokens) - 1
+    ms_tok = wall * 1e3 / n
+    n_ctx = wl.prompt_len + (K + 1) / 2.0
+    step_bytes = wl.decode_bytes(int(round(n_ctx)))
+    m.close()
+    log(f"4b: {n / wall:.1f} tok/s through generate, {ms_tok:.4f} ms/token")
+    return {
+        "workload": f"{wl.name}: {wl.prompt_len}-token prompt, {K} sampled tokens (T=0.8, top-k 50, top-p 0.9, "
+                    f"penalty 1.1, seed 42) through generate",
+        "ms_per_token": round(ms_tok, 4), "tok_s": round(n / wall, 1),
+        "prefill_ms": round(gen.prefill_secs * 1e3, 2),
+        "step_hbm": {"bytes_per_token": step_bytes, "n_ctx_avg": n_ctx,
+                     "frac": round(step_bytes / (ms_tok * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+    }
 
 
 def bench_batch(args, T, W, wl, m, load_s):
@@ -219,6 +316,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true", help="skip the GEMV shape sweep")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the long-context (8192-token) and 4B sampled workloads reported beside the 1b line")
     ap.add_argument("--weights", choices=["bf16", "i8"], default="bf16",
                     help="i8: load with TMG_I8=1, the reference's int8 weight-only mode (per-row int8 q/k/v/o/"
                          "gate/up/down, BF16 lm_head); the CPU baseline then times the oracle's int8 path")
@@ -317,15 +416,14 @@ def main():
         logits = m.forward_seq(prompt, cache)
         toks = [int(np.argmax(logits))]
     else:
-        # warmup on its own cache, then the timed steps on a fresh one
+        # warmup on the timed cache itself (its step graph is captured there
+        # and kept across the reset), then the prompt again and the timed steps
         cache = T.KvCache(m, cap)
         logits = m.forward_seq(prompt, cache)
         first = int(np.argmax(logits))
-        if Wm:
-            wc = T.KvCache(m, P + Wm + 8)
-            m.forward_seq(prompt, wc, want_logits=False)
-            m.decode_greedy(first, Wm, wc)
-            wc.close()
+        m.decode_greedy(first, max(Wm, 1), cache)
+        cache.reset()
+        m.forward_seq(prompt, cache, want_logits=False)
         sync()
         t = time.perf_counter()
         toks, ev_ms = m.decode_greedy(first, K, cache)
@@ -358,12 +456,20 @@ def main():
 
     sweep = None if (args.no_sweep or args.workload != "1b" or i8) else gemv_sweep(T)
 
+    # the other two model workloads, reported beside the headline (1b line only)
+    extras = {}
+    if args.workload == "1b" and not i8 and not sampled and not args.no_extras:
+        extras["c3_long_context"] = extra_long_context(T, W, m, sync)
+
     cpu = None
     if not args.no_cpu:
         log("timing the CPU baseline")
         cpu = cpu_baseline(path, prompt, args.cpu_seconds, wl if args.workload == "8k" else None,
                            m if args.workload == "8k" else None, cache if args.workload == "8k" else None,
                            samp if sampled else None, i8)
+
+    if args.workload == "1b" and not i8 and not sampled and not args.no_extras:
+        extras["c4_four_b_sampled"] = extra_four_b(T, W, args.model_dir, sync)
 
     kind = (f"{K} sampled tokens (T={samp['temperature']:g}, top-k {samp['top_k']}, top-p {samp['top_p']:g}, "
              f"penalty {samp['repetition_penalty']:g}, seed {samp['seed']}) through generate"
@@ -406,6 +512,7 @@ def main():
                      "launches_per_step": n_launch},
         "kernels": kernels,
         "gemv_sweep": sweep,
+        **extras,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
