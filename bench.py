@@ -302,6 +302,34 @@ def bench_batch(args, T, W, wl, m, load_s):
     }), flush=True)
 
 
+def bench_prefill(args, T, wl, m, prompt, sync):
+    """Prefill only (no decode step, so no graph launch): the workload's
+    prompt through forward_seq on fresh caches, --prefill-reps times; the
+    line reports the median.  For profiling the prefill kernels."""
+    import numpy as np
+    P = len(prompt)
+    pf = []
+    for _ in range(max(1, args.prefill_reps)):
+        c = T.KvCache(m, P + 8)
+        sync()
+        t = time.perf_counter()
+        m.forward_seq(prompt, c, want_logits=False)
+        sync()
+        pf.append(time.perf_counter() - t)
+        c.close()
+    s = float(np.median(pf))
+    flops = wl.prefill_flops(P)
+    log(f"prefill {P} tokens: {s * 1e3:.2f} ms ({flops / s / 1e12:.1f} TFLOP/s algorithmic)")
+    print(json.dumps({
+        "metric": METRIC + " [prefill only]", "value": round(P / s, 1), "unit": "tok/s", "n_gpus": 1,
+        "steps": len(pf), "warmup": 0, "ms_per_step": round(s * 1e3, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{wl.name}: {P}-token prompt, batched prefill", "global_batch": 1, "seq_len": P,
+                   "parallelism": "none (1 GPU)"},
+        "prefill_tflops": round(flops / s / 1e12, 2), "prefill_flops": flops, "cpu_baseline": None,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -316,6 +344,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true", help="skip the GEMV shape sweep")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="time only the prefill of the workload's prompt (no decode, no graph launches)")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the long-context (8192-token) and 4B sampled workloads reported beside the 1b line")
     ap.add_argument("--weights", choices=["bf16", "i8"], default="bf16",
@@ -382,6 +412,8 @@ def main():
 
     if args.batch > 1:
         return bench_batch(args, T, W, wl, m, load_s)
+    if args.prefill_only:
+        return bench_prefill(args, T, wl, m, prompt, sync)
 
     # prefill tok/s: median over repetitions on fresh caches (one for 8k)
     pf = []
