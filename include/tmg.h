@@ -142,8 +142,9 @@ int tmg_prefill(tmg_model *model, tmg_cache *cache, const uint32_t *tokens, size
 /* generate (src/model.rs:614-663).  Tokens are written to out_tokens
  * (capacity out_cap >= max_tokens), their count to *n_out.  first_logits
  * (vocab_size floats) and prefill_secs may be NULL.  Sampling (temperature >
- * 0) runs on the GPU; its uniform draws are the reference's
- * StdRng::seed_from_u64(seed) stream (tmg_stdrng_uniform), one per step. */
+ * 0) runs on the GPU; its uniform draws are a restatement of the
+ * reference's StdRng::seed_from_u64(seed) stream (tmg_stdrng_uniform), one
+ * per step. */
 int tmg_generate(tmg_model *model, const uint32_t *prompt, size_t n_prompt, const tmg_gen_params *params,
                  tmg_on_token_fn on_token, void *user, uint32_t *out_tokens, size_t out_cap, size_t *n_out,
                  float *first_logits, float *prefill_secs);
@@ -162,10 +163,12 @@ int tmg_generate(tmg_model *model, const uint32_t *prompt, size_t n_prompt, cons
 int tmg_generate_batch(tmg_model *model, const uint32_t *const *prompts, const size_t *n_prompt, size_t n_seq,
                        uint32_t max_tokens, uint32_t *out_tokens, size_t *n_out, float *decode_ms);
 
-/* The first n draws generate samples with: StdRng::seed_from_u64(seed)
+/* The first n draws generate samples with, restating StdRng::seed_from_u64
  * (src/model.rs:629) followed by one StandardUniform f32 per call
- * (src/tensor.rs:1204), i.e. rand 0.10.2's ChaCha12 StdRng seeded through
- * rand_core's PCG32 expansion, (next_u32 >> 8) * 2^-24.  Host only. */
+ * (src/tensor.rs:1204): rand 0.10.2's ChaCha12 StdRng seeded through
+ * rand_core's PCG32 expansion, (next_u32 >> 8) * 2^-24, as published.  The
+ * crates are absent here and give no test vectors, so equality with the
+ * reference's stream is unpinned.  Host only. */
 int tmg_stdrng_uniform(uint64_t seed, size_t n, float *out);
 
 /* Kernel level: y[out] = W[out,in] x[in] with W raw BF16 row-major and x, y
