@@ -573,6 +573,28 @@ def test_short_prompt_splitk_gemm_vs_oracle(T, O, W, one_b):
     assert np.array_equal(a, g.forward_seq(ids[:150], gc2))
 
 
+@pytest.mark.parametrize("which", ["1b", "4b"])
+def test_short_prompt_chunks_vs_oracle(T, O, W, one_b, four_b, which):
+    # chunks of at most 64 tokens through the split-K MFMA GEMM on both
+    # models' shapes (4B: K = 2560 and 10240, M = 6144 and 20480): 64
+    # tokens, then 1, then 37 at position 65; the split reduction is
+    # order-independent, so a rerun is bitwise identical
+    g, o = one_b if which == "1b" else four_b
+    wl = W.ONE_B if which == "1b" else W.FOUR_B
+    ids = [int(t) for t in T.synth_tokens(71, 102, wl.vocab_size)]
+    gc, oc = T.KvCache(g, 128), o.new_cache()
+    a = g.forward_seq(ids[:64], gc)
+    close_logits(a, o.forward_seq(ids[:64], oc), f"{which} prefill 64")
+    close_logits(g.forward_seq(ids[64:65], gc), o.forward_seq(ids[64:65], oc), f"{which} prefill 1 at 64")
+    close_logits(g.forward_seq(ids[65:], gc), o.forward_seq(ids[65:], oc), f"{which} prefill 37 at 65")
+    for layer in (0, wl.num_hidden_layers - 1):
+        for x, y in ((gc.keys_flat(layer), oc.keys_flat(layer)), (gc.values_flat(layer), oc.values_flat(layer))):
+            d = np.abs(x - y)
+            assert np.all(d <= ABS_TOL + REL_TOL * np.abs(y)), f"{which} layer {layer} kv: {d.max():.3e}"
+    gc2 = T.KvCache(g, 128)
+    assert np.array_equal(a, g.forward_seq(ids[:64], gc2))
+
+
 def test_long_context_8k_vs_oracle_fixture(T, W, one_b):
     """The long-context workload against the oracle: 8192 prompt ids (seed 5)
     through the batched prefill, then 128 greedy ids, compared with the
