@@ -12,9 +12,9 @@
 //   lane runs the reference's sequential tail over the k candidates in
 //   order: softmax (max, exp, sequential sum, divide), nucleus cut at the
 //   first cumulative sum > top_p, renormalization, and the inverse-CDF walk.
-// Whole-vocabulary path (no top-k, or top_k > kSampleMaxK): each of the
-// reference's sorts becomes a threshold search over the whole vocabulary,
-// run as wide histogram launches (search_hist_kernel and the others below).
+// Whole-vocabulary path (no top-k, or top_k > kSampleMaxK): the same steps
+// over up to the whole vocabulary, with a device sort for the orders and
+// each running sum computed exactly in one workgroup (chain_kernel below).
 //
 // Keys order by value descending, then id ascending, which is the reference
 // argmax tie rule; the reference's sort_unstable_by leaves equal-value order
@@ -22,6 +22,7 @@
 // Keys are unique (they contain the id), so the top k set is exact.
 #include "common.cuh"
 #include "kernels.hpp"
+#include "ref_expf.h"
 
 namespace tmg {
 namespace {
@@ -270,7 +271,7 @@ __global__ __launch_bounds__(kSelectThreads) void sample_select_kernel(const Sam
     // softmax over the k candidates (src/tensor.rs:1177-1179)
     const float val = key_value(v);
     const float mx = lane_f(val, 0);
-    float p = lane < K ? expf(val - mx) : 0.0f;
+    float p = lane < K ? ref_expf(val - mx) : 0.0f;
     float sum = 0.0f;
     for (int i = 0; i < K; i++) sum += lane_f(p, i);
     p = p / sum;
@@ -312,54 +313,51 @@ __global__ __launch_bounds__(kSelectThreads) void sample_select_kernel(const Sam
 
 // ---------------------------------------------------------------------------
 // Whole-vocabulary path: no top-k (with or without a nucleus cut), or top_k
-// above kSampleMaxK.  Every pass is a launch over many workgroups; only the
-// bin and chunk selections run in one workgroup.
-//
-// The orders the reference gets by sorting are found by threshold searches:
-// among the selected ids, in (key descending, id ascending) order, the first
-// at which a running total of weights exceeds a target.
-//   SK_COUNT   key = scaled logit, weight 1, target k - 1: the k-th best
-//              logit (the reference's top-k sort);
-//   SK_NUCLEUS key = probability, weight = probability, target top_p: the
-//              nucleus cut (the reference sorts by probability, ties
-//              unspecified); the kept mass is the running total at the cut;
-//   SK_WALK    key = scaled logit, weight = probability, target = the draw:
-//              the inverse-CDF walk over the sorted top-k candidates.
-// A search is a radix search over the 32-bit key (12, 12, then 8 bits): per
-// level a histogram launch (LDS bins, then global bins) and a pick launch
-// (the bin where the running total crosses what is left of the target);
-// ties at the final key go in id order (chunk masses, then one chunk
-// scanned).  Without top-k the draw walks the ids in order (chunk masses,
-// then one chunk).  Probability masses are summed in 2^-40 fixed point, so
-// every sum is exact and independent of order.
+// above kSampleMaxK.  The reference's steps, in its orders, with its float
+// operations (src/tensor.rs:1157-1213):
+//   candidate order  ids in id order without top-k; with top-k the k best
+//                    scaled logits in descending order (the reference sorts;
+//                    ties are unspecified there, id order here);
+//   softmax          M = max, e = expf(s - M) (glibc's expf, ref_expf.h),
+//                    Z = the f32 running sum of e in candidate order, p = e/Z;
+//   nucleus          the f32 running sum of p in descending order until it
+//                    exceeds top_p, the f32 running sum of the kept p, then
+//                    p / kept sum;
+//   walk             the f32 running sum of p in candidate order until it
+//                    exceeds the draw; past the end, the first candidate
+//                    with p > 0.
+// Orders come from one bitonic sort of (scaled logit, id) keys.  Each running
+// sum is one workgroup's `chain` (below), which gives the f32 sequential
+// sum's every partial result exactly without a sequential loop over the
+// terms.
 // ---------------------------------------------------------------------------
 
 constexpr int kGenWide = 2048;  // ids per workgroup of the elementwise passes
 constexpr int kGenParts = kSampleMaxVocab / kGenWide;
-constexpr int kHistIds = 4096;  // ids per workgroup of a histogram pass
-constexpr int kGenBins = 4096;
-constexpr int kPickThreads = 1024;
-constexpr double kFx = 1099511627776.0;  // 2^40
-static_assert(kGenParts == 128 && kGenParts <= kBlock, "scratch layout: 128 partials of each kind");
-static_assert(kGenBins == 4 * kPickThreads, "the pick takes four bins per thread");
+static_assert(kGenParts == 128 && kGenParts <= kBlock, "scratch layout: 128 partial maxima");
 
-enum SearchKind { SK_COUNT = 0, SK_NUCLEUS = 1, SK_WALK = 2 };
-constexpr int kSearchRunning = -2;  // SearchState::id while levels remain
+// The running sums of the whole-vocabulary path.
+enum ChainKind { CH_Z = 0, CH_N = 1, CH_K = 2, CH_W = 3 };
 
-struct SearchState {
-    unsigned long long rest;     // target left after the heavier keys
-    unsigned long long through;  // running total through the found id
-    uint32_t pfx;                // key bits decided (the whole key after the last level)
-    int id;                      // the found id; -1: the total does not exceed the target
-    int pad[2];
+struct ChainOut {
+    float total;  // the sum over all n terms (when no partial sum exceeds the threshold)
+    int found;    // first index whose partial sum exceeds the threshold, or -1
+    float at;     // that partial sum
+    int n;        // terms summed
 };
 
-// a.scratch: sc [V] | pr [V] | max partials [128] | sum partials [128] |
-// u64 mass partials [128] | u64 histogram [4096] | SearchState [3]
+// a.scratch: sc [V] | pr [V] | max partials [128] | ChainOut [4] | sort
+// keys [sort_n(V)] (8-byte aligned: V * 8 + 512 + 64 bytes before them) |
+// running-sum chunk metadata | running-sum group metadata
+struct ChainChunkMeta;
+struct ChainGroupMeta;
+
 struct GenBufs {
-    float *sc, *pr, *pmax, *psum;
-    unsigned long long *pmass, *hist;
-    SearchState *ss;
+    float *sc, *pr, *pmax;
+    ChainOut *cs;
+    unsigned long long *keys;
+    ChainChunkMeta *cmeta;  // [kChainMaxChunks]
+    ChainGroupMeta *gmeta;  // [2][kChainMaxChunks * kChainPer]
 };
 
 __device__ __forceinline__ GenBufs gen_bufs(const SampleArgs &a) {
@@ -367,57 +365,11 @@ __device__ __forceinline__ GenBufs gen_bufs(const SampleArgs &a) {
     b.sc = a.scratch;
     b.pr = a.scratch + a.V;
     b.pmax = a.scratch + 2 * (size_t)a.V;
-    b.psum = b.pmax + kGenParts;
-    b.pmass = reinterpret_cast<unsigned long long *>(b.psum + kGenParts);
-    b.hist = b.pmass + kGenParts;
-    b.ss = reinterpret_cast<SearchState *>(b.hist + kGenBins);
+    b.cs = reinterpret_cast<ChainOut *>(b.pmax + kGenParts);
+    b.keys = reinterpret_cast<unsigned long long *>(b.cs + 4);
+    b.cmeta = reinterpret_cast<ChainChunkMeta *>(b.keys + sort_n(a.V));
+    b.gmeta = reinterpret_cast<ChainGroupMeta *>(reinterpret_cast<char *>(b.cmeta) + kSampleChainChunkBytes);
     return b;
-}
-
-// floor(p * 2^40) for 0 <= p < 2 (exact: p's 24-bit significand shifted by
-// its exponent); 0 for subnormals, negatives, NaN and p >= 2.
-__device__ __forceinline__ unsigned long long fx(float p) {
-    const uint32_t u = __float_as_uint(p);
-    const int e = (int)(u >> 23);  // with the sign bit set e > 255
-    if (e == 0 || e > 127) return 0ull;
-    const unsigned long long m = (u & 0x7fffffu) | 0x800000u;
-    const int sh = e - 110;  // value = m * 2^(e - 150), times 2^40
-    return sh >= 0 ? m << sh : (sh > -24 ? m >> -sh : 0ull);
-}
-
-__device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += shfl_xor_u64(v, off);
-    return v;
-}
-
-__device__ __forceinline__ unsigned long long wave_incl_u64(unsigned long long v) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t lo = __shfl_up((uint32_t)v, off, 64), hi = __shfl_up((uint32_t)(v >> 32), off, 64);
-        if (lane >= off) v += ((unsigned long long)hi << 32) | lo;
-    }
-    return v;
-}
-
-// Exclusive prefix over the workgroup's threads in thread order (NW
-// wavefronts); *total gets the sum.  wt holds NW values of LDS.
-template <int NW>
-__device__ unsigned long long block_excl_u64(unsigned long long v, unsigned long long *wt, unsigned long long *total) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const unsigned long long incl = wave_incl_u64(v);
-    __syncthreads();
-    if (lane == 63) wt[w] = incl;
-    __syncthreads();
-    unsigned long long before = 0, all = 0;
-#pragma unroll
-    for (int i = 0; i < NW; i++) {
-        if (i < w) before += wt[i];
-        all += wt[i];
-    }
-    *total = all;
-    return before + incl - v;
 }
 
 __device__ __forceinline__ float wg_reduce(float v, bool is_max, float *red4) {
@@ -427,31 +379,8 @@ __device__ __forceinline__ float wg_reduce(float v, bool is_max, float *red4) {
     return is_max ? fmaxf(fmaxf(red4[0], red4[1]), fmaxf(red4[2], red4[3])) : (red4[0] + red4[1]) + (red4[2] + red4[3]);
 }
 
-__device__ __forceinline__ bool use_topk(const DevState &st, int V) { return st.top_k > 0 && st.top_k < V; }
-
-// Key and weight of id i for a search; false when the weight is 0 (such an
-// id can never be where the running total crosses the target).
-__device__ __forceinline__ bool kind_kw(int kind, float s, float p, uint32_t &k, unsigned long long &w) {
-    if (kind == SK_COUNT) {
-        k = f32_order(s);
-        w = 1;
-    } else if (kind == SK_NUCLEUS) {
-        k = f32_order(p);
-        w = fx(p);
-    } else {
-        k = f32_order(s);
-        w = fx(p);
-    }
-    return w != 0;
-}
-
-__device__ __forceinline__ unsigned long long kind_target(int kind, const SampleArgs &a, const DevState &st) {
-    return kind == SK_COUNT ? (unsigned long long)(st.top_k - 1)
-                            : kind == SK_NUCLEUS ? fx(st.top_p) : fx(step_draw(a, st.step));
-}
-
 // pass 1: scaled logits (penalty, temperature; src/tensor.rs:1142-1154,
-// :1168) and the workgroup maximum
+// :1168), the workgroup maximum, and pr cleared
 __global__ __launch_bounds__(kBlock) void sample_scale_kernel(const SampleArgs a) {
     __shared__ float red4[4];
     const DevState st = *a.st;
@@ -473,6 +402,7 @@ __global__ __launch_bounds__(kBlock) void sample_scale_kernel(const SampleArgs a
                 v = v > 0.0f ? __fdiv_rn(v, st.penalty) : __fmul_rn(v, st.penalty);
             v = __fdiv_rn(v, st.temperature);
             b.sc[i] = v;
+            b.pr[i] = 0.0f;
             mx = fmaxf(mx, v);
         }
     }
@@ -480,334 +410,607 @@ __global__ __launch_bounds__(kBlock) void sample_scale_kernel(const SampleArgs a
     if (threadIdx.x == 0) b.pmax[blockIdx.x] = m;
 }
 
-// pass 2: softmax numerators over the candidates (src/tensor.rs:1177-1179):
-// pr = exp(s - M) for candidates (all ids, or the top-k found by SK_COUNT),
-// 0 for the others; M the overall maximum (always a candidate); workgroup sum
+// The maximum scaled logit (f32::max ignores NaN, as fmaxf does): every
+// workgroup's partial maxima reduced again.
+__device__ float scaled_max(const SampleArgs &a, const GenBufs &b, float *red4) {
+    const int nparts = (a.V + kGenWide - 1) / kGenWide;
+    float m = -INFINITY;
+    for (int i = threadIdx.x; i < nparts; i += kBlock) m = fmaxf(m, b.pmax[i]);
+    return wg_reduce(m, true, red4);
+}
+
+// ---- the sort: keys (scaled logit order, then ~id) descending --------------
+
+// keys[i] = argmax_key(scaled, i) for ids with a non-NaN scaled logit, 0 for
+// NaN ones and for the padding up to sort_n(V)
+__global__ __launch_bounds__(kBlock) void sort_keys_kernel(const SampleArgs a) {
+    const GenBufs b = gen_bufs(a);
+    const int n = sort_n(a.V);
+    for (int i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) {
+        unsigned long long k = 0ull;
+        if (i < a.V) {
+            const float v = b.sc[i];
+            if (v == v) k = argmax_key(v, (uint32_t)i);
+        }
+        b.keys[i] = k;
+    }
+}
+
+// compare-exchange of a bitonic network sorting descending: in stage `size`
+// the pair (i, i + stride) is ordered descending when (i & size) == 0
+__device__ __forceinline__ void bitonic_cx(unsigned long long &x, unsigned long long &y, bool desc) {
+    const bool swap = desc ? x < y : x > y;
+    if (swap) {
+        const unsigned long long t = x;
+        x = y;
+        y = t;
+    }
+}
+
+// stages size = 2 .. kSortBlock within each block of kSortBlock keys (LDS),
+// or, with size0 > kSortBlock, stage size0's strides below kSortBlock
+__global__ __launch_bounds__(kSortThreads) void sort_block_kernel(const SampleArgs a, int size0) {
+    __shared__ unsigned long long sk[kSortBlock];
+    const GenBufs b = gen_bufs(a);
+    unsigned long long *g = b.keys + (size_t)blockIdx.x * kSortBlock;
+    const int base = blockIdx.x * kSortBlock;
+    for (int i = threadIdx.x; i < kSortBlock; i += kSortThreads) sk[i] = g[i];
+    __syncthreads();
+    const int s_lo = size0 > kSortBlock ? size0 : 2, s_hi = size0 > kSortBlock ? size0 : kSortBlock;
+    for (int size = s_lo; size <= s_hi; size <<= 1) {
+        for (int stride = min(size, kSortBlock) >> 1; stride > 0; stride >>= 1) {
+            for (int p = threadIdx.x; p < kSortBlock / 2; p += kSortThreads) {
+                const int i = (p / stride) * 2 * stride + (p % stride);
+                bitonic_cx(sk[i], sk[i + stride], ((base + i) & size) == 0);
+            }
+            __syncthreads();
+        }
+    }
+    for (int i = threadIdx.x; i < kSortBlock; i += kSortThreads) g[i] = sk[i];
+}
+
+// one stride >= kSortBlock of stage `size`, across blocks
+__global__ __launch_bounds__(kBlock) void sort_global_kernel(const SampleArgs a, int size, int stride) {
+    const GenBufs b = gen_bufs(a);
+    const int half = sort_n(a.V) / 2;
+    for (int p = blockIdx.x * kBlock + threadIdx.x; p < half; p += gridDim.x * kBlock) {
+        const int i = (p / stride) * 2 * stride + (p % stride);
+        unsigned long long x = b.keys[i], y = b.keys[i + stride];
+        bitonic_cx(x, y, (i & size) == 0);
+        b.keys[i] = x;
+        b.keys[i + stride] = y;
+    }
+}
+
+// id of the candidate at rank j (0 for a NaN key, which holds no id)
+__device__ __forceinline__ int rank_id(const GenBufs &b, int j) {
+    const unsigned long long k = b.keys[j];
+    return k ? key_index(k) : 0;
+}
+
+__device__ __forceinline__ bool use_topk(const DevState &st, int V) { return st.top_k > 0 && st.top_k < V; }
+
+// softmax numerators over the candidates (src/tensor.rs:1177-1179, :1057):
+// e = expf(s - M); without top-k every id (by id), with it the ranks below k
 __global__ __launch_bounds__(kBlock) void sample_exp_kernel(const SampleArgs a) {
     __shared__ float red4[4];
     const DevState st = *a.st;
     const GenBufs b = gen_bufs(a);
-    const int nparts = (a.V + kGenWide - 1) / kGenWide;
-    float m = -INFINITY;
-    for (int i = threadIdx.x; i < nparts; i += kBlock) m = fmaxf(m, b.pmax[i]);
-    const float M = wg_reduce(m, true, red4);
-    __syncthreads();
+    const float M = scaled_max(a, b, red4);
     const bool k_on = use_topk(st, a.V);
-    uint32_t kk = 0;
-    int kid = a.V;
-    if (k_on) {
-        kk = b.ss[SK_COUNT].pfx;
-        kid = b.ss[SK_COUNT].id;
+    const int n = k_on ? st.top_k : a.V;
+    for (int j = blockIdx.x * kBlock + threadIdx.x; j < n; j += gridDim.x * kBlock) {
+        const int id = k_on ? rank_id(b, j) : j;
+        b.pr[id] = ref_expf(b.sc[id] - M);
     }
-    const int base = blockIdx.x * kGenWide + threadIdx.x;
-    float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kGenWide / kBlock; j++) {
-        const int i = base + j * kBlock;
-        if (i < a.V) {
-            const float s = b.sc[i];
-            const uint32_t k = f32_order(s);
-            const float e = (!k_on || k > kk || (k == kk && i <= kid)) ? expf(s - M) : 0.0f;
-            b.pr[i] = e;
-            sum += e;
-        }
-    }
-    const float S = wg_reduce(sum, false, red4);
-    if (threadIdx.x == 0) b.psum[blockIdx.x] = S;
 }
 
-// pass 3: pr = pr / S, S the partial sums added in order
+// ---- the f32 running sum --------------------------------------------------
+//
+// s_0 = 0, s_j = fl(s_{j-1} + x_j) with x_j >= 0.  While the partial sums
+// stay in one binade [2^e, 2^(e+1)) (ulp u), fl(s + x) = s + q u with q the
+// integer nearest x / u; when x / u is exactly half-way (a tie), q is the
+// choice that leaves s + q u even, i.e. floor(x / u) + 1 exactly when the
+// running significand after floor(x / u) is odd.  Writing m for s / u (the
+// significand, 2^23 <= m < 2^24, or below 2^23 for subnormal s, whose u is
+// 2^-149 like the first normal binade's), s's bits are ((e_u - 1) << 23) + m
+// for e_u = max(biased exponent, 1), and within a binade the partial sums are
+// m plus integer prefix sums of the q: order-free, except for the parity at
+// ties, which is settled tie by tie in order.  A real f32 add is needed only
+// at a term of 2^24 u or more, where the sum leaves the binade, and after a
+// non-finite value.
+
+// q = x / u rounded to nearest for u = 2^(eu - 150), or its floor with `tie`
+// set when x / u is half-way; `flag` when x is negative, -0 or not finite,
+// or x >= 2^24 u
+__device__ __forceinline__ uint32_t chain_q(float x, int eu, bool &tie, bool &flag) {
+    const uint32_t ux = __float_as_uint(x);
+    if (ux == 0u) return 0u;
+    int ex = (int)(ux >> 23);
+    if (ex >= 255) {  // sign bit set (negative or -0), or inf / NaN
+        flag = true;
+        return 0u;
+    }
+    uint32_t mx = ux & 0x7fffffu;
+    if (ex) mx |= 0x800000u;
+    else ex = 1;
+    const int k = eu - ex;  // x / u = mx / 2^k
+    if (k < 0) {
+        flag = true;
+        return 0u;
+    }
+    if (k == 0) return mx;
+    if (k > 24) return 0u;  // x / u < 1/2
+    uint32_t q = mx >> k;
+    const uint32_t rem = mx & ((1u << k) - 1u), half = 1u << (k - 1);
+    if (rem > half) q++;
+    else if (rem == half) tie = true;
+    return q;
+}
+
+constexpr int kChainThreads = 1024;
+constexpr int kChainChunk = 1024;  // terms per chunk: 16 per lane of one wavefront
+constexpr int kChainPer = kChainChunk / 64;  // groups of 64 terms per chunk
+constexpr int kChainMaxChunks = kSampleMaxVocab / kChainChunk;
+constexpr int kChainTies = 32;  // ties per chunk its one-step advance settles
+constexpr int kGroupTies = 2;   // ties per group its one-step advance settles
+constexpr uint32_t kChainSat = 1u << 25;  // integer sums saturate here (>= 2^24 leaves any binade)
+static_assert(kChainMaxChunks == 256 && kChainPer == 16, "chain layout");
+
+// Per chunk: the double sum, the guessed starting binade, and under it the
+// integer sum of the q (floors at ties; saturated), the ties' inclusive
+// integer prefixes from the chunk start in order, and whether any term is
+// flagged or there are more than kChainTies ties.
+struct ChainChunkMeta {
+    double dsum;
+    uint32_t q;
+    int ntie, flag, eguess;
+    uint32_t ties[kChainTies];
+};
+// Per group of 64 terms, under the group's own guessed starting binade
+// (bin 0) and the next one (bin 1): the integer sum, tie count, the first
+// kGroupTies ties' inclusive prefixes from the group start, and the flag.
+struct ChainGroupMeta {
+    uint32_t q;
+    uint32_t tie[kGroupTies];
+    int16_t ntie_flag;  // tie count, or -1 when a term is flagged
+    int16_t eguess;     // the group's guessed starting binade (bin 0)
+};
+
+static_assert(sizeof(ChainChunkMeta) * kChainMaxChunks == kSampleChainChunkBytes, "scratch layout");
+static_assert(sizeof(ChainGroupMeta) * 2 * kChainMaxChunks * kChainPer == kSampleChainGroupBytes, "scratch layout");
+
+__device__ __forceinline__ ChainChunkMeta *chain_chunks(const GenBufs &b) { return b.cmeta; }
+__device__ __forceinline__ ChainGroupMeta *chain_groups(const GenBufs &b) { return b.gmeta; }
+
+// Inclusive prefix sum over the wavefront's 64 lanes: shifts within rows of
+// 16 lanes, then each row's total broadcast to the rows above it.
+__device__ __forceinline__ uint32_t wave_incl_u32(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);  // row_shr:1
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);  // row_shr:2
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true);  // row_shr:4
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true);  // row_shr:8
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+    return v;
+}
+
+__device__ __forceinline__ uint32_t lane_u32(uint32_t v, int i) { return (uint32_t)__builtin_amdgcn_readlane((int)v, i); }
+
+// One wavefront adds terms j0 .. j0 + 63 (lane l holds x of j0 + l; terms at
+// or past n are absent) to the running sum whose bits are *sb.  With a
+// threshold, returns the first index whose partial sum exceeds T (its sum in
+// *at), else -1.
+__device__ int chain_group(float x, int j0, int n, bool has_t, float T, uint32_t *sb, float *at) {
+    const int lane = threadIdx.x & 63;
+    const bool in = j0 + lane < n;
+    const unsigned long long upto = lane == 63 ? ~0ull : (2ull << lane) - 1ull;  // lanes 0 .. lane
+    int start = 0;
+    uint32_t s = *sb;
+    while (start < 64) {
+        const bool pend = in && lane >= start;
+        const unsigned long long pm = __ballot(pend);
+        if (!pm) break;
+        const int es = (int)(s >> 23);
+        const bool nonfinite = es >= 255;
+        const int eu = es > 1 ? es : 1;
+        const uint32_t m = es ? ((s & 0x7fffffu) | 0x800000u) : s;
+        bool tie = false, flag = false;
+        uint32_t q = 0u;
+        if (pend) {
+            if (nonfinite) flag = true;
+            else q = chain_q(x, eu, tie, flag);
+        }
+        uint32_t incl = wave_incl_u32(q);
+        // ties in order: round up where the running significand is odd
+        unsigned long long tm = __ballot(pend && tie), ups = 0ull;
+        uint32_t adj = 0u;
+        while (tm) {
+            const int tl = __builtin_ctzll(tm);
+            tm &= tm - 1ull;
+            if ((m + lane_u32(incl, tl) + adj) & 1u) {
+                adj++;
+                ups |= 1ull << tl;
+            }
+        }
+        incl += (uint32_t)__builtin_popcountll(ups & upto);
+        const bool special = pend && (flag || (!nonfinite && m + incl >= (1u << 24)));
+        const unsigned long long sm = __ballot(special);
+        const int f = sm ? __builtin_ctzll(sm) : 64;
+        const uint32_t sl = ((uint32_t)(eu - 1) << 23) + m + incl;  // partial sum of committed lanes
+        if (has_t) {
+            const unsigned long long hm = __ballot(pend && lane < f && __uint_as_float(sl) > T);
+            if (hm) {
+                const int h = __builtin_ctzll(hm);
+                *at = __uint_as_float(lane_u32(sl, h));
+                *sb = lane_u32(sl, h);
+                return j0 + h;
+            }
+        }
+        if (f == 64) {
+            s = lane_u32(sl, 63 - __builtin_clzll(pm));
+            break;
+        }
+        const uint32_t before = f > start ? lane_u32(sl, f - 1) : s;
+        const float xf = __uint_as_float(lane_u32(__float_as_uint(x), f));
+        s = __float_as_uint(__uint_as_float(before) + xf);
+        if (has_t && __uint_as_float(s) > T) {
+            *at = __uint_as_float(s);
+            *sb = s;
+            return j0 + f;
+        }
+        start = f + 1;
+    }
+    *sb = s;
+    return -1;
+}
+
+// The chain's terms: pr by id in id order, or by rank (sorted order).
+__device__ __forceinline__ float chain_x(const GenBufs &b, bool by_rank, int j) {
+    return by_rank ? b.pr[rank_id(b, j)] : b.pr[j];
+}
+
+// Lane l's kChainPer terms of chunk c: c * kChainChunk + 64 i + l (0 past n).
+__device__ __forceinline__ void chain_load(const GenBufs &b, bool by_rank, int c, int n, int lane,
+                                           float (&xs)[kChainPer]) {
+#pragma unroll
+    for (int i = 0; i < kChainPer; i++) {
+        const int j = c * kChainChunk + i * 64 + lane;
+        xs[i] = j < n ? chain_x(b, by_rank, j) : 0.0f;
+    }
+}
+
+// A chain's terms (order, count) and threshold.
+struct ChainSpec {
+    bool by_rank, has_t;
+    float T;
+    int n;
+};
+
+__device__ ChainSpec chain_spec(const SampleArgs &a, const GenBufs &b, const DevState &st, int kind) {
+    const bool k_on = use_topk(st, a.V);
+    ChainSpec c{k_on, false, 0.0f, k_on ? st.top_k : a.V};
+    if (kind == CH_N) {
+        c.by_rank = true;
+        c.has_t = true;
+        c.T = st.top_p;
+    } else if (kind == CH_K) {
+        c.by_rank = true;
+        const int f = b.cs[CH_N].found;
+        c.n = f >= 0 ? f + 1 : b.cs[CH_N].n;
+    } else if (kind == CH_W) {
+        c.has_t = true;
+        c.T = step_draw(a, st.step);
+    }
+    return c;
+}
+
+// A running sum (kind CH_*) over n terms in three launches:
+//   chain_sum_kernel    per chunk of kChainChunk terms (a wavefront each),
+//                       a double sum in any order;
+//   chain_quant_kernel  per chunk, the starting binade guessed from the
+//                       double prefix, and under it the chunk's and its
+//                       groups' integer sums and tie prefixes (the groups'
+//                       also under the next binade);
+//   chain_walk_kernel   one wavefront walks the chunks: a chunk whose guess
+//                       holds (the running sum is in that binade, no flag,
+//                       its ties settled, the integer sum stays inside the
+//                       binade and, with a threshold, the sum at its end does
+//                       not exceed it) advances in one step; in any other,
+//                       each group of 64 terms advances in one step the same
+//                       way under its binade, or is added term by term
+//                       (chain_group).  CH_W then emits the token.
+__global__ __launch_bounds__(64) void chain_sum_kernel(const SampleArgs a, int kind) {
+    const DevState st = *a.st;
+    const GenBufs b = gen_bufs(a);
+    const ChainSpec cs = chain_spec(a, b, st, kind);
+    const int lane = threadIdx.x;
+    const int c = blockIdx.x;
+    if (c * kChainChunk >= cs.n) return;
+    float xs[kChainPer];
+    chain_load(b, cs.by_rank, c, cs.n, lane, xs);
+    double d = 0.0;
+#pragma unroll
+    for (int i = 0; i < kChainPer; i++) d += (double)xs[i];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) d += __shfl_xor(d, off, 64);
+    if (lane == 0) chain_chunks(b)[c].dsum = d;
+}
+
+__global__ __launch_bounds__(64) void chain_quant_kernel(const SampleArgs a, int kind) {
+    const DevState st = *a.st;
+    const GenBufs b = gen_bufs(a);
+    const ChainSpec cs = chain_spec(a, b, st, kind);
+    const int lane = threadIdx.x;
+    const int c = blockIdx.x;
+    if (c * kChainChunk >= cs.n) return;
+    ChainChunkMeta *cm = chain_chunks(b);
+    ChainGroupMeta *gm = chain_groups(b);
+    // the double prefix at the chunk's start
+    double pre = 0.0;
+    for (int k = lane; k < c; k += 64) pre += cm[k].dsum;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) pre += __shfl_xor(pre, off, 64);
+    float xs[kChainPer];
+    chain_load(b, cs.by_rank, c, cs.n, lane, xs);
+    // each group's guessed starting binade, from the prefix and the groups' sums
+    int eg[kChainPer];
+#pragma unroll
+    for (int i = 0; i < kChainPer; i++) {
+        const int e = (int)(__float_as_uint((float)pre) >> 23);
+        eg[i] = e > 1 ? e : 1;
+        pre += (double)wave_sum(xs[i]);
+    }
+    const unsigned long long below = (1ull << lane) - 1ull;
+    uint32_t run = 0u;
+    int nt = 0;
+    bool cflag = false;
+#pragma unroll
+    for (int bin = 0; bin < 2; bin++) {
+#pragma unroll
+        for (int i = 0; i < kChainPer; i++) {
+            bool tie = false, fl = false;
+            const uint32_t q = chain_q(xs[i], eg[i] + bin, tie, fl);
+            const uint32_t incl = wave_incl_u32(q);
+            const unsigned long long tm = __ballot(tie);
+            const int gt = __builtin_popcountll(tm);
+            const bool gflag = __ballot(fl) != 0ull;
+            // the group's ties, first kGroupTies of them
+            ChainGroupMeta g;
+            g.q = lane_u32(incl, 63);
+            g.tie[0] = g.tie[1] = 0u;
+            unsigned long long tt = tm;
+#pragma unroll
+            for (int k = 0; k < kGroupTies; k++)
+                if (tt) {
+                    g.tie[k] = lane_u32(incl, __builtin_ctzll(tt));
+                    tt &= tt - 1ull;
+                }
+            g.ntie_flag = (int16_t)(gflag ? -1 : gt);
+            g.eguess = (int16_t)eg[i];
+            if (lane == 0) gm[(size_t)bin * kChainMaxChunks * kChainPer + c * kChainPer + i] = g;
+            if (bin == 0) {
+                // the chunk's one-step advance: all its groups under the chunk's
+                // guess (any group guessed otherwise makes it walk group by group)
+                if (tie) {
+                    const int slot = nt + __builtin_popcountll(tm & below);
+                    if (slot < kChainTies) cm[c].ties[slot] = min(run + incl, kChainSat);
+                }
+                nt += gt;
+                run = min(run + g.q, kChainSat);
+                cflag |= gflag || eg[i] != eg[0];
+            }
+        }
+    }
+    if (lane == 0) {
+        cm[c].q = run;
+        cm[c].ntie = nt;
+        cm[c].flag = cflag || nt > kChainTies;
+        cm[c].eguess = eg[0];
+    }
+}
+
+// Chunks whose terms and group metadata the walk stages in LDS up front:
+// the first chunk, flagged ones, ones whose guessed binade differs from the
+// next chunk's, and, with a threshold, the one where the double prefix
+// crosses it and its neighbours (in chunk order, the first kChainStaged).
+constexpr int kChainStaged = 12;
+
+__global__ __launch_bounds__(kChainThreads) void chain_walk_kernel(const SampleArgs a, int kind) {
+    __shared__ uint32_t ties[kChainMaxChunks][kChainTies];
+    __shared__ uint32_t cq[kChainMaxChunks];
+    __shared__ int cnt[kChainMaxChunks], cfl[kChainMaxChunks], ceg[kChainMaxChunks], slot[kChainMaxChunks];
+    __shared__ float sx[kChainStaged][kChainChunk];
+    __shared__ ChainGroupMeta sg[kChainStaged][2 * kChainPer];
+    __shared__ int staged[kChainStaged];
+    __shared__ int nstaged, fb_sh;
+    const DevState st = *a.st;
+    const GenBufs b = gen_bufs(a);
+    const ChainSpec cs = chain_spec(a, b, st, kind);
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int n = cs.n, nch = (n + kChainChunk - 1) / kChainChunk;
+    const ChainChunkMeta *cm = chain_chunks(b);
+    const ChainGroupMeta *gm = chain_groups(b);
+    for (int k = t; k < nch * kChainTies; k += kChainThreads) {
+        const int c = k / kChainTies, i = k % kChainTies;
+        ties[c][i] = cm[c].ties[i];
+    }
+    for (int c = t; c < nch; c += kChainThreads) {
+        cq[c] = cm[c].q;
+        cnt[c] = cm[c].ntie;
+        cfl[c] = cm[c].flag;
+        ceg[c] = cm[c].eguess;
+        slot[c] = -1;
+    }
+    __syncthreads();
+    if (w == 0) {
+        // pick the chunks to stage (one wavefront, chunks 64 at a time)
+        int ns = 0;
+        double pre = 0.0;
+        for (int c0 = 0; c0 < nch && ns < kChainStaged; c0 += 64) {
+            const int c = c0 + lane;
+            const double d = c < nch ? cm[c].dsum : 0.0;
+            double incl = d;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const double o = __shfl_up(incl, off, 64);
+                if (lane >= off) incl += o;
+            }
+            const double before = pre + incl - d, after = pre + incl;
+            bool want = false;
+            if (c < nch) {
+                want = c == 0 || cfl[c] || (c + 1 < nch && ceg[c + 1] != ceg[c]);
+                // the threshold's chunk by the double prefix, and its neighbours
+                if (cs.has_t && before <= 1.01 * cs.T && after >= 0.99 * cs.T) want = true;
+            }
+            const unsigned long long wm = __ballot(want);
+            const int r = ns + __builtin_popcountll(wm & ((1ull << lane) - 1ull));
+            if (want && r < kChainStaged) {
+                slot[c] = r;
+                staged[r] = c;
+            }
+            ns = min(kChainStaged, ns + __builtin_popcountll(wm));
+            pre += __shfl(incl, 63, 64);
+        }
+        if (lane == 0) nstaged = ns;
+    }
+    __syncthreads();
+    // stage them (all wavefronts)
+    for (int k = w; k < nstaged; k += kChainThreads / 64) {
+        const int c = staged[k];
+        float xs[kChainPer];
+        chain_load(b, cs.by_rank, c, n, lane, xs);
+#pragma unroll
+        for (int i = 0; i < kChainPer; i++) sx[k][i * 64 + lane] = xs[i];
+        if (lane < 2 * kChainPer)
+            sg[k][lane] = gm[(size_t)(lane / kChainPer) * kChainMaxChunks * kChainPer + c * kChainPer + lane % kChainPer];
+    }
+    __syncthreads();
+    if (w == 0) {
+        // the chunks' metadata in registers: lane l holds chunks l + 64 r
+        constexpr int R = kChainMaxChunks / 64;
+        uint32_t rq[R], rnt[R], rfl[R], reg[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int c = r * 64 + lane;
+            rq[r] = c < nch ? cq[c] : 0u;
+            rnt[r] = c < nch ? (uint32_t)cnt[c] : 0u;
+            rfl[r] = c < nch ? (uint32_t)cfl[c] : 1u;
+            reg[r] = c < nch ? (uint32_t)ceg[c] : 0u;
+        }
+        auto meta = [&](const uint32_t(&v)[R], int c) {
+            const int r = c >> 6;
+            const uint32_t x = r == 0 ? v[0] : r == 1 ? v[1] : r == 2 ? v[2] : v[3];
+            return lane_u32(x, c & 63);
+        };
+        uint32_t s = 0u;  // +0.0
+        int found = -1;
+        float at = 0.0f;
+        for (int c = 0; c < nch && found < 0; c++) {
+            const int es = (int)(s >> 23);
+            const int eg = (int)meta(reg, c);
+            if (es < 255 && !meta(rfl, c)) {
+                const int eu = es > 1 ? es : 1;
+                const uint32_t m = es ? ((s & 0x7fffffu) | 0x800000u) : s;
+                if (eu == eg) {
+                    uint32_t adj = 0u;
+                    const int nt = (int)meta(rnt, c);
+                    for (int i = 0; i < nt; i++) adj += (m + ties[c][i] + adj) & 1u;
+                    const uint32_t mend = m + meta(rq, c) + adj;  // < 2^26: no wrap
+                    if (mend < (1u << 24)) {
+                        const uint32_t sn = ((uint32_t)(eu - 1) << 23) + mend;
+                        if (!cs.has_t || !(__uint_as_float(sn) > cs.T)) {
+                            s = sn;
+                            continue;
+                        }
+                    }
+                }
+            }
+            // group by group: lanes 0-15 hold the groups' bin-0 data, 16-31 bin 1
+            float xs[kChainPer];
+            ChainGroupMeta g{};
+            const int sl = slot[c];
+            if (sl >= 0) {
+#pragma unroll
+                for (int i = 0; i < kChainPer; i++) xs[i] = sx[sl][i * 64 + lane];
+                if (lane < 2 * kChainPer) g = sg[sl][lane];
+            } else {
+                chain_load(b, cs.by_rank, c, n, lane, xs);
+                if (lane < 2 * kChainPer)
+                    g = gm[(size_t)(lane / kChainPer) * kChainMaxChunks * kChainPer + c * kChainPer + lane % kChainPer];
+            }
+            for (int i = 0; i < kChainPer; i++) {
+                const int es2 = (int)(s >> 23);
+                const int eu = es2 > 1 ? es2 : 1;
+                const int bin = eu - (int)lane_u32((uint32_t)(int)g.eguess, i);
+                if (es2 < 255 && (bin == 0 || bin == 1)) {
+                    const int src = bin * kChainPer + i;
+                    const int ntf = (int)lane_u32((uint32_t)g.ntie_flag, src);
+                    if (ntf >= 0 && ntf <= kGroupTies) {
+                        const uint32_t m = es2 ? ((s & 0x7fffffu) | 0x800000u) : s;
+                        uint32_t adj = 0u;
+                        if (ntf > 0) adj += (m + lane_u32(g.tie[0], src) + adj) & 1u;
+                        if (ntf > 1) adj += (m + lane_u32(g.tie[1], src) + adj) & 1u;
+                        const uint32_t mend = m + lane_u32(g.q, src) + adj;
+                        if (mend < (1u << 24)) {
+                            const uint32_t sn = ((uint32_t)(eu - 1) << 23) + mend;
+                            if (!cs.has_t || !(__uint_as_float(sn) > cs.T)) {
+                                s = sn;
+                                continue;
+                            }
+                        }
+                    }
+                }
+                found = chain_group(xs[i], c * kChainChunk + i * 64, n, cs.has_t, cs.T, &s, &at);
+                if (found >= 0) break;
+            }
+        }
+        if (lane == 0) {
+            ChainOut o;
+            o.total = __uint_as_float(s);
+            o.found = found;
+            o.at = at;
+            o.n = n;
+            b.cs[kind] = o;
+        }
+    }
+    if (kind != CH_W) return;
+    __syncthreads();
+    int pick = b.cs[CH_W].found;
+    if (pick < 0) {
+        // past the last partial sum: the first candidate with p > 0
+        if (t == 0) fb_sh = 0x7fffffff;
+        __syncthreads();
+        int first = 0x7fffffff;
+        for (int j = t; j < n; j += kChainThreads)
+            if (chain_x(b, cs.by_rank, j) > 0.0f) {
+                first = j;
+                break;
+            }
+        if (first != 0x7fffffff) atomicMin(&fb_sh, first);
+        __syncthreads();
+        pick = fb_sh == 0x7fffffff ? 0 : fb_sh;
+    }
+    if (t == 0) emit_token(a, cs.by_rank ? rank_id(b, pick) : pick);
+}
+
+// p = e / Z over all ids (non-candidates hold 0)
 __global__ __launch_bounds__(kBlock) void sample_norm_kernel(const SampleArgs a) {
-    __shared__ float Ssh;
     const GenBufs b = gen_bufs(a);
-    const int nparts = (a.V + kGenWide - 1) / kGenWide;
-    if (threadIdx.x == 0) {
-        float S = 0.0f;
-        for (int i = 0; i < nparts; i++) S += b.psum[i];
-        Ssh = S;
-    }
-    __syncthreads();
-    const float S = Ssh;
-    const int base = blockIdx.x * kGenWide + threadIdx.x;
-#pragma unroll
-    for (int j = 0; j < kGenWide / kBlock; j++) {
-        const int i = base + j * kBlock;
-        if (i < a.V) b.pr[i] = b.pr[i] / S;
-    }
+    const float Z = b.cs[CH_Z].total;
+    for (int i = blockIdx.x * kBlock + threadIdx.x; i < a.V; i += gridDim.x * kBlock) b.pr[i] = b.pr[i] / Z;
 }
 
-// A search level's histogram: key digit `level` of the selected ids whose
-// higher digits equal the prefix picked so far, weights into LDS bins, then
-// the non-zero bins into the global histogram.
-__global__ __launch_bounds__(kBlock) void search_hist_kernel(const SampleArgs a, int kind, int level) {
-    __shared__ unsigned long long h[kGenBins];
-    const GenBufs b = gen_bufs(a);
-    const SearchState s = b.ss[kind];
-    if (level > 0 && s.id != kSearchRunning) return;
-    const int shift = level == 0 ? 20 : level == 1 ? 8 : 0;
-    const uint32_t nb = level == 2 ? 256u : 4096u;
-    const int above = level == 1 ? 20 : 8;  // levels 1, 2: the prefix is key >> above
-    for (int i = threadIdx.x; i < (int)nb; i += kBlock) h[i] = 0;
-    __syncthreads();
-    constexpr int PER = kHistIds / kBlock;
-    const int base = blockIdx.x * kHistIds + threadIdx.x;
-    float sv[PER], pv[PER];
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int i = base + j * kBlock;
-        sv[j] = (kind != SK_NUCLEUS && i < a.V) ? b.sc[i] : 0.0f;
-        pv[j] = (kind != SK_COUNT && i < a.V) ? b.pr[i] : 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int i = base + j * kBlock;
-        uint32_t k;
-        unsigned long long w;
-        if (i >= a.V || !kind_kw(kind, sv[j], pv[j], k, w)) continue;
-        if (level > 0 && (k >> above) != s.pfx) continue;
-        atomicAdd(&h[(k >> shift) & (nb - 1)], w);
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < (int)nb; i += kBlock)
-        if (h[i]) __hip_atomic_fetch_add(&b.hist[i], h[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// A search level's pick: the bin (from the top) where the running total
-// first exceeds what is left of the target; clears the global histogram for
-// the next level.  At level 0 a total that does not exceed the target ends
-// the search (id -1).
-__global__ __launch_bounds__(kPickThreads) void search_pick_kernel(const SampleArgs a, int kind, int level) {
-    __shared__ unsigned long long wt[kPickThreads / 64];
-    __shared__ unsigned long long pk;
-    const DevState st = *a.st;
-    const GenBufs b = gen_bufs(a);
-    const SearchState s = b.ss[kind];
-    if (level > 0 && s.id != kSearchRunning) return;
-    const int t = threadIdx.x;
-    const unsigned long long rest = level == 0 ? kind_target(kind, a, st) : s.rest;
-    const int nb = level == 2 ? 256 : 4096;
-    unsigned long long c[4], mine = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int bin = nb - 1 - 4 * t - j;
-        c[j] = bin >= 0 ? b.hist[bin] : 0ull;
-        mine += c[j];
-    }
-    if (t == 0) pk = ~0ull;
-    unsigned long long total;
-    unsigned long long cum = block_excl_u64<kPickThreads / 64>(mine, wt, &total);
-    if (cum <= rest && cum + mine > rest) {
-        for (int j = 0; j < 4; j++) {
-            if (cum + c[j] > rest) {
-                // the bin (12 bits) and the weight before it (< 2^52)
-                pk = ((unsigned long long)(nb - 1 - 4 * t - j) << 52) | cum;
-                break;
-            }
-            cum += c[j];
-        }
-    }
-    __syncthreads();
-    const unsigned long long hit = pk;
-    // every thread has read its bins: clear them for the next level
-#pragma unroll
-    for (int j = 0; j < 4; j++) b.hist[4 * t + j] = 0ull;
-    if (t == 0) {
-        SearchState n = s;
-        if (total <= rest || hit == ~0ull) {
-            n.id = -1;
-        } else {
-            n.pfx = ((level == 0 ? 0u : s.pfx) << (level == 2 ? 8 : 12)) | (uint32_t)(hit >> 52);
-            n.rest = rest - (hit & ((1ull << 52) - 1));
-            n.id = kSearchRunning;
-        }
-        b.ss[kind] = n;
-    }
-}
-
-// Ties at the final key, in id order: pass 1, the mass of the tied ids per
-// 2048-id chunk.
-__global__ __launch_bounds__(kBlock) void search_tie_sums_kernel(const SampleArgs a, int kind) {
-    __shared__ unsigned long long red4[4];
-    const GenBufs b = gen_bufs(a);
-    const SearchState s = b.ss[kind];
-    if (s.id != kSearchRunning) return;
-    const int i0 = blockIdx.x * kGenWide + 8 * threadIdx.x;
-    unsigned long long m = 0;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int i = i0 + j;
-        if (i >= a.V) break;
-        uint32_t k;
-        unsigned long long w;
-        if (kind_kw(kind, b.sc[i], b.pr[i], k, w) && k == s.pfx) m += w;
-    }
-    m = wave_sum_u64(m);
-    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) b.pmass[blockIdx.x] = (red4[0] + red4[1]) + (red4[2] + red4[3]);
-}
-
-// The first id, in id order, where the running mass of wv(i) (any i < V)
-// exceeds `rest`, given each 2048-id chunk's mass in pmass: the chunk by a
-// prefix over the chunk masses, then the id within it (thread t holds ids
-// 8t .. 8t+7 of the chunk, so thread order is id order).  Returns -1 when
-// the total does not exceed `rest`; *through gets the running mass through
-// the id.  One workgroup of kBlock threads.
-template <class Wv>
-__device__ int chunk_threshold(const SampleArgs &a, const unsigned long long *pmass, Wv wv, unsigned long long rest,
-                               unsigned long long *through) {
-    __shared__ unsigned long long wt[4];
-    __shared__ unsigned long long pk, pth;
-    const int t = threadIdx.x;
-    const int nparts = (a.V + kGenWide - 1) / kGenWide;  // <= kGenParts <= kBlock
-    if (t == 0) pk = ~0ull;
-    const unsigned long long c = t < nparts ? pmass[t] : 0ull;
-    unsigned long long tot;
-    const unsigned long long cum = block_excl_u64<4>(c, wt, &tot);
-    if (t < nparts && cum <= rest && cum + c > rest) pk = ((unsigned long long)t << 48) | cum;
-    __syncthreads();
-    const unsigned long long hit = pk;
-    __syncthreads();
-    if (hit == ~0ull) return -1;
-    const int g = (int)(hit >> 48);
-    const unsigned long long before = hit & ((1ull << 48) - 1), left = rest - before;
-    const int i0 = g * kGenWide + 8 * t;
-    unsigned long long q[8], m = 0;
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        q[k] = i0 + k < a.V ? wv(i0 + k) : 0ull;
-        m += q[k];
-    }
-    if (t == 0) pk = ~0ull;
-    unsigned long long t2;
-    unsigned long long cu = block_excl_u64<4>(m, wt, &t2);
-    if (cu <= left && cu + m > left) {
-        for (int k = 0; k < 8; k++) {
-            cu += q[k];
-            if (cu > left) {
-                pk = (unsigned long long)(i0 + k);
-                pth = before + cu;
-                break;
-            }
-        }
-    }
-    __syncthreads();
-    const unsigned long long r = pk;
-    if (through) *through = pth;
-    __syncthreads();
-    return r == ~0ull ? -1 : (int)r;
-}
-
-// Ties, pass 2: the id; SK_WALK then emits the token (with the reference's
-// fallback when the draw lies past the last cumulative sum: the first
-// candidate with p > 0 in walk order, i.e. the best key).
-__global__ __launch_bounds__(kBlock) void search_tie_pick_kernel(const SampleArgs a, int kind) {
-    __shared__ unsigned long long best_sh;
-    const DevState st = *a.st;
-    const GenBufs b = gen_bufs(a);
-    const SearchState s = b.ss[kind];
-    const int t = threadIdx.x;
-    int id = -1;
-    unsigned long long through = 0;
-    if (s.id == kSearchRunning) {
-        id = chunk_threshold(
-            a, b.pmass,
-            [&](int i) -> unsigned long long {
-                uint32_t k;
-                unsigned long long w;
-                return kind_kw(kind, b.sc[i], b.pr[i], k, w) && k == s.pfx ? w : 0ull;
-            },
-            s.rest, &through);
-        // the running total from the search's start: the heavier keys'
-        // target - rest, then the ties'
-        through += kind_target(kind, a, st) - s.rest;
-    }
-    if (kind != SK_WALK) {
-        if (t == 0) {
-            SearchState n = s;
-            n.id = s.id == kSearchRunning ? id : -1;
-            n.through = through;
-            b.ss[kind] = n;
-        }
-        return;
-    }
-    if (id < 0) {
-        unsigned long long best = ~0ull;
-        for (int i = t; i < a.V; i += kBlock) {
-            const float p = b.pr[i];
-            if (!(p > 0.0f)) continue;
-            const unsigned long long k = ((unsigned long long)~f32_order(b.sc[i]) << 32) | (uint32_t)i;
-            best = k < best ? k : best;
-        }
-        if (t == 0) best_sh = ~0ull;
-        __syncthreads();
-        atomicMin(&best_sh, best);
-        __syncthreads();
-        id = best_sh == ~0ull ? 0 : (int)(uint32_t)best_sh;
-    }
-    if (t == 0) emit_token(a, id);
-}
-
-// The nucleus cut (src/tensor.rs:1182-1201): ids after the cut in
-// probability order get 0, the kept ones p / (kept mass).
+// The nucleus cut (src/tensor.rs:1192-1200): ranks below the cutoff get
+// p / (kept sum), the others 0
 __global__ __launch_bounds__(kBlock) void sample_renorm_kernel(const SampleArgs a) {
     const GenBufs b = gen_bufs(a);
-    const SearchState s = b.ss[SK_NUCLEUS];
-    if (s.id < 0) return;
-    const float sumk = (float)((double)s.through / kFx);
-    const int base = blockIdx.x * kGenWide + threadIdx.x;
-#pragma unroll
-    for (int j = 0; j < kGenWide / kBlock; j++) {
-        const int i = base + j * kBlock;
-        if (i < a.V) {
-            const float p = b.pr[i];
-            const uint32_t k = f32_order(p);
-            b.pr[i] = (k > s.pfx || (k == s.pfx && i <= s.id)) ? p / sumk : 0.0f;
-        }
+    const ChainOut nc = b.cs[CH_N], kc = b.cs[CH_K];
+    const int cutoff = kc.n;
+    for (int j = blockIdx.x * kBlock + threadIdx.x; j < nc.n; j += gridDim.x * kBlock) {
+        const int id = rank_id(b, j);
+        b.pr[id] = j < cutoff ? b.pr[id] / kc.total : 0.0f;
     }
-}
-
-// Without top-k: the inverse-CDF walk in id order (src/tensor.rs:1203-1212),
-// pass 1: each 2048-id chunk's probability mass.
-__global__ __launch_bounds__(kBlock) void sample_walk_sums_kernel(const SampleArgs a) {
-    __shared__ unsigned long long red4[4];
-    const GenBufs b = gen_bufs(a);
-    const int base = blockIdx.x * kGenWide + threadIdx.x;
-    unsigned long long m = 0;
-#pragma unroll
-    for (int j = 0; j < kGenWide / kBlock; j++) {
-        const int i = base + j * kBlock;
-        if (i < a.V) m += fx(b.pr[i]);
-    }
-    m = wave_sum_u64(m);
-    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) b.pmass[blockIdx.x] = (red4[0] + red4[1]) + (red4[2] + red4[3]);
-}
-
-// pass 2: the id where the running mass first exceeds the draw, emitted
-// (past the last cumulative sum: the lowest id with p > 0).
-__global__ __launch_bounds__(kBlock) void sample_walk_kernel(const SampleArgs a) {
-    __shared__ unsigned long long best_sh;
-    const DevState st = *a.st;
-    const GenBufs b = gen_bufs(a);
-    const int t = threadIdx.x;
-    int pick = chunk_threshold(
-        a, b.pmass, [&](int i) { return fx(b.pr[i]); }, fx(step_draw(a, st.step)), nullptr);
-    if (pick < 0) {
-        unsigned long long best = ~0ull;
-        for (int i = t; i < a.V; i += kBlock)
-            if (b.pr[i] > 0.0f) {
-                best = (unsigned long long)i;
-                break;
-            }
-        if (t == 0) best_sh = ~0ull;
-        __syncthreads();
-        atomicMin(&best_sh, best);
-        __syncthreads();
-        pick = best_sh == ~0ull ? 0 : (int)best_sh;
-    }
-    if (t == 0) emit_token(a, pick);
 }
 
 }  // namespace
@@ -825,29 +1028,37 @@ hipError_t launch_sample(const SampleArgs &a, hipStream_t s) {
         return hipGetLastError();
     }
     if (!a.scratch) return hipErrorInvalidValue;
-    const dim3 wide((a.V + kGenWide - 1) / kGenWide), hist((a.V + kHistIds - 1) / kHistIds);
-    auto search = [&](int kind) {
-        for (int level = 0; level < 3; level++) {
-            hipLaunchKernelGGL(search_hist_kernel, hist, dim3(kBlock), 0, s, a, kind, level);
-            hipLaunchKernelGGL(search_pick_kernel, dim3(1), dim3(kPickThreads), 0, s, a, kind, level);
-        }
-        hipLaunchKernelGGL(search_tie_sums_kernel, wide, dim3(kBlock), 0, s, a, kind);
-        hipLaunchKernelGGL(search_tie_pick_kernel, dim3(1), dim3(kBlock), 0, s, a, kind);
-    };
+    const dim3 wide((a.V + kGenWide - 1) / kGenWide);
     hipLaunchKernelGGL(sample_scale_kernel, wide, dim3(kBlock), 0, s, a);
-    if (a.use_k) search(SK_COUNT);
+    if (a.use_k || a.use_p) {
+        // all ids by (scaled logit, id) descending: a bitonic network, LDS
+        // blocks of kSortBlock keys and one launch per longer stride
+        const int n = sort_n(a.V), nb = n / kSortBlock;
+        const dim3 g((n / 2 + kBlock - 1) / kBlock);
+        hipLaunchKernelGGL(sort_keys_kernel, g, dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL(sort_block_kernel, dim3(nb), dim3(kSortThreads), 0, s, a, 0);
+        for (int size = 2 * kSortBlock; size <= n; size <<= 1) {
+            for (int stride = size / 2; stride >= kSortBlock; stride >>= 1)
+                hipLaunchKernelGGL(sort_global_kernel, g, dim3(kBlock), 0, s, a, size, stride);
+            hipLaunchKernelGGL(sort_block_kernel, dim3(nb), dim3(kSortThreads), 0, s, a, size);
+        }
+    }
+    // a running sum: chunk sums, chunk and group metadata, the walk
+    const dim3 chunks((a.V + kChainChunk - 1) / kChainChunk);
+    auto chain = [&](int kind) {
+        hipLaunchKernelGGL(chain_sum_kernel, chunks, dim3(64), 0, s, a, kind);
+        hipLaunchKernelGGL(chain_quant_kernel, chunks, dim3(64), 0, s, a, kind);
+        hipLaunchKernelGGL(chain_walk_kernel, dim3(1), dim3(kChainThreads), 0, s, a, kind);
+    };
     hipLaunchKernelGGL(sample_exp_kernel, wide, dim3(kBlock), 0, s, a);
+    chain(CH_Z);
     hipLaunchKernelGGL(sample_norm_kernel, wide, dim3(kBlock), 0, s, a);
     if (a.use_p) {
-        search(SK_NUCLEUS);
+        chain(CH_N);
+        chain(CH_K);
         hipLaunchKernelGGL(sample_renorm_kernel, wide, dim3(kBlock), 0, s, a);
     }
-    if (a.use_k) {
-        search(SK_WALK);
-    } else {
-        hipLaunchKernelGGL(sample_walk_sums_kernel, wide, dim3(kBlock), 0, s, a);
-        hipLaunchKernelGGL(sample_walk_kernel, dim3(1), dim3(kBlock), 0, s, a);
-    }
+    chain(CH_W);
     return hipGetLastError();
 }
 
