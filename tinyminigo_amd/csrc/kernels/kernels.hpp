@@ -255,25 +255,21 @@ constexpr int kSampleSlice = 2048;
 constexpr int kSampleSelectKeys = 8192;
 // Largest vocabulary either sampling path takes.
 constexpr int kSampleMaxVocab = 262144;
-// The whole-vocabulary sampler sorts (scaled logit, id) keys with a bitonic
-// network over sort_n(V) keys (a power of two), in LDS blocks of kSortBlock
-// keys sorted by kSortThreads threads.
-constexpr int kSortBlock = 8192;
-constexpr int kSortThreads = 1024;
-constexpr int sort_n(int V) {
-    int n = kSortBlock;
-    while (n < V) n <<= 1;
-    return n;
-}
+// The whole-vocabulary sampler's radix sort: kRadixBlock keys per block
+// (at most 256 blocks), the offsets scanned by kRadixScanThreads threads.
+constexpr int kRadixBlock = 1024;
+constexpr int kRadixScanThreads = 1024;
+constexpr size_t kSampleRadixCounts = 256 * (kSampleMaxVocab / kRadixBlock);
 // The running sums' metadata: per 1024-term chunk (256 chunks) 152 bytes,
 // per 64-term group and binade (2 x 4096) 16 bytes.
 constexpr size_t kSampleChainChunkBytes = 256 * 152;
 constexpr size_t kSampleChainGroupBytes = 2 * 4096 * 16;
 // Scratch bytes of the whole-vocabulary sampler for a vocabulary of V ids:
 // scaled logits and probabilities [V] f32, 128 partial maxima, 4 running-sum
-// results of 16 bytes, the sort keys and the running sums' metadata.
+// results of 16 bytes, two sort key buffers [V] u64, the radix counts and
+// the running sums' metadata.
 constexpr size_t kSampleScratchBytes(size_t V) {
-    return V * 8 + 576 + (size_t)sort_n((int)V) * 8 + kSampleChainChunkBytes + kSampleChainGroupBytes;
+    return V * 8 + 576 + V * 16 + kSampleRadixCounts * 4 + kSampleChainChunkBytes + kSampleChainGroupBytes;
 }
 
 struct SampleArgs {

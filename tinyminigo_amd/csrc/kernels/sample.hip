@@ -347,15 +347,17 @@ struct ChainOut {
 };
 
 // a.scratch: sc [V] | pr [V] | max partials [128] | ChainOut [4] | sort
-// keys [sort_n(V)] (8-byte aligned: V * 8 + 512 + 64 bytes before them) |
-// running-sum chunk metadata | running-sum group metadata
+// keys [V] | keys2 [V] (8-byte aligned: V * 8 + 512 + 64 bytes before them) |
+// radix counts [kSampleRadixCounts] | running-sum chunk metadata |
+// running-sum group metadata
 struct ChainChunkMeta;
 struct ChainGroupMeta;
 
 struct GenBufs {
     float *sc, *pr, *pmax;
     ChainOut *cs;
-    unsigned long long *keys;
+    unsigned long long *keys, *keys2;  // sort keys [V], and the radix passes' other buffer [V]
+    uint32_t *radix;                    // radix digit counts / offsets [256][blocks]
     ChainChunkMeta *cmeta;  // [kChainMaxChunks]
     ChainGroupMeta *gmeta;  // [2][kChainMaxChunks * kChainPer]
 };
@@ -367,7 +369,9 @@ __device__ __forceinline__ GenBufs gen_bufs(const SampleArgs &a) {
     b.pmax = a.scratch + 2 * (size_t)a.V;
     b.cs = reinterpret_cast<ChainOut *>(b.pmax + kGenParts);
     b.keys = reinterpret_cast<unsigned long long *>(b.cs + 4);
-    b.cmeta = reinterpret_cast<ChainChunkMeta *>(b.keys + sort_n(a.V));
+    b.keys2 = b.keys + a.V;
+    b.radix = reinterpret_cast<uint32_t *>(b.keys2 + a.V);
+    b.cmeta = reinterpret_cast<ChainChunkMeta *>(b.radix + kSampleRadixCounts);
     b.gmeta = reinterpret_cast<ChainGroupMeta *>(reinterpret_cast<char *>(b.cmeta) + kSampleChainChunkBytes);
     return b;
 }
@@ -378,6 +382,20 @@ __device__ __forceinline__ float wg_reduce(float v, bool is_max, float *red4) {
     __syncthreads();
     return is_max ? fmaxf(fmaxf(red4[0], red4[1]), fmaxf(red4[2], red4[3])) : (red4[0] + red4[1]) + (red4[2] + red4[3]);
 }
+
+// Inclusive prefix sum over the wavefront's 64 lanes: shifts within rows of
+// 16 lanes, then each row's total broadcast to the rows above it.
+__device__ __forceinline__ uint32_t wave_incl_u32(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);  // row_shr:1
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);  // row_shr:2
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true);  // row_shr:4
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true);  // row_shr:8
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
+    return v;
+}
+
+__device__ __forceinline__ uint32_t lane_u32(uint32_t v, int i) { return (uint32_t)__builtin_amdgcn_readlane((int)v, i); }
 
 // pass 1: scaled logits (penalty, temperature; src/tensor.rs:1142-1154,
 // :1168), the workgroup maximum, and pr cleared
@@ -420,65 +438,159 @@ __device__ float scaled_max(const SampleArgs &a, const GenBufs &b, float *red4) 
 }
 
 // ---- the sort: keys (scaled logit order, then ~id) descending --------------
+//
+// A stable LSD radix sort of the V keys on their upper 32 bits (the scaled
+// logit's order), descending, in four passes of 8-bit digits; equal values
+// keep id order.  Per pass: per-block digit counts (kRadixBlock keys per
+// block), one exclusive scan over them in (digit, block) order, and a stable
+// scatter.  Passes alternate between keys and keys2 and end in keys.
 
 // keys[i] = argmax_key(scaled, i) for ids with a non-NaN scaled logit, 0 for
-// NaN ones and for the padding up to sort_n(V)
+// NaN ones (they sort last)
 __global__ __launch_bounds__(kBlock) void sort_keys_kernel(const SampleArgs a) {
     const GenBufs b = gen_bufs(a);
-    const int n = sort_n(a.V);
-    for (int i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) {
-        unsigned long long k = 0ull;
-        if (i < a.V) {
-            const float v = b.sc[i];
-            if (v == v) k = argmax_key(v, (uint32_t)i);
-        }
-        b.keys[i] = k;
+    for (int i = blockIdx.x * kBlock + threadIdx.x; i < a.V; i += gridDim.x * kBlock) {
+        const float v = b.sc[i];
+        b.keys[i] = v == v ? argmax_key(v, (uint32_t)i) : 0ull;
     }
 }
 
-// compare-exchange of a bitonic network sorting descending: in stage `size`
-// the pair (i, i + stride) is ordered descending when (i & size) == 0
-__device__ __forceinline__ void bitonic_cx(unsigned long long &x, unsigned long long &y, bool desc) {
-    const bool swap = desc ? x < y : x > y;
-    if (swap) {
-        const unsigned long long t = x;
-        x = y;
-        y = t;
-    }
+__device__ __forceinline__ uint32_t radix_digit(unsigned long long k, int pass) {
+    return (~(uint32_t)(k >> 32) >> (8 * pass)) & 255u;  // ascending digits = descending keys
 }
 
-// stages size = 2 .. kSortBlock within each block of kSortBlock keys (LDS),
-// or, with size0 > kSortBlock, stage size0's strides below kSortBlock
-__global__ __launch_bounds__(kSortThreads) void sort_block_kernel(const SampleArgs a, int size0) {
-    __shared__ unsigned long long sk[kSortBlock];
+__device__ __forceinline__ void radix_src_dst(const GenBufs &b, int pass, const unsigned long long **src,
+                                              unsigned long long **dst) {
+    *src = (pass & 1) ? b.keys2 : b.keys;
+    *dst = (pass & 1) ? b.keys : b.keys2;
+}
+
+// digit counts of block blockIdx.x, into off[digit * nb + block]
+__global__ __launch_bounds__(kBlock) void radix_hist_kernel(const SampleArgs a, int pass) {
+    __shared__ uint32_t h[256];
     const GenBufs b = gen_bufs(a);
-    unsigned long long *g = b.keys + (size_t)blockIdx.x * kSortBlock;
-    const int base = blockIdx.x * kSortBlock;
-    for (int i = threadIdx.x; i < kSortBlock; i += kSortThreads) sk[i] = g[i];
+    const unsigned long long *src;
+    unsigned long long *dst;
+    radix_src_dst(b, pass, &src, &dst);
+    const int nb = (a.V + kRadixBlock - 1) / kRadixBlock;
+    h[threadIdx.x] = 0u;
     __syncthreads();
-    const int s_lo = size0 > kSortBlock ? size0 : 2, s_hi = size0 > kSortBlock ? size0 : kSortBlock;
-    for (int size = s_lo; size <= s_hi; size <<= 1) {
-        for (int stride = min(size, kSortBlock) >> 1; stride > 0; stride >>= 1) {
-            for (int p = threadIdx.x; p < kSortBlock / 2; p += kSortThreads) {
-                const int i = (p / stride) * 2 * stride + (p % stride);
-                bitonic_cx(sk[i], sk[i + stride], ((base + i) & size) == 0);
-            }
-            __syncthreads();
-        }
+#pragma unroll
+    for (int r = 0; r < kRadixBlock / kBlock; r++) {
+        const int i = blockIdx.x * kRadixBlock + r * kBlock + threadIdx.x;
+        if (i < a.V) atomicAdd(&h[radix_digit(src[i], pass)], 1u);
     }
-    for (int i = threadIdx.x; i < kSortBlock; i += kSortThreads) g[i] = sk[i];
+    __syncthreads();
+    b.radix[threadIdx.x * nb + blockIdx.x] = h[threadIdx.x];
 }
 
-// one stride >= kSortBlock of stage `size`, across blocks
-__global__ __launch_bounds__(kBlock) void sort_global_kernel(const SampleArgs a, int size, int stride) {
+// exclusive prefix over off[0 .. 256 nb), in place (one workgroup): tile r
+// of kRadixScanThreads values is thread-indexed (coalesced); each wavefront
+// scans its 64 values of every tile, one wavefront scans the (tile,
+// wavefront) totals in order, and the tiles are read and scanned again to
+// write the result
+constexpr int kRadixTiles = (int)(kSampleRadixCounts / kRadixScanThreads);
+__global__ __launch_bounds__(kRadixScanThreads) void radix_scan_kernel(const SampleArgs a) {
+    constexpr int NW = kRadixScanThreads / 64;
+    __shared__ uint32_t wt[kRadixTiles * NW];
     const GenBufs b = gen_bufs(a);
-    const int half = sort_n(a.V) / 2;
-    for (int p = blockIdx.x * kBlock + threadIdx.x; p < half; p += gridDim.x * kBlock) {
-        const int i = (p / stride) * 2 * stride + (p % stride);
-        unsigned long long x = b.keys[i], y = b.keys[i + stride];
-        bitonic_cx(x, y, (i & size) == 0);
-        b.keys[i] = x;
-        b.keys[i + stride] = y;
+    const int nb = (a.V + kRadixBlock - 1) / kRadixBlock;
+    const int total = 256 * nb, tiles = (total + kRadixScanThreads - 1) / kRadixScanThreads;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    for (int r0 = 0; r0 < tiles; r0 += 4) {  // four tiles' loads in flight at a time
+        uint32_t v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = (r0 + k) * kRadixScanThreads + t;
+            v[k] = r0 + k < tiles && i < total ? b.radix[i] : 0u;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t incl = wave_incl_u32(v[k]);
+            if (lane == 63 && r0 + k < tiles) wt[(r0 + k) * NW + w] = incl;
+        }
+    }
+    __syncthreads();
+    if (w == 0) {
+        // exclusive scan of tiles * NW totals, in (tile, wavefront) order
+        constexpr int PER = kRadixTiles * NW / 64;
+        uint32_t x[PER], sum = 0u;
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const int i = lane * PER + k;
+            x[k] = i < tiles * NW ? wt[i] : 0u;
+            sum += x[k];
+        }
+        uint32_t run = wave_incl_u32(sum) - sum;
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const int i = lane * PER + k;
+            if (i < tiles * NW) wt[i] = run;
+            run += x[k];
+        }
+    }
+    __syncthreads();
+    for (int r0 = 0; r0 < tiles; r0 += 4) {
+        uint32_t v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = (r0 + k) * kRadixScanThreads + t;
+            v[k] = r0 + k < tiles && i < total ? b.radix[i] : 0u;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = (r0 + k) * kRadixScanThreads + t;
+            const uint32_t ex = wave_incl_u32(v[k]) - v[k];
+            if (r0 + k < tiles && i < total) b.radix[i] = wt[(r0 + k) * NW + w] + ex;
+        }
+    }
+}
+
+// stable scatter of block blockIdx.x: rounds of kBlock keys in id order;
+// within a round, a key's rank among equal digits is its wavefront's earlier
+// lanes (ballot matching) plus the earlier wavefronts' counts
+__global__ __launch_bounds__(kBlock) void radix_scatter_kernel(const SampleArgs a, int pass) {
+    __shared__ uint32_t cnt[256];
+    __shared__ uint32_t wc[kBlock / 64][256];
+    const GenBufs b = gen_bufs(a);
+    const unsigned long long *src;
+    unsigned long long *dst;
+    radix_src_dst(b, pass, &src, &dst);
+    const int nb = (a.V + kRadixBlock - 1) / kRadixBlock;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    cnt[t] = b.radix[t * nb + blockIdx.x];
+#pragma unroll
+    for (int k = 0; k < kBlock / 64; k++) wc[k][t] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kRadixBlock / kBlock; r++) {
+        const int i = blockIdx.x * kRadixBlock + r * kBlock + t;
+        const bool valid = i < a.V;
+        const unsigned long long key = valid ? src[i] : 0ull;
+        const uint32_t d = radix_digit(key, pass);
+        unsigned long long peers = __ballot(valid);
+#pragma unroll
+        for (int bit = 0; bit < 8; bit++) {
+            const unsigned long long m = __ballot((d >> bit) & 1u);
+            peers &= ((d >> bit) & 1u) ? m : ~m;
+        }
+        if (valid && !(peers & below)) wc[w][d] = (uint32_t)__builtin_popcountll(peers);
+        __syncthreads();
+        if (valid) {
+            uint32_t pos = cnt[d] + (uint32_t)__builtin_popcountll(peers & below);
+            for (int k = 0; k < w; k++) pos += wc[k][d];
+            dst[pos] = key;
+        }
+        __syncthreads();
+        uint32_t add = 0u;
+#pragma unroll
+        for (int k = 0; k < kBlock / 64; k++) {
+            add += wc[k][t];
+            wc[k][t] = 0u;
+        }
+        cnt[t] += add;
+        __syncthreads();
     }
 }
 
@@ -489,21 +601,6 @@ __device__ __forceinline__ int rank_id(const GenBufs &b, int j) {
 }
 
 __device__ __forceinline__ bool use_topk(const DevState &st, int V) { return st.top_k > 0 && st.top_k < V; }
-
-// softmax numerators over the candidates (src/tensor.rs:1177-1179, :1057):
-// e = expf(s - M); without top-k every id (by id), with it the ranks below k
-__global__ __launch_bounds__(kBlock) void sample_exp_kernel(const SampleArgs a) {
-    __shared__ float red4[4];
-    const DevState st = *a.st;
-    const GenBufs b = gen_bufs(a);
-    const float M = scaled_max(a, b, red4);
-    const bool k_on = use_topk(st, a.V);
-    const int n = k_on ? st.top_k : a.V;
-    for (int j = blockIdx.x * kBlock + threadIdx.x; j < n; j += gridDim.x * kBlock) {
-        const int id = k_on ? rank_id(b, j) : j;
-        b.pr[id] = ref_expf(b.sc[id] - M);
-    }
-}
 
 // ---- the f32 running sum --------------------------------------------------
 //
@@ -582,20 +679,6 @@ static_assert(sizeof(ChainGroupMeta) * 2 * kChainMaxChunks * kChainPer == kSampl
 
 __device__ __forceinline__ ChainChunkMeta *chain_chunks(const GenBufs &b) { return b.cmeta; }
 __device__ __forceinline__ ChainGroupMeta *chain_groups(const GenBufs &b) { return b.gmeta; }
-
-// Inclusive prefix sum over the wavefront's 64 lanes: shifts within rows of
-// 16 lanes, then each row's total broadcast to the rows above it.
-__device__ __forceinline__ uint32_t wave_incl_u32(uint32_t v) {
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);  // row_shr:1
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);  // row_shr:2
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true);  // row_shr:4
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true);  // row_shr:8
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);  // row_bcast:15 -> rows 1, 3
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);  // row_bcast:31 -> rows 2, 3
-    return v;
-}
-
-__device__ __forceinline__ uint32_t lane_u32(uint32_t v, int i) { return (uint32_t)__builtin_amdgcn_readlane((int)v, i); }
 
 // One wavefront adds terms j0 .. j0 + 63 (lane l holds x of j0 + l; terms at
 // or past n are absent) to the running sum whose bits are *sb.  With a
@@ -737,11 +820,11 @@ __global__ __launch_bounds__(64) void chain_sum_kernel(const SampleArgs a, int k
     if (lane == 0) chain_chunks(b)[c].dsum = d;
 }
 
-__global__ __launch_bounds__(64) void chain_quant_kernel(const SampleArgs a, int kind) {
+__global__ __launch_bounds__(128) void chain_quant_kernel(const SampleArgs a, int kind) {
     const DevState st = *a.st;
     const GenBufs b = gen_bufs(a);
     const ChainSpec cs = chain_spec(a, b, st, kind);
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63, bin = threadIdx.x >> 6;  // wavefront 0: bin 0 and the chunk, 1: bin 1
     const int c = blockIdx.x;
     if (c * kChainChunk >= cs.n) return;
     ChainChunkMeta *cm = chain_chunks(b);
@@ -765,8 +848,7 @@ __global__ __launch_bounds__(64) void chain_quant_kernel(const SampleArgs a, int
     uint32_t run = 0u;
     int nt = 0;
     bool cflag = false;
-#pragma unroll
-    for (int bin = 0; bin < 2; bin++) {
+    {
 #pragma unroll
         for (int i = 0; i < kChainPer; i++) {
             bool tie = false, fl = false;
@@ -802,7 +884,7 @@ __global__ __launch_bounds__(64) void chain_quant_kernel(const SampleArgs a, int
             }
         }
     }
-    if (lane == 0) {
+    if (bin == 0 && lane == 0) {
         cm[c].q = run;
         cm[c].ntie = nt;
         cm[c].flag = cflag || nt > kChainTies;
@@ -887,46 +969,54 @@ __global__ __launch_bounds__(kChainThreads) void chain_walk_kernel(const SampleA
     }
     __syncthreads();
     if (w == 0) {
-        // the chunks' metadata in registers: lane l holds chunks l + 64 r
-        constexpr int R = kChainMaxChunks / 64;
-        uint32_t rq[R], rnt[R], rfl[R], reg[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int c = r * 64 + lane;
-            rq[r] = c < nch ? cq[c] : 0u;
-            rnt[r] = c < nch ? (uint32_t)cnt[c] : 0u;
-            rfl[r] = c < nch ? (uint32_t)cfl[c] : 1u;
-            reg[r] = c < nch ? (uint32_t)ceg[c] : 0u;
-        }
-        auto meta = [&](const uint32_t(&v)[R], int c) {
-            const int r = c >> 6;
-            const uint32_t x = r == 0 ? v[0] : r == 1 ? v[1] : r == 2 ? v[2] : v[3];
-            return lane_u32(x, c & 63);
-        };
         uint32_t s = 0u;  // +0.0
         int found = -1;
         float at = 0.0f;
-        for (int c = 0; c < nch && found < 0; c++) {
-            const int es = (int)(s >> 23);
-            const int eg = (int)meta(reg, c);
-            if (es < 255 && !meta(rfl, c)) {
+        int c = 0;
+        while (c < nch && found < 0) {
+            // a run of chunks that each advance in one step without ties:
+            // lanes hold chunks c .. c + 63; the integer sums are prefix-summed
+            // and the run ends at the first chunk that does not qualify
+            {
+                const int cl = c + lane;
+                const bool in = cl < nch;
+                const int es = (int)(s >> 23);
                 const int eu = es > 1 ? es : 1;
                 const uint32_t m = es ? ((s & 0x7fffffu) | 0x800000u) : s;
-                if (eu == eg) {
-                    uint32_t adj = 0u;
-                    const int nt = (int)meta(rnt, c);
-                    for (int i = 0; i < nt; i++) adj += (m + ties[c][i] + adj) & 1u;
-                    const uint32_t mend = m + meta(rq, c) + adj;  // < 2^26: no wrap
-                    if (mend < (1u << 24)) {
-                        const uint32_t sn = ((uint32_t)(eu - 1) << 23) + mend;
-                        if (!cs.has_t || !(__uint_as_float(sn) > cs.T)) {
-                            s = sn;
-                            continue;
+                const bool ok = in && es < 255 && !cfl[cl] && ceg[cl] == eu && cnt[cl] == 0;
+                const uint32_t incl = wave_incl_u32(ok ? cq[cl] : 0u);  // < 64 * 2^25: no wrap
+                const uint32_t sl = ((uint32_t)(eu - 1) << 23) + m + incl;
+                const bool good = ok && m + incl < (1u << 24) && !(cs.has_t && __uint_as_float(sl) > cs.T);
+                const unsigned long long bad = __ballot(in && !good);
+                const int f = bad ? __builtin_ctzll(bad) : min(64, nch - c);
+                if (f > 0) s = lane_u32(sl, f - 1);
+                c += f;
+                if (f == 64 || c >= nch) continue;
+            }
+            // chunk c: in one step with its ties settled, or group by group
+            {
+                const int es = (int)(s >> 23);
+                const int eg = ceg[c];
+                if (es < 255 && !cfl[c]) {
+                    const int eu = es > 1 ? es : 1;
+                    const uint32_t m = es ? ((s & 0x7fffffu) | 0x800000u) : s;
+                    if (eu == eg) {
+                        uint32_t adj = 0u;
+                        const int nt = cnt[c];
+                        for (int i = 0; i < nt; i++) adj += (m + ties[c][i] + adj) & 1u;
+                        const uint32_t mend = m + cq[c] + adj;  // < 2^26: no wrap
+                        if (mend < (1u << 24)) {
+                            const uint32_t sn = ((uint32_t)(eu - 1) << 23) + mend;
+                            if (!cs.has_t || !(__uint_as_float(sn) > cs.T)) {
+                                s = sn;
+                                c++;
+                                continue;
+                            }
                         }
                     }
                 }
             }
-            // group by group: lanes 0-15 hold the groups' bin-0 data, 16-31 bin 1
+            // lanes 0-15 hold the groups' bin-0 metadata, 16-31 their bin-1
             float xs[kChainPer];
             ChainGroupMeta g{};
             const int sl = slot[c];
@@ -939,13 +1029,39 @@ __global__ __launch_bounds__(kChainThreads) void chain_walk_kernel(const SampleA
                 if (lane < 2 * kChainPer)
                     g = gm[(size_t)(lane / kChainPer) * kChainMaxChunks * kChainPer + c * kChainPer + lane % kChainPer];
             }
-            for (int i = 0; i < kChainPer; i++) {
+            int i = 0;
+            while (i < kChainPer && found < 0) {
+                // a run of groups i .. that each advance in one step without
+                // ties, under whichever bin matches the running binade
+                {
+                    const int gi = i + lane;
+                    const bool in = lane < kChainPer - i;
+                    const int es = (int)(s >> 23);
+                    const int eu = es > 1 ? es : 1;
+                    const uint32_t m = es ? ((s & 0x7fffffu) | 0x800000u) : s;
+                    const int egi = __shfl((int)g.eguess, gi & (kChainPer - 1), 64);
+                    const int bin = eu - egi;
+                    const int srcl = (bin == 1 ? kChainPer : 0) + (gi & (kChainPer - 1));
+                    const int ntf = __shfl((int)g.ntie_flag, srcl, 64);
+                    const uint32_t q = (uint32_t)__shfl((int)g.q, srcl, 64);
+                    const bool ok = in && es < 255 && (bin == 0 || bin == 1) && ntf == 0;
+                    const uint32_t incl = wave_incl_u32(ok ? q : 0u);
+                    const uint32_t sl2 = ((uint32_t)(eu - 1) << 23) + m + incl;
+                    const bool good = ok && m + incl < (1u << 24) && !(cs.has_t && __uint_as_float(sl2) > cs.T);
+                    const unsigned long long bad = __ballot(in && !good);
+                    const int f = bad ? __builtin_ctzll(bad) : kChainPer - i;
+                    if (f > 0) s = lane_u32(sl2, f - 1);
+                    i += f;
+                    if (i >= kChainPer) break;
+                }
+                // group i: in one step with up to kGroupTies ties settled, or term by term
                 const int es2 = (int)(s >> 23);
                 const int eu = es2 > 1 ? es2 : 1;
                 const int bin = eu - (int)lane_u32((uint32_t)(int)g.eguess, i);
+                bool done = false;
                 if (es2 < 255 && (bin == 0 || bin == 1)) {
                     const int src = bin * kChainPer + i;
-                    const int ntf = (int)lane_u32((uint32_t)g.ntie_flag, src);
+                    const int ntf = (int)lane_u32((uint32_t)(int)g.ntie_flag, src);
                     if (ntf >= 0 && ntf <= kGroupTies) {
                         const uint32_t m = es2 ? ((s & 0x7fffffu) | 0x800000u) : s;
                         uint32_t adj = 0u;
@@ -956,14 +1072,15 @@ __global__ __launch_bounds__(kChainThreads) void chain_walk_kernel(const SampleA
                             const uint32_t sn = ((uint32_t)(eu - 1) << 23) + mend;
                             if (!cs.has_t || !(__uint_as_float(sn) > cs.T)) {
                                 s = sn;
-                                continue;
+                                done = true;
                             }
                         }
                     }
                 }
-                found = chain_group(xs[i], c * kChainChunk + i * 64, n, cs.has_t, cs.T, &s, &at);
-                if (found >= 0) break;
+                if (!done) found = chain_group(xs[i], c * kChainChunk + i * 64, n, cs.has_t, cs.T, &s, &at);
+                i++;
             }
+            c++;
         }
         if (lane == 0) {
             ChainOut o;
@@ -994,11 +1111,71 @@ __global__ __launch_bounds__(kChainThreads) void chain_walk_kernel(const SampleA
     if (t == 0) emit_token(a, cs.by_rank ? rank_id(b, pick) : pick);
 }
 
+// Block-wide double sum of one value per thread (kBlock threads), returned
+// to thread 0.
+__device__ __forceinline__ double block_sum_d(double d, double *red4) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) d += __shfl_xor(d, off, 64);
+    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = d;
+    __syncthreads();
+    return (red4[0] + red4[1]) + (red4[2] + red4[3]);
+}
+
+// softmax numerators over the candidates (src/tensor.rs:1177-1179, :1057):
+// e = expf(s - M) in candidate order (ids without top-k, ranks below k with
+// it), one kChainChunk-term chunk per workgroup; each chunk's double sum
+// goes to the running sum Z's metadata (chain_sum_kernel's work)
+__global__ __launch_bounds__(kBlock) void sample_exp_kernel(const SampleArgs a) {
+    __shared__ float red4[4];
+    __shared__ double dred4[4];
+    const DevState st = *a.st;
+    const GenBufs b = gen_bufs(a);
+    const float M = scaled_max(a, b, red4);
+    const bool k_on = use_topk(st, a.V);
+    const int n = k_on ? st.top_k : a.V;
+    const int c = blockIdx.x;
+    if (c * kChainChunk >= n) return;
+    double d = 0.0;
+#pragma unroll
+    for (int r = 0; r < kChainChunk / kBlock; r++) {
+        const int j = c * kChainChunk + r * kBlock + threadIdx.x;
+        if (j < n) {
+            const int id = k_on ? rank_id(b, j) : j;
+            const float e = ref_expf(b.sc[id] - M);
+            b.pr[id] = e;
+            d += (double)e;
+        }
+    }
+    d = block_sum_d(d, dred4);
+    if (threadIdx.x == 0) chain_chunks(b)[c].dsum = d;
+}
+
 // p = e / Z over all ids (non-candidates hold 0)
+// in candidate order, one chunk per workgroup; without a nucleus cut the
+// chunk sums are those of the walk's running sum
 __global__ __launch_bounds__(kBlock) void sample_norm_kernel(const SampleArgs a) {
+    __shared__ double dred4[4];
+    const DevState st = *a.st;
     const GenBufs b = gen_bufs(a);
     const float Z = b.cs[CH_Z].total;
-    for (int i = blockIdx.x * kBlock + threadIdx.x; i < a.V; i += gridDim.x * kBlock) b.pr[i] = b.pr[i] / Z;
+    const bool k_on = use_topk(st, a.V);
+    const int n = k_on ? st.top_k : a.V;
+    const int c = blockIdx.x;
+    if (c * kChainChunk >= n) return;
+    double d = 0.0;
+#pragma unroll
+    for (int r = 0; r < kChainChunk / kBlock; r++) {
+        const int j = c * kChainChunk + r * kBlock + threadIdx.x;
+        if (j < n) {
+            const int id = k_on ? rank_id(b, j) : j;
+            const float p = b.pr[id] / Z;
+            b.pr[id] = p;
+            d += (double)p;
+        }
+    }
+    if (a.use_p) return;
+    d = block_sum_d(d, dred4);
+    if (threadIdx.x == 0) chain_chunks(b)[c].dsum = d;
 }
 
 // The nucleus cut (src/tensor.rs:1192-1200): ranks below the cutoff get
@@ -1031,34 +1208,33 @@ hipError_t launch_sample(const SampleArgs &a, hipStream_t s) {
     const dim3 wide((a.V + kGenWide - 1) / kGenWide);
     hipLaunchKernelGGL(sample_scale_kernel, wide, dim3(kBlock), 0, s, a);
     if (a.use_k || a.use_p) {
-        // all ids by (scaled logit, id) descending: a bitonic network, LDS
-        // blocks of kSortBlock keys and one launch per longer stride
-        const int n = sort_n(a.V), nb = n / kSortBlock;
-        const dim3 g((n / 2 + kBlock - 1) / kBlock);
-        hipLaunchKernelGGL(sort_keys_kernel, g, dim3(kBlock), 0, s, a);
-        hipLaunchKernelGGL(sort_block_kernel, dim3(nb), dim3(kSortThreads), 0, s, a, 0);
-        for (int size = 2 * kSortBlock; size <= n; size <<= 1) {
-            for (int stride = size / 2; stride >= kSortBlock; stride >>= 1)
-                hipLaunchKernelGGL(sort_global_kernel, g, dim3(kBlock), 0, s, a, size, stride);
-            hipLaunchKernelGGL(sort_block_kernel, dim3(nb), dim3(kSortThreads), 0, s, a, size);
+        // all ids by (scaled logit, id) descending
+        const dim3 rb((a.V + kRadixBlock - 1) / kRadixBlock);
+        hipLaunchKernelGGL(sort_keys_kernel, wide, dim3(kBlock), 0, s, a);
+        for (int pass = 0; pass < 4; pass++) {
+            hipLaunchKernelGGL(radix_hist_kernel, rb, dim3(kBlock), 0, s, a, pass);
+            hipLaunchKernelGGL(radix_scan_kernel, dim3(1), dim3(kRadixScanThreads), 0, s, a);
+            hipLaunchKernelGGL(radix_scatter_kernel, rb, dim3(kBlock), 0, s, a, pass);
         }
     }
     // a running sum: chunk sums, chunk and group metadata, the walk
     const dim3 chunks((a.V + kChainChunk - 1) / kChainChunk);
-    auto chain = [&](int kind) {
-        hipLaunchKernelGGL(chain_sum_kernel, chunks, dim3(64), 0, s, a, kind);
-        hipLaunchKernelGGL(chain_quant_kernel, chunks, dim3(64), 0, s, a, kind);
+    auto chain = [&](int kind, bool sums) {
+        if (sums) hipLaunchKernelGGL(chain_sum_kernel, chunks, dim3(64), 0, s, a, kind);
+        hipLaunchKernelGGL(chain_quant_kernel, chunks, dim3(128), 0, s, a, kind);
         hipLaunchKernelGGL(chain_walk_kernel, dim3(1), dim3(kChainThreads), 0, s, a, kind);
     };
-    hipLaunchKernelGGL(sample_exp_kernel, wide, dim3(kBlock), 0, s, a);
-    chain(CH_Z);
-    hipLaunchKernelGGL(sample_norm_kernel, wide, dim3(kBlock), 0, s, a);
+    // the exp and norm passes leave the chunk sums of Z and (without a
+    // nucleus cut) of the walk
+    hipLaunchKernelGGL(sample_exp_kernel, chunks, dim3(kBlock), 0, s, a);
+    chain(CH_Z, false);
+    hipLaunchKernelGGL(sample_norm_kernel, chunks, dim3(kBlock), 0, s, a);
     if (a.use_p) {
-        chain(CH_N);
-        chain(CH_K);
+        chain(CH_N, true);
+        chain(CH_K, true);
         hipLaunchKernelGGL(sample_renorm_kernel, wide, dim3(kBlock), 0, s, a);
     }
-    chain(CH_W);
+    chain(CH_W, a.use_p != 0);
     return hipGetLastError();
 }
 
