@@ -308,6 +308,101 @@ __global__ __launch_bounds__(kGWaves * 64) void gemm_dma_kernel(const GemmArgs a
             gemm_store<EPI>(a, m0 + wm * 64 + i * 16 + q4 * 4, n0 + wn * NJ * 16 + j * 16 + r, acc[i][j]);
 }
 
+// Large-tile MFMA GEMM for long prompts: workgroup tile 256 weight rows x
+// 256 tokens, K in steps of 32.  The global -> LDS DMA path carries about
+// 45 GB/s per CU (measured), and a step's W, Bhi and Blo tiles are 48 KB
+// either way; the 256 x 256 tile does twice the MFMA work of the 128 x 128
+// one for them.  Three-stage ring of 48 KB stages, one barrier per step;
+// LDS rows are 64 B (32 bf16) with the four 16-byte chunks XOR-swizzled by
+// (row >> 2) & 3, so a fragment read's 16 rows hit 16 distinct bank groups,
+// and a DMA wave-instruction fills 16 rows (1 KB).  Wave w owns rows
+// 128 (w & 1) .. +127 and tokens 64 (w >> 1) .. +63 (8 x 4 MFMA fragments).
+constexpr int kBM = 256, kBN = 256, kBK = 32;
+constexpr int kBStages = 3;
+constexpr int kBTile = kBM * kBK * 2;  // bytes of one 256 x 32 bf16 tile (kBN == kBM)
+static_assert(kBM == kBN, "W and B tiles share the staging layout");
+
+template <int EPI>
+__global__ __launch_bounds__(kGWaves * 64) void gemm_big_kernel(const GemmArgs a) {
+    constexpr int DPW = kBTile / 1024 / kGWaves;  // DMA instructions per wave per tile
+    constexpr int FI = 8, FJ = 4;                 // row / token fragments per wave
+    static_assert(3 * DPW <= 15, "vmcnt immediate");
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[kBStages * 3 * kBTile];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int m0 = blockIdx.x * kBM, n0 = blockIdx.y * kBN;
+    const int K = a.K;
+    const int nsteps = K / kBK;
+    // DMA: wave w's instruction i fills rows (DPW w + i) * 16 .. +15 of a
+    // tile; lane l writes row (DPW w + i) * 16 + (l >> 2), physical chunk
+    // l & 3, which holds logical chunk (l & 3) ^ ((row >> 2) & 3)
+    uint32_t off[2][DPW];
+#pragma unroll
+    for (int i = 0; i < DPW; i++) {
+        const int row = (wave * DPW + i) * 16 + (lane >> 2);
+        const int lc = (lane & 3) ^ ((row >> 2) & 3);
+        off[0][i] = (uint32_t)min(m0 + row, a.M - 1) * (uint32_t)K + lc * 8;
+        off[1][i] = (uint32_t)min(n0 + row, a.N - 1) * (uint32_t)K + lc * 8;
+    }
+    auto issue = [&](int stage, int k0) {
+#pragma unroll
+        for (int x = 0; x < 3; x++) {
+            const uint16_t *base = x == 0 ? a.W : (x == 1 ? a.Bhi : a.Blo);
+#pragma unroll
+            for (int i = 0; i < DPW; i++)
+                __builtin_amdgcn_global_load_lds(base + off[x == 0 ? 0 : 1][i] + k0,
+                                                 smem + (stage * 3 + x) * kBTile + (wave * DPW + i) * 1024, 16, 0, 0);
+        }
+    };
+    issue(0, 0);
+    if (nsteps > 1) issue(1, kBK);
+    f32x4 acc[FI][FJ];
+#pragma unroll
+    for (int i = 0; i < FI; i++)
+#pragma unroll
+        for (int j = 0; j < FJ; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int r = lane & 15, q4 = lane >> 4;
+    for (int st = 0; st < nsteps; st++) {
+        // this step's 3 DPW DMAs are complete once at most the next step's are
+        // outstanding (only DMAs are in flight here, and they complete in order)
+        if (st + 1 < nsteps)
+            __builtin_amdgcn_s_waitcnt(0xF70 | (3 * DPW));  // vmcnt(3 DPW)
+        else
+            __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+        __builtin_amdgcn_s_barrier();  // every wave's DMAs for this step landed; step - 1's reads are done
+        if (st + 2 < nsteps) issue((st + 2) % kBStages, (st + 2) * kBK);
+        const unsigned char *sa = smem + ((st % kBStages) * 3 + 0) * kBTile;
+        const unsigned char *sh = sa + kBTile, *sl = sa + 2 * kBTile;
+        bf16x8 fa[FI], fh[FJ], fl[FJ];
+#pragma unroll
+        for (int i = 0; i < FI; i++) {
+            const int ra = wm * 128 + i * 16 + r;
+            fa[i] = *reinterpret_cast<const bf16x8 *>(sa + ra * 64 + ((q4 ^ ((ra >> 2) & 3)) * 16));
+        }
+#pragma unroll
+        for (int j = 0; j < FJ; j++) {
+            const int rb = wn * 64 + j * 16 + r;
+            fh[j] = *reinterpret_cast<const bf16x8 *>(sh + rb * 64 + ((q4 ^ ((rb >> 2) & 3)) * 16));
+            fl[j] = *reinterpret_cast<const bf16x8 *>(sl + rb * 64 + ((q4 ^ ((rb >> 2) & 3)) * 16));
+        }
+#pragma unroll
+        for (int i = 0; i < FI; i++)
+#pragma unroll
+            for (int j = 0; j < FJ; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fh[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < FI; i++)
+#pragma unroll
+            for (int j = 0; j < FJ; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fl[j], acc[i][j], 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < FI; i++)
+#pragma unroll
+        for (int j = 0; j < FJ; j++)
+            gemm_store<EPI>(a, m0 + wm * 128 + i * 16 + q4 * 4, n0 + wn * 64 + j * 16 + r, acc[i][j]);
+}
+
 // Split-K MFMA GEMM for short prompts (fewer than kTiledMinTokens tokens).
 //
 // Workgroup tile: 64 weight rows x 64 tokens over one contiguous range of K
@@ -493,6 +588,18 @@ hipError_t launch_rmsnorm_split(const float *x, const float *w, float eps, int T
 
 hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
     if (a.K % 32 != 0 || a.M <= 0 || a.N <= 0) return hipErrorInvalidValue;
+    // the 256 x 256 tile once its grid is about a workgroup per CU
+    if (a.N >= kTiledMinTokens && a.K % kBK == 0 && ((a.M + kBM - 1) / kBM) * ((a.N + kBN - 1) / kBN) >= 240) {
+        const dim3 grid((a.M + kBM - 1) / kBM, (a.N + kBN - 1) / kBN);
+        switch (epi) {
+            case GEPI_STORE: hipLaunchKernelGGL(gemm_big_kernel<GEPI_STORE>, grid, dim3(kGWaves * 64), 0, s, a); break;
+            case GEPI_RESID: hipLaunchKernelGGL(gemm_big_kernel<GEPI_RESID>, grid, dim3(kGWaves * 64), 0, s, a); break;
+            case GEPI_SWIGLU: hipLaunchKernelGGL(gemm_big_kernel<GEPI_SWIGLU>, grid, dim3(kGWaves * 64), 0, s, a); break;
+            case GEPI_QKV: hipLaunchKernelGGL(gemm_big_kernel<GEPI_QKV>, grid, dim3(kGWaves * 64), 0, s, a); break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     if (a.N >= kTiledMinTokens && a.K % kTK == 0) {
         const dim3 grid((a.M + kTM - 1) / kTM, (a.N + kTN - 1) / kTN);
         switch (epi) {
