@@ -75,9 +75,19 @@ __device__ __forceinline__ float max_xor16_32(float v) {
     return v;
 }
 
+// Slot of a key (its position within its 64-key block) in a V^T row.  The
+// P^T operand of O^T += V^T P^T gives lane (q4, r) the keys 4 q4 .. +3 of two
+// adjacent 16-key tiles; within each 32-key group those eight keys are
+// stored next to each other, so the lane reads its V^T operand as one
+// 16-byte chunk: key y of the group (y < 16: tile one, else tile two) goes to
+// slot 8 (y mod 16) / 4 + 4 (y / 16) + y mod 4.
+__host__ __device__ constexpr int vt_slot(int row) {
+    return (row & 32) | (((row & 15) >> 2) << 3) | ((row & 16) >> 2) | (row & 3);
+}
+
 // One workgroup per (64 positions, KV head): f32 K/V rows -> split-bf16 K
-// [pos][kvd] and V^T [head][dim][pos] (through an LDS transpose); rows at or
-// past n are zeros.
+// [pos][kvd] and V^T [head][dim][slot] (through an LDS transpose; the keys of
+// each 64-key block in vt_slot order); rows at or past n are zeros.
 __global__ __launch_bounds__(kBlock) void kv_split_kernel(const KVSplitArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t sT[2][kPHD][kSVP];
     const int t = threadIdx.x;
@@ -95,13 +105,14 @@ __global__ __launch_bounds__(kBlock) void kv_split_kernel(const KVSplitArgs a) {
         }
         const float kk[4] = {k.x, k.y, k.z, k.w}, vv[4] = {v.x, v.y, v.z, v.w};
         uint16_t kh[4], kl[4];
+        const int prow = vt_slot(row);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             split2(kk[j], kh[j], kl[j]);
             uint16_t vh, vl;
             split2(vv[j], vh, vl);
-            sT[0][d + j][row] = vh;
-            sT[1][d + j][row] = vl;
+            sT[0][d + j][prow] = vh;
+            sT[1][d + j][prow] = vl;
         }
         const size_t o = (size_t)pos * kvd + g * kPHD + d;
         *reinterpret_cast<u32x2 *>(a.kh + o) =
@@ -269,13 +280,10 @@ __global__ __launch_bounds__(kPWaves * 64) void attn_prefill_kernel(const AttnAr
             }
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) {
+                // keys 32 ks + 4 q4 .. +3 and 32 ks + 16 + 4 q4 .. +3: slots 32 ks + 8 q4 .. +7
                 const int dim = dt * 16 + r;
-                const u32x2 h0 = *reinterpret_cast<const u32x2 *>(&sV[0][dim][32 * ks + 4 * q4]);
-                const u32x2 h1 = *reinterpret_cast<const u32x2 *>(&sV[0][dim][32 * ks + 16 + 4 * q4]);
-                const u32x2 l0 = *reinterpret_cast<const u32x2 *>(&sV[1][dim][32 * ks + 4 * q4]);
-                const u32x2 l1 = *reinterpret_cast<const u32x2 *>(&sV[1][dim][32 * ks + 16 + 4 * q4]);
-                const bf16x8 vh = __builtin_bit_cast(bf16x8, u32x4{h0[0], h0[1], h1[0], h1[1]});
-                const bf16x8 vl = __builtin_bit_cast(bf16x8, u32x4{l0[0], l0[1], l1[0], l1[1]});
+                const bf16x8 vh = *reinterpret_cast<const bf16x8 *>(&sV[0][dim][32 * ks + 8 * q4]);
+                const bf16x8 vl = *reinterpret_cast<const bf16x8 *>(&sV[1][dim][32 * ks + 8 * q4]);
 #pragma unroll
                 for (int qt = 0; qt < kPQT; qt++) {
                     o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[qt], o[qt][dt], 0, 0, 0);
