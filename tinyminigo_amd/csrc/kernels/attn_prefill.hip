@@ -48,16 +48,21 @@ __device__ __forceinline__ void split2(float x, uint16_t &h, uint16_t &l) {
     l = f32_to_bf16_rne(x - bf16_to_f32(h));
 }
 
-// 8 floats -> (hi, lo) bf16x8 fragments
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// 8 floats -> (hi, lo) bf16x8 fragments, two values per packed conversion
+// (the same rounding as split2: hi = bf16(x), lo = bf16(x - hi), RNE)
 __device__ __forceinline__ void split8(const float (&v)[8], bf16x8 &hi, bf16x8 &lo) {
     u32x4 h, l;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        uint16_t h0, l0, h1, l1;
-        split2(v[2 * i], h0, l0);
-        split2(v[2 * i + 1], h1, l1);
-        h[i] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-        l[i] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+        const f32x2 x = {v[2 * i], v[2 * i + 1]};
+        const bf16x2 hb = __builtin_convertvector(x, bf16x2);
+        const f32x2 hf = __builtin_convertvector(hb, f32x2);
+        const bf16x2 lb = __builtin_convertvector(x - hf, bf16x2);
+        h[i] = __builtin_bit_cast(uint32_t, hb);
+        l[i] = __builtin_bit_cast(uint32_t, lb);
     }
     hi = __builtin_bit_cast(bf16x8, h);
     lo = __builtin_bit_cast(bf16x8, l);
