@@ -39,9 +39,11 @@ constexpr int kPKB = 64;         // keys per block
 constexpr int kPCols = 128;      // query columns per workgroup
 constexpr int kPWaves = 8;       // wavefronts per workgroup (two per SIMD)
 constexpr int kPQT = kPCols / (16 * kPWaves);  // 16-column query tiles per wavefront
-constexpr int kPCopies = kPKB * kPHD / 8 / (kPWaves * 64);  // 16-byte staging copies per thread per K (or V) half
-constexpr int kSKP = kPHD + 8;   // sK row pitch, bf16
-constexpr int kSVP = kPKB + 8;   // sV row pitch, bf16
+constexpr int kSVP = kPKB + 8;   // kv_split_kernel's transpose buffer row pitch, bf16
+// One staged block: K hi / lo [64 keys][256 B] and V^T hi / lo [128 dims][128 B]
+constexpr int kPKTile = kPKB * kPHD * 2, kPVTile = kPHD * kPKB * 2;
+constexpr int kPStage = 2 * kPKTile + 2 * kPVTile;
+constexpr int kPDma = kPStage / 1024 / kPWaves;  // 1 KB DMA instructions per wave per block
 
 __device__ __forceinline__ void split2(float x, uint16_t &h, uint16_t &l) {
     h = f32_to_bf16_rne(x);
@@ -137,12 +139,23 @@ __global__ __launch_bounds__(kBlock) void kv_split_kernel(const KVSplitArgs a) {
     }
 }
 
+// K and V^T blocks go global -> LDS by DMA (global_load_lds_dwordx4) into a
+// two-stage ring: block kb + 1 is in flight while block kb is multiplied.
+// LDS rows are unpadded, their 16-byte chunks XOR-swizzled so that a
+// fragment read's 16 rows hit 16 distinct bank groups: K rows (256 B, 16
+// chunks) by key & 15, V^T rows (128 B, 8 chunks) by (dim >> 1) & 7.  A DMA
+// wave-instruction fills 1 KB: 4 K rows or 8 V^T rows.
+__device__ __forceinline__ int k_chunk(int key, int c) { return c ^ (key & 15); }
+__device__ __forceinline__ int vt_chunk(int dim, int c) { return c ^ ((dim >> 1) & 7); }
+
+__device__ __forceinline__ void dma16(const uint16_t *src, unsigned char *dst) {
+    __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+}
+
 template <int GROUP>
 __global__ __launch_bounds__(kPWaves * 64) void attn_prefill_kernel(const AttnArgs a) {
     constexpr int QB = kPCols / GROUP;  // query positions per workgroup
-    constexpr int NT = kPWaves * 64;    // threads
-    __shared__ __attribute__((aligned(16))) uint16_t sK[2][kPKB][kSKP];  // [hi/lo][key][dim]
-    __shared__ __attribute__((aligned(16))) uint16_t sV[2][kPHD][kSVP];  // [hi/lo][dim][key]
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * kPStage];
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int r = lane & 15, q4 = lane >> 4;
     const int nqb = (a.T + QB - 1) / QB;
@@ -150,7 +163,7 @@ __global__ __launch_bounds__(kPWaves * 64) void attn_prefill_kernel(const AttnAr
     const int g = blockIdx.y;
     const int kvd = a.nkv * kPHD, qd = a.nq * kPHD;
 
-    // this lane's query column in each of its two 16-column tiles
+    // this lane's query column in each of its 16-column tiles
     int ti[kPQT], qpos[kPQT], qhead[kPQT];
 #pragma unroll
     for (int qt = 0; qt < kPQT; qt++) {
@@ -163,28 +176,9 @@ __global__ __launch_bounds__(kPWaves * 64) void attn_prefill_kernel(const AttnAr
     const int last_pos = a.start + min(a.T, (qb + 1) * QB) - 1;  // the workgroup's last query position
     const int nkb = last_pos / kPKB + 1;
 
-    // staging map: copy c = t + NT i (i < kPCopies) of a block is K row c >> 4,
-    // 16-byte column c & 15, and V^T row c >> 3, 16-byte column c & 7
-    const uint16_t *gk[2], *gv[2];
-    gk[0] = a.kh + g * kPHD;
-    gk[1] = a.kl + g * kPHD;
-    gv[0] = a.vth + (size_t)g * kPHD * a.vt_pitch;
-    gv[1] = a.vtl + (size_t)g * kPHD * a.vt_pitch;
-    u32x4 rk[2][kPCopies], rv[2][kPCopies];
-    auto fetch = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < kPCopies; i++) {
-            const int c = t + NT * i;
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                rk[h][i] = *reinterpret_cast<const u32x4 *>(gk[h] + (size_t)(k0 + (c >> 4)) * kvd + (c & 15) * 8);
-                rv[h][i] = *reinterpret_cast<const u32x4 *>(gv[h] + (size_t)(c >> 3) * a.vt_pitch + k0 + (c & 7) * 8);
-            }
-        }
-    };
-    fetch(0);
-
-    // Q^T fragments (MFMA B operand): dims 32 ds + 8 q4 .. +7 of the column
+    // Q^T fragments (MFMA B operand): dims 32 ds + 8 q4 .. +7 of the column.
+    // Loaded and consumed before any DMA is issued: the DMA waits below count
+    // only DMAs.
     bf16x8 qh[kPQT][4], ql[kPQT][4];
 #pragma unroll
     for (int qt = 0; qt < kPQT; qt++) {
@@ -197,6 +191,37 @@ __global__ __launch_bounds__(kPWaves * 64) void attn_prefill_kernel(const AttnAr
             split8(v, qh[qt][ds], ql[qt][ds]);
         }
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // DMA map: instruction i (of kPDma) of wave w is global instruction
+    // n = kPDma w + i of the block: n / 16 selects K hi, K lo, V^T hi, V^T lo,
+    // n % 16 the 1 KB slice (K rows 4 (n % 16) ..; V^T rows 8 (n % 16) ..)
+    const uint16_t *dsrc[kPDma];
+    int ddst[kPDma];
+#pragma unroll
+    for (int i = 0; i < kPDma; i++) {
+        const int n = kPDma * wave + i, part = n / 16, sl = n % 16;
+        if (part < 2) {
+            const int key = 4 * sl + (lane >> 4), pc = lane & 15;
+            dsrc[i] = (part ? a.kl : a.kh) + (size_t)key * kvd + g * kPHD + k_chunk(key, pc) * 8;
+        } else {
+            const int dim = 8 * sl + (lane >> 3), pc = lane & 7;
+            dsrc[i] = (part == 3 ? a.vtl : a.vth) + ((size_t)g * kPHD + dim) * a.vt_pitch + vt_chunk(dim, pc) * 8;
+        }
+        ddst[i] = (part < 2 ? part * kPKTile : 2 * kPKTile + (part - 2) * kPVTile) + sl * 1024;
+    }
+    auto issue = [&](int kb) {
+        unsigned char *st = smem + (kb & 1) * kPStage;
+#pragma unroll
+        for (int i = 0; i < kPDma; i++) {
+            const int part = (kPDma * wave + i) / 16;
+            // K rows advance by 64 keys per block, V^T columns by 64 positions
+            const size_t adv = part < 2 ? (size_t)kb * kPKB * kvd : (size_t)kb * kPKB;
+            dma16(dsrc[i] + adv, st + ddst[i]);
+        }
+    };
+    issue(0);
+
     const float sl2 = a.scale * 1.4426950408889634f;  // scores in log2 units
     float m[kPQT], l[kPQT];
     f32x4 o[kPQT][8];
@@ -210,18 +235,14 @@ __global__ __launch_bounds__(kPWaves * 64) void attn_prefill_kernel(const AttnAr
 
     for (int kb = 0; kb < nkb; kb++) {
         const int k0 = kb * kPKB;
-        __syncthreads();  // the previous block's fragments are read
-#pragma unroll
-        for (int i = 0; i < kPCopies; i++) {
-            const int c = t + NT * i;
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                *reinterpret_cast<u32x4 *>(&sK[h][c >> 4][(c & 15) * 8]) = rk[h][i];
-                *reinterpret_cast<u32x4 *>(&sV[h][c >> 3][(c & 7) * 8]) = rv[h][i];
-            }
-        }
-        __syncthreads();
-        if (kb + 1 < nkb) fetch(k0 + kPKB);  // in flight during this block's MFMAs
+        // block kb landed (only its DMAs are outstanding) in every wave, and
+        // every wave is done with block kb - 1, whose stage block kb + 1 reuses
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kb + 1 < nkb) issue(kb + 1);
+        const unsigned char *sK0 = smem + (kb & 1) * kPStage, *sK1 = sK0 + kPKTile;
+        const unsigned char *sV0 = sK0 + 2 * kPKTile, *sV1 = sV0 + kPVTile;
 
         // S^T = K Q^T: 4 key tiles x 2 query tiles
         f32x4 s[4][kPQT];
@@ -233,8 +254,9 @@ __global__ __launch_bounds__(kPWaves * 64) void attn_prefill_kernel(const AttnAr
         for (int ds = 0; ds < 4; ds++) {
 #pragma unroll
             for (int kt = 0; kt < 4; kt++) {
-                const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(&sK[0][kt * 16 + r][32 * ds + 8 * q4]);
-                const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(&sK[1][kt * 16 + r][32 * ds + 8 * q4]);
+                const int key = kt * 16 + r, ko = key * 256 + k_chunk(key, 4 * ds + q4) * 16;
+                const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(sK0 + ko);
+                const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(sK1 + ko);
 #pragma unroll
                 for (int qt = 0; qt < kPQT; qt++) {
                     s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[qt][ds], s[kt][qt], 0, 0, 0);
@@ -286,9 +308,9 @@ __global__ __launch_bounds__(kPWaves * 64) void attn_prefill_kernel(const AttnAr
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) {
                 // keys 32 ks + 4 q4 .. +3 and 32 ks + 16 + 4 q4 .. +3: slots 32 ks + 8 q4 .. +7
-                const int dim = dt * 16 + r;
-                const bf16x8 vh = *reinterpret_cast<const bf16x8 *>(&sV[0][dim][32 * ks + 8 * q4]);
-                const bf16x8 vl = *reinterpret_cast<const bf16x8 *>(&sV[1][dim][32 * ks + 8 * q4]);
+                const int dim = dt * 16 + r, vo = dim * 128 + vt_chunk(dim, 4 * ks + q4) * 16;
+                const bf16x8 vh = *reinterpret_cast<const bf16x8 *>(sV0 + vo);
+                const bf16x8 vl = *reinterpret_cast<const bf16x8 *>(sV1 + vo);
 #pragma unroll
                 for (int qt = 0; qt < kPQT; qt++) {
                     o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[qt], o[qt][dt], 0, 0, 0);
