@@ -139,6 +139,19 @@ def test_i8_teacher_forced_logits_vs_oracle(T, O, untied_i8):
     assert np.abs(a - b).max() * 20 < np.abs(a - c).max()
 
 
+def test_i8_tiled_prefill_vs_oracle(T, O, untied_i8):
+    """A 300-token prompt takes the tiled MFMA GEMMs, whose epilogues apply the
+    int8 row scales with vector loads: logits and K/V rows against the int8
+    oracle, then greedy decode steps on that cache."""
+    g, o, _, wl = untied_i8
+    ids = [int(t) for t in T.synth_tokens(25, 306, wl.vocab_size)]
+    gc, oc = T.KvCache(g, 320), o.new_cache()
+    print("i8 prefill 300", flush=True)
+    close_logits(g.forward_seq(ids[:300], gc), o.forward_seq(ids[:300], oc), "i8 prefill 300")
+    for i, t in enumerate(ids[300:]):
+        close_logits(g.forward_token(t, gc), o.forward_token(t, oc), f"i8 decode after 300, step {i}")
+
+
 def test_i8_generate_greedy_vs_oracle(T, O, untied_i8):
     g, o, _, wl = untied_i8
     prompt = [int(t) for t in T.synth_tokens(23, 16, wl.vocab_size)]

@@ -150,6 +150,107 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &a, int mb, int n, con
     }
 }
 
+// The epilogue of rows mb .. mb+3 (mb a multiple of 4) of token column n with
+// 16-, 8- or 4-byte accesses per lane; gemm_store at the edges and for the
+// shapes the vector forms do not cover (M or head_dim not a multiple of 4).
+template <int EPI>
+__device__ __forceinline__ void gemm_store4(const GemmArgs &a, int mb, int n, const f32x4 &acc) {
+    if (n >= a.N) return;
+    if (mb + 3 >= a.M || (a.M & 3) || (EPI == GEPI_QKV && (a.hd & 3))) {
+        gemm_store<EPI>(a, mb, n, acc);
+        return;
+    }
+    f32x4 v = acc;
+    if (a.wscale) {
+#pragma clang fp contract(off)
+        const f32x4 sc = *reinterpret_cast<const f32x4 *>(a.wscale + mb);
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = v[i] * sc[i];
+    }
+    if constexpr (EPI == GEPI_STORE || EPI == GEPI_RESID) {
+        f32x4 *yr = reinterpret_cast<f32x4 *>(a.y + (size_t)n * a.M + mb);
+        if constexpr (EPI == GEPI_RESID) {
+            f32x4 y = *yr;
+#pragma unroll
+            for (int i = 0; i < 4; i++) y[i] = y[i] + v[i];
+            *yr = y;
+        } else {
+            *yr = v;
+        }
+    } else if constexpr (EPI == GEPI_SWIGLU) {
+        // pairs (mb, mb+1) and (mb+2, mb+3) -> h[P], h[P+1], P = mb / 2
+        uint32_t hi = 0, lo = 0;
+#pragma unroll
+        for (int pr = 0; pr < 2; pr++) {
+            uint16_t h, l;
+            split_bf16(swiglu(v[2 * pr], v[2 * pr + 1]), &h, &l);
+            hi |= (uint32_t)h << (16 * pr);
+            lo |= (uint32_t)l << (16 * pr);
+        }
+        const size_t o = (size_t)n * (a.M >> 1) + (mb >> 1);
+        *reinterpret_cast<uint32_t *>(a.h_hi + o) = hi;
+        *reinterpret_cast<uint32_t *>(a.h_lo + o) = lo;
+    } else {  // GEPI_QKV: pairs P, P+1 are rotation pairs j, j+1 of one head
+        const int half = a.hd >> 1;
+        const int P = mb >> 1;
+        const int head = P / half, j = P - head * half;
+        const int pos = a.pos_seq ? a.pos_seq[n] : a.start + n;
+        const int kvd = a.nkv * a.hd;
+        float *dst;
+        float2 o0, o1;  // values at j, j+1 and at j+half, j+half+1
+        if (head < a.nq + a.nkv) {
+            const float2 c = *reinterpret_cast<const float2 *>(a.rope_cos + (size_t)pos * half + j);
+            const float2 sn = *reinterpret_cast<const float2 *>(a.rope_sin + (size_t)pos * half + j);
+            rope_pair(v[0], v[1], c.x, sn.x, &o0.x, &o1.x);
+            rope_pair(v[2], v[3], c.y, sn.y, &o0.y, &o1.y);
+            if (head < a.nq) {
+                dst = a.q_out + (size_t)n * a.nq * a.hd + head * a.hd;
+            } else {
+                float *const kcache = a.k_seq ? a.k_seq[n] + a.kv_layer_off : a.k_cache;
+                dst = kcache + (size_t)pos * kvd + (head - a.nq) * a.hd;
+            }
+        } else {
+            o0 = make_float2(v[0], v[2]);
+            o1 = make_float2(v[1], v[3]);
+            float *const vcache = a.v_seq ? a.v_seq[n] + a.kv_layer_off : a.v_cache;
+            dst = vcache + (size_t)pos * kvd + (head - a.nq - a.nkv) * a.hd;
+        }
+        *reinterpret_cast<float2 *>(dst + j) = o0;
+        *reinterpret_cast<float2 *>(dst + j + half) = o1;
+    }
+}
+
+// The output of one wavefront's FI x FJ MFMA fragments (fragment (i, j): rows
+// mw + 16 i + 4 (lane >> 4) .. +3 of token nw + 16 j + (lane & 15)) through
+// the wavefront's own LDS region `buf` (FJ 16 token rows of kStagePitch
+// floats), 64 rows at a time: written as [token][row], read back as four
+// consecutive rows per lane, so that 16 lanes cover 64 consecutive rows of
+// one token for gemm_store4.  LDS accesses of one wavefront execute in order,
+// so no barrier separates the writes from the reads.
+constexpr int kStagePitch = 68;  // 64 + 4: the fragment writes' 16 token rows fall in distinct banks
+
+template <int EPI, int FI, int FJ>
+__device__ __forceinline__ void stage_epilogue(const GemmArgs &a, float *buf, int mw, int nw,
+                                               const f32x4 (&acc)[FI][FJ]) {
+    static_assert(FI % 4 == 0, "64-row passes");
+    const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
+    const int mq = (lane & 15) * 4, nsub = lane >> 4;
+#pragma unroll
+    for (int h = 0; h < FI / 4; h++) {
+#pragma unroll
+        for (int ii = 0; ii < 4; ii++)
+#pragma unroll
+            for (int j = 0; j < FJ; j++)
+                *reinterpret_cast<f32x4 *>(buf + (j * 16 + r) * kStagePitch + ii * 16 + q4 * 4) = acc[4 * h + ii][j];
+#pragma unroll
+        for (int rr = 0; rr < FJ * 4; rr++) {
+            const int nl = rr * 4 + nsub;
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(buf + nl * kStagePitch + mq);
+            gemm_store4<EPI>(a, mw + h * 64 + mq, nw + nl, v);
+        }
+    }
+}
+
 // MFMA GEMM D[m][n] = sum_k W[m][k] * (Bhi[n][k] + Blo[n][k]).
 //
 // Workgroup tile: 16 weight rows x 64 tokens; the four wavefronts split K in
@@ -301,22 +402,23 @@ __global__ __launch_bounds__(kGWaves * 64) void gemm_dma_kernel(const GemmArgs a
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fl[j], acc[i][j], 0, 0, 0);
         }
     }
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < NJ; j++)
-            gemm_store<EPI>(a, m0 + wm * 64 + i * 16 + q4 * 4, n0 + wn * NJ * 16 + j * 16 + r, acc[i][j]);
+    // the ring is free once every wave is past its last fragment reads
+    __builtin_amdgcn_s_barrier();
+    stage_epilogue<EPI, 4, NJ>(a, reinterpret_cast<float *>(smem) + wave * NJ * 16 * kStagePitch, m0 + wm * 64,
+                               n0 + wn * NJ * 16, acc);
 }
 
 // Large-tile MFMA GEMM for long prompts: workgroup tile 256 weight rows x
 // 256 tokens, K in steps of 32.  The global -> LDS DMA path carries about
 // 45 GB/s per CU (measured), and a step's W, Bhi and Blo tiles are 48 KB
 // either way; the 256 x 256 tile does twice the MFMA work of the 128 x 128
-// one for them.  Three-stage ring of 48 KB stages, one barrier per step;
-// LDS rows are 64 B (32 bf16) with the four 16-byte chunks XOR-swizzled by
-// (row >> 2) & 3, so a fragment read's 16 rows hit 16 distinct bank groups,
-// and a DMA wave-instruction fills 16 rows (1 KB).  Wave w owns rows
-// 128 (w & 1) .. +127 and tokens 64 (w >> 1) .. +63 (8 x 4 MFMA fragments).
+// one for them.  Three-stage ring of 48 KB stages, up to three steps in
+// flight, one barrier per step; LDS rows are 64 B (32 bf16) with the four
+// 16-byte chunks XOR-swizzled by (row >> 2) & 3, so a fragment read's 16 rows
+// hit 16 distinct bank groups, and a DMA wave-instruction fills 16 rows
+// (1 KB).  Wave w owns rows 128 (w & 1) .. +127 and tokens 64 (w >> 1) .. +63
+// (8 x 4 MFMA fragments); its fragment reads for the next step overlap the
+// current step's MFMAs.  The output leaves through LDS (stage_epilogue).
 constexpr int kBM = 256, kBN = 256, kBK = 32;
 constexpr int kBStages = 3;
 constexpr int kBTile = kBM * kBK * 2;  // bytes of one 256 x 32 bf16 tile (kBN == kBM)
@@ -326,16 +428,13 @@ template <int EPI>
 __global__ __launch_bounds__(kGWaves * 64) void gemm_big_kernel(const GemmArgs a) {
     constexpr int DPW = kBTile / 1024 / kGWaves;  // DMA instructions per wave per tile
     constexpr int FI = 8, FJ = 4;                 // row / token fragments per wave
-    static_assert(3 * DPW <= 15, "vmcnt immediate");
+    static_assert(6 * DPW <= 15, "vmcnt immediate");
     __shared__ __attribute__((aligned(1024))) unsigned char smem[kBStages * 3 * kBTile];
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int wm = wave & 1, wn = wave >> 1;
     const int m0 = blockIdx.x * kBM, n0 = blockIdx.y * kBN;
     const int K = a.K;
     const int nsteps = K / kBK;
-    // DMA: wave w's instruction i fills rows (DPW w + i) * 16 .. +15 of a
-    // tile; lane l writes row (DPW w + i) * 16 + (l >> 2), physical chunk
-    // l & 3, which holds logical chunk (l & 3) ^ ((row >> 2) & 3)
     uint32_t off[2][DPW];
 #pragma unroll
     for (int i = 0; i < DPW; i++) {
@@ -354,53 +453,99 @@ __global__ __launch_bounds__(kGWaves * 64) void gemm_big_kernel(const GemmArgs a
                                                  smem + (stage * 3 + x) * kBTile + (wave * DPW + i) * 1024, 16, 0, 0);
         }
     };
+    const int r = lane & 15, q4 = lane >> 4;
+    uint32_t ao[FI], bo[FJ];
+#pragma unroll
+    for (int i = 0; i < FI; i++) {
+        const int ra = wm * 128 + i * 16 + r;
+        ao[i] = ra * 64 + ((q4 ^ ((ra >> 2) & 3)) * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < FJ; j++) {
+        const int rb = wn * 64 + j * 16 + r;
+        bo[j] = kBTile + rb * 64 + ((q4 ^ ((rb >> 2) & 3)) * 16);
+    }
+    auto rd = [&](int stage, uint32_t o) {
+        return *reinterpret_cast<const bf16x8 *>(smem + stage * 3 * kBTile + o);
+    };
+    // three steps in flight; wait for step 0 (the later groups may remain:
+    // only DMAs are outstanding, and they complete in issue order)
     issue(0, 0);
     if (nsteps > 1) issue(1, kBK);
+    if (nsteps > 2) issue(2, 2 * kBK);
+    if (nsteps > 2)
+        __builtin_amdgcn_s_waitcnt(0xF70 | (6 * DPW));
+    else if (nsteps > 1)
+        __builtin_amdgcn_s_waitcnt(0xF70 | (3 * DPW));
+    else
+        __builtin_amdgcn_s_waitcnt(0xF70);
+    __builtin_amdgcn_s_barrier();
     f32x4 acc[FI][FJ];
 #pragma unroll
     for (int i = 0; i < FI; i++)
 #pragma unroll
         for (int j = 0; j < FJ; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int r = lane & 15, q4 = lane >> 4;
-    for (int st = 0; st < nsteps; st++) {
-        // this step's 3 DPW DMAs are complete once at most the next step's are
-        // outstanding (only DMAs are in flight here, and they complete in order)
-        if (st + 1 < nsteps)
-            __builtin_amdgcn_s_waitcnt(0xF70 | (3 * DPW));  // vmcnt(3 DPW)
-        else
-            __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
-        __builtin_amdgcn_s_barrier();  // every wave's DMAs for this step landed; step - 1's reads are done
-        if (st + 2 < nsteps) issue((st + 2) % kBStages, (st + 2) * kBK);
-        const unsigned char *sa = smem + ((st % kBStages) * 3 + 0) * kBTile;
-        const unsigned char *sh = sa + kBTile, *sl = sa + 2 * kBTile;
-        bf16x8 fa[FI], fh[FJ], fl[FJ];
+    bf16x8 fa[FI], fh[FJ], fl[FJ];
+#pragma unroll
+    for (int i = 0; i < FI; i++) fa[i] = rd(0, ao[i]);
+#pragma unroll
+    for (int j = 0; j < FJ; j++) fh[j] = rd(0, bo[j]);
+    // Step st: the hi pass (W x Bhi) from registers, reading step st's Blo
+    // fragments after its first row group (their registers are free once the
+    // previous lo pass is done); then, with every wave's reads of stage st
+    // done and step st + 1's DMAs landed, one barrier, step st + 3's DMAs
+    // into the freed stage, and the lo pass (W x Blo) with step st + 1's W and
+    // Bhi fragment reads interleaved, each into registers the pass no longer
+    // needs.  The scheduling barriers keep each read where it is placed.
+    auto hi_pass = [&](int stage) {
 #pragma unroll
         for (int i = 0; i < FI; i++) {
-            const int ra = wm * 128 + i * 16 + r;
-            fa[i] = *reinterpret_cast<const bf16x8 *>(sa + ra * 64 + ((q4 ^ ((ra >> 2) & 3)) * 16));
-        }
-#pragma unroll
-        for (int j = 0; j < FJ; j++) {
-            const int rb = wn * 64 + j * 16 + r;
-            fh[j] = *reinterpret_cast<const bf16x8 *>(sh + rb * 64 + ((q4 ^ ((rb >> 2) & 3)) * 16));
-            fl[j] = *reinterpret_cast<const bf16x8 *>(sl + rb * 64 + ((q4 ^ ((rb >> 2) & 3)) * 16));
-        }
-#pragma unroll
-        for (int i = 0; i < FI; i++)
 #pragma unroll
             for (int j = 0; j < FJ; j++)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fh[j], acc[i][j], 0, 0, 0);
+            if (i == 0) {
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < FI; i++)
+                for (int j = 0; j < FJ; j++) fl[j] = rd(stage, bo[j] + kBTile);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    for (int st = 0; st + 1 < nsteps; st++) {
+        const int ns = (st + 1) % kBStages;
+        hi_pass(st % kBStages);
+        // this wave's reads of stage st are done (lgkmcnt 0) and step st + 1's
+        // DMAs have landed: only step st + 2's group may remain outstanding
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        if (st + 2 < nsteps)
+            __builtin_amdgcn_s_waitcnt(0xF70 | (3 * DPW));  // vmcnt(3 DPW)
+        else
+            __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        if (st + 3 < nsteps) issue(st % kBStages, (st + 3) * kBK);
+#pragma unroll
+        for (int j = 0; j < FJ; j++) fh[j] = rd(ns, bo[j]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < FI; i++) {
 #pragma unroll
             for (int j = 0; j < FJ; j++)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fl[j], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            fa[i] = rd(ns, ao[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
+    hi_pass((nsteps - 1) % kBStages);
 #pragma unroll
     for (int i = 0; i < FI; i++)
 #pragma unroll
         for (int j = 0; j < FJ; j++)
-            gemm_store<EPI>(a, m0 + wm * 128 + i * 16 + q4 * 4, n0 + wn * 64 + j * 16 + r, acc[i][j]);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fl[j], acc[i][j], 0, 0, 0);
+    // the ring is free once every wave is past its last fragment reads
+    __builtin_amdgcn_s_barrier();
+    stage_epilogue<EPI, FI, FJ>(a, reinterpret_cast<float *>(smem) + wave * FJ * 16 * kStagePitch, m0 + wm * 128,
+                                n0 + wn * 64, acc);
 }
 
 // Split-K MFMA GEMM for short prompts (fewer than kTiledMinTokens tokens).
