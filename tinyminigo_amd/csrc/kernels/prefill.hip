@@ -639,7 +639,8 @@ __global__ __launch_bounds__(kBlock, 2) void gemm_skinny_kernel(const GemmArgs a
             for (int i = 0; i < 4; i++) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fl, acc[i], 0, 0, 0);
         }
     }
-    const int col = n0 + rb;
+    // the ring is free for the output staging once every wave is past its reads
+    __builtin_amdgcn_s_barrier();
     if (nsplit > 1) {
         // wave w's quarter of the tile (its 16 tokens) is reduced by the last
         // of the tile's nsplit waves w to arrive.  Partials move through
@@ -679,8 +680,8 @@ __global__ __launch_bounds__(kBlock, 2) void gemm_skinny_kernel(const GemmArgs a
                     for (int e = 0; e < 4; e++) acc[i][e] += pv[sp][i * 4 + e];
         if (lane == 0) __hip_atomic_store(&a.cnt[slot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-#pragma unroll
-    for (int i = 0; i < 4; i++) gemm_store<EPI>(a, m0 + i * 16 + q * 4, col, acc[i]);
+    const f32x4 out[4][1] = {{acc[0]}, {acc[1]}, {acc[2]}, {acc[3]}};
+    stage_epilogue<EPI, 4, 1>(a, reinterpret_cast<float *>(smem) + wave * 16 * kStagePitch, m0, n0 + wave * 16, out);
 }
 
 hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
