@@ -432,7 +432,20 @@ __global__ __launch_bounds__(kGWaves * 64) void gemm_big_kernel(const GemmArgs a
     __shared__ __attribute__((aligned(1024))) unsigned char smem[kBStages * 3 * kBTile];
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int wm = wave & 1, wn = wave >> 1;
-    const int m0 = blockIdx.x * kBM, n0 = blockIdx.y * kBN;
+    // A grid of at most one workgroup per CU runs in one round: each XCD (one
+    // L2; workgroups go to XCDs round robin) then takes an eighth of the
+    // token tiles against every row tile, so it fetches its activation rows
+    // once and the weights (the smaller operand at these shapes) once per XCD,
+    // instead of every activation row once per XCD (6-9% faster at 2048
+    // weight rows x 8192 tokens; no gain or a loss for larger grids).
+    int mt = blockIdx.x, nt = blockIdx.y;
+    if ((gridDim.y & 7) == 0 && gridDim.x * gridDim.y <= 256) {
+        const int L = blockIdx.x + gridDim.x * blockIdx.y;
+        const int sl = L >> 3;
+        mt = sl % gridDim.x;
+        nt = (L & 7) * (gridDim.y >> 3) + sl / gridDim.x;
+    }
+    const int m0 = mt * kBM, n0 = nt * kBN;
     const int K = a.K;
     const int nsteps = K / kBK;
     uint32_t off[2][DPW];
