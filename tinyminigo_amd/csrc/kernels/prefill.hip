@@ -222,31 +222,35 @@ __device__ __forceinline__ void gemm_store4(const GemmArgs &a, int mb, int n, co
 
 // The output of one wavefront's FI x FJ MFMA fragments (fragment (i, j): rows
 // mw + 16 i + 4 (lane >> 4) .. +3 of token nw + 16 j + (lane & 15)) through
-// the wavefront's own LDS region `buf` (FJ 16 token rows of kStagePitch
-// floats), 64 rows at a time: written as [token][row], read back as four
-// consecutive rows per lane, so that 16 lanes cover 64 consecutive rows of
-// one token for gemm_store4.  LDS accesses of one wavefront execute in order,
-// so no barrier separates the writes from the reads.
-constexpr int kStagePitch = 68;  // 64 + 4: the fragment writes' 16 token rows fall in distinct banks
+// the wavefront's own LDS region `buf` (FJ 16 token rows of 64 floats), 64
+// rows at a time: written as [token][row], read back as four consecutive rows
+// per lane, so that 16 lanes cover 64 consecutive rows of one token for
+// gemm_store4.  The 16-byte chunk c of token t sits at chunk c ^ (t & 15):
+// both the fragment writes and the row reads are then free of bank conflicts
+// (measured; a padded 68-float pitch conflicts on the reads).  LDS accesses
+// of one wavefront execute in order, so no barrier separates the writes from
+// the reads.
+constexpr int kStagePitch = 64;  // floats per staged token row
 
 template <int EPI, int FI, int FJ>
 __device__ __forceinline__ void stage_epilogue(const GemmArgs &a, float *buf, int mw, int nw,
                                                const f32x4 (&acc)[FI][FJ]) {
     static_assert(FI % 4 == 0, "64-row passes");
     const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
-    const int mq = (lane & 15) * 4, nsub = lane >> 4;
+    const int nsub = lane >> 4;
 #pragma unroll
     for (int h = 0; h < FI / 4; h++) {
 #pragma unroll
         for (int ii = 0; ii < 4; ii++)
 #pragma unroll
             for (int j = 0; j < FJ; j++)
-                *reinterpret_cast<f32x4 *>(buf + (j * 16 + r) * kStagePitch + ii * 16 + q4 * 4) = acc[4 * h + ii][j];
+                *reinterpret_cast<f32x4 *>(buf + (j * 16 + r) * kStagePitch + (((ii * 4 + q4) ^ r) * 4)) =
+                    acc[4 * h + ii][j];
 #pragma unroll
         for (int rr = 0; rr < FJ * 4; rr++) {
             const int nl = rr * 4 + nsub;
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(buf + nl * kStagePitch + mq);
-            gemm_store4<EPI>(a, mw + h * 64 + mq, nw + nl, v);
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(buf + nl * kStagePitch + ((r ^ (nl & 15)) * 4));
+            gemm_store4<EPI>(a, mw + h * 64 + r * 4, nw + nl, v);
         }
     }
 }
@@ -414,9 +418,10 @@ __global__ __launch_bounds__(kGWaves * 64) void gemm_dma_kernel(const GemmArgs a
 // either way; the 256 x 256 tile does twice the MFMA work of the 128 x 128
 // one for them.  Three-stage ring of 48 KB stages, up to three steps in
 // flight, one barrier per step; LDS rows are 64 B (32 bf16) with the four
-// 16-byte chunks XOR-swizzled by (row >> 2) & 3, so a fragment read's 16 rows
-// hit 16 distinct bank groups, and a DMA wave-instruction fills 16 rows
-// (1 KB).  Wave w owns rows 128 (w & 1) .. +127 and tokens 64 (w >> 1) .. +63
+// 16-byte chunks XOR-swizzled by (row >> 1) & 3: by rocprofv3's
+// SQ_LDS_BANK_CONFLICT, a fragment read (16 rows x 4 chunks) is then
+// conflict-free, where (row >> 2) & 3 or row & 3 cost a second cycle per read;
+// a DMA wave-instruction fills 16 rows (1 KB).  Wave w owns rows 128 (w & 1) .. +127 and tokens 64 (w >> 1) .. +63
 // (8 x 4 MFMA fragments); its fragment reads for the next step overlap the
 // current step's MFMAs.  The output leaves through LDS (stage_epilogue).
 constexpr int kBM = 256, kBN = 256, kBK = 32;
@@ -452,7 +457,7 @@ __global__ __launch_bounds__(kGWaves * 64) void gemm_big_kernel(const GemmArgs a
 #pragma unroll
     for (int i = 0; i < DPW; i++) {
         const int row = (wave * DPW + i) * 16 + (lane >> 2);
-        const int lc = (lane & 3) ^ ((row >> 2) & 3);
+        const int lc = (lane & 3) ^ ((row >> 1) & 3);
         off[0][i] = (uint32_t)min(m0 + row, a.M - 1) * (uint32_t)K + lc * 8;
         off[1][i] = (uint32_t)min(n0 + row, a.N - 1) * (uint32_t)K + lc * 8;
     }
@@ -471,12 +476,12 @@ __global__ __launch_bounds__(kGWaves * 64) void gemm_big_kernel(const GemmArgs a
 #pragma unroll
     for (int i = 0; i < FI; i++) {
         const int ra = wm * 128 + i * 16 + r;
-        ao[i] = ra * 64 + ((q4 ^ ((ra >> 2) & 3)) * 16);
+        ao[i] = ra * 64 + ((q4 ^ ((ra >> 1) & 3)) * 16);
     }
 #pragma unroll
     for (int j = 0; j < FJ; j++) {
         const int rb = wn * 64 + j * 16 + r;
-        bo[j] = kBTile + rb * 64 + ((q4 ^ ((rb >> 2) & 3)) * 16);
+        bo[j] = kBTile + rb * 64 + ((q4 ^ ((rb >> 1) & 3)) * 16);
     }
     auto rd = [&](int stage, uint32_t o) {
         return *reinterpret_cast<const bf16x8 *>(smem + stage * 3 * kBTile + o);
