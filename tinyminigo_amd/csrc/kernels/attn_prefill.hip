@@ -158,9 +158,13 @@ __global__ __launch_bounds__(kPWaves * 64) void attn_prefill_kernel(const AttnAr
     __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * kPStage];
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int r = lane & 15, q4 = lane >> 4;
+    // workgroup L: KV head L % nkv, the (L / nkv)-th longest query block, so
+    // the dispatch order is longest causal range first across all heads, and
+    // as workgroups go to the 8 XCDs round robin, with nkv dividing 8 each
+    // XCD streams only its heads' K/V through its L2
     const int nqb = (a.T + QB - 1) / QB;
-    const int qb = nqb - 1 - (int)blockIdx.x;  // longest causal ranges first
-    const int g = blockIdx.y;
+    const int g = (int)blockIdx.x % a.nkv;
+    const int qb = nqb - 1 - (int)blockIdx.x / a.nkv;
     const int kvd = a.nkv * kPHD, qd = a.nq * kPHD;
 
     // this lane's query column in each of its 16-column tiles
@@ -360,7 +364,7 @@ hipError_t launch_attn_prefill(const AttnArgs &a, hipStream_t s) {
         return hipErrorInvalidValue;
     const int group = a.nq / a.nkv;
     const int QB = kPCols / group;
-    const dim3 grid((a.T + QB - 1) / QB, a.nkv);
+    const dim3 grid(((a.T + QB - 1) / QB) * a.nkv);
     switch (group) {
         case 1: hipLaunchKernelGGL(attn_prefill_kernel<1>, grid, dim3(kPWaves * 64), 0, s, a); break;
         case 2: hipLaunchKernelGGL(attn_prefill_kernel<2>, grid, dim3(kPWaves * 64), 0, s, a); break;
