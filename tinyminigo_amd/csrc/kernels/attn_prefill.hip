@@ -180,6 +180,8 @@ __global__ __launch_bounds__(kPWaves * 64) void attn_prefill_kernel(const AttnAr
     const int last_pos = a.start + min(a.T, (qb + 1) * QB) - 1;  // the workgroup's last query position
     const int nkb = last_pos / kPKB + 1;
 
+    // Q is pre-scaled by scale / ln 2, so the scores come out in log2 units
+    const float sl2 = a.scale * 1.4426950408889634f;
     // Q^T fragments (MFMA B operand): dims 32 ds + 8 q4 .. +7 of the column.
     // Loaded and consumed before any DMA is issued: the DMA waits below count
     // only DMAs.
@@ -191,42 +193,43 @@ __global__ __launch_bounds__(kPWaves * 64) void attn_prefill_kernel(const AttnAr
         for (int ds = 0; ds < 4; ds++) {
             const float4 v0 = *reinterpret_cast<const float4 *>(src + 32 * ds);
             const float4 v1 = *reinterpret_cast<const float4 *>(src + 32 * ds + 4);
-            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            const float v[8] = {v0.x * sl2, v0.y * sl2, v0.z * sl2, v0.w * sl2,
+                                v1.x * sl2, v1.y * sl2, v1.z * sl2, v1.w * sl2};
             split8(v, qh[qt][ds], ql[qt][ds]);
         }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    // DMA map: instruction i (of kPDma) of wave w is global instruction
-    // n = kPDma w + i of the block: n / 16 selects K hi, K lo, V^T hi, V^T lo,
-    // n % 16 the 1 KB slice (K rows 4 (n % 16) ..; V^T rows 8 (n % 16) ..)
+    // DMA map: wave w's instruction i fills 1 KB slice 2 w + (i & 1) of part
+    // i / 2 (K hi, K lo, V^T hi, V^T lo): K rows 4 slice .., V^T rows 8 slice ..
+    // K blocks go to a two-stage K ring, V^T blocks to a two-stage V ring.
+    static_assert(kPDma == 8 && kPWaves == 8, "two slices of each part per wave");
     const uint16_t *dsrc[kPDma];
     int ddst[kPDma];
 #pragma unroll
     for (int i = 0; i < kPDma; i++) {
-        const int n = kPDma * wave + i, part = n / 16, sl = n % 16;
+        const int part = i / 2, sl = 2 * wave + (i & 1);
         if (part < 2) {
             const int key = 4 * sl + (lane >> 4), pc = lane & 15;
             dsrc[i] = (part ? a.kl : a.kh) + (size_t)key * kvd + g * kPHD + k_chunk(key, pc) * 8;
+            ddst[i] = part * kPKTile + sl * 1024;
         } else {
             const int dim = 8 * sl + (lane >> 3), pc = lane & 7;
             dsrc[i] = (part == 3 ? a.vtl : a.vth) + ((size_t)g * kPHD + dim) * a.vt_pitch + vt_chunk(dim, pc) * 8;
+            ddst[i] = (part - 2) * kPVTile + sl * 1024;
         }
-        ddst[i] = (part < 2 ? part * kPKTile : 2 * kPKTile + (part - 2) * kPVTile) + sl * 1024;
     }
-    auto issue = [&](int kb) {
-        unsigned char *st = smem + (kb & 1) * kPStage;
+    constexpr int kKStage = 2 * kPKTile, kVStage = 2 * kPVTile;
+    unsigned char *const sKring = smem, *const sVring = smem + 2 * kKStage;
+    auto issue_k = [&](int kb) {  // K rows advance by 64 keys per block
 #pragma unroll
-        for (int i = 0; i < kPDma; i++) {
-            const int part = (kPDma * wave + i) / 16;
-            // K rows advance by 64 keys per block, V^T columns by 64 positions
-            const size_t adv = part < 2 ? (size_t)kb * kPKB * kvd : (size_t)kb * kPKB;
-            dma16(dsrc[i] + adv, st + ddst[i]);
-        }
+        for (int i = 0; i < 4; i++) dma16(dsrc[i] + (size_t)kb * kPKB * kvd, sKring + (kb & 1) * kKStage + ddst[i]);
     };
-    issue(0);
+    auto issue_v = [&](int kb) {  // V^T columns advance by 64 positions
+#pragma unroll
+        for (int i = 4; i < 8; i++) dma16(dsrc[i] + (size_t)kb * kPKB, sVring + (kb & 1) * kVStage + ddst[i]);
+    };
 
-    const float sl2 = a.scale * 1.4426950408889634f;  // scores in log2 units
     float m[kPQT], l[kPQT];
     f32x4 o[kPQT][8];
 #pragma unroll
@@ -237,70 +240,100 @@ __global__ __launch_bounds__(kPWaves * 64) void attn_prefill_kernel(const AttnAr
         for (int dt = 0; dt < 8; dt++) o[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    for (int kb = 0; kb < nkb; kb++) {
-        const int k0 = kb * kPKB;
-        // block kb landed (only its DMAs are outstanding) in every wave, and
-        // every wave is done with block kb - 1, whose stage block kb + 1 reuses
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        if (kb + 1 < nkb) issue(kb + 1);
-        const unsigned char *sK0 = smem + (kb & 1) * kPStage, *sK1 = sK0 + kPKTile;
-        const unsigned char *sV0 = sK0 + 2 * kPKTile, *sV1 = sV0 + kPVTile;
-
-        // S^T = K Q^T: 4 key tiles x 2 query tiles
-        f32x4 s[4][kPQT];
+    // S^T = K Q^T of block kb (K ring stage kb & 1): 4 key tiles x kPQT
+    // query tiles.  The K fragments of dim step ds + 1 are read while step
+    // ds is multiplied (the scheduling barriers keep the reads ahead).
+    auto scores = [&](int kb, f32x4 (&s)[4][kPQT]) {
+        const unsigned char *sK0 = sKring + (kb & 1) * kKStage, *sK1 = sK0 + kPKTile;
+        bf16x8 kf[2][4][2];
+        auto load = [&](int ds, bf16x8 (&f)[4][2]) {
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++) {
+                const int key = kt * 16 + r, ko = key * 256 + k_chunk(key, 4 * ds + q4) * 16;
+                f[kt][0] = *reinterpret_cast<const bf16x8 *>(sK0 + ko);
+                f[kt][1] = *reinterpret_cast<const bf16x8 *>(sK1 + ko);
+            }
+        };
 #pragma unroll
         for (int kt = 0; kt < 4; kt++)
 #pragma unroll
             for (int qt = 0; qt < kPQT; qt++) s[kt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        load(0, kf[0]);
 #pragma unroll
         for (int ds = 0; ds < 4; ds++) {
+            if (ds + 1 < 4) load(ds + 1, kf[(ds + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int kt = 0; kt < 4; kt++) {
-                const int key = kt * 16 + r, ko = key * 256 + k_chunk(key, 4 * ds + q4) * 16;
-                const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(sK0 + ko);
-                const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(sK1 + ko);
+            for (int kt = 0; kt < 4; kt++)
 #pragma unroll
                 for (int qt = 0; qt < kPQT; qt++) {
+                    const bf16x8 &kh = kf[ds & 1][kt][0], &kl = kf[ds & 1][kt][1];
                     s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[qt][ds], s[kt][qt], 0, 0, 0);
                     s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[qt][ds], s[kt][qt], 0, 0, 0);
                     s[kt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[qt][ds], s[kt][qt], 0, 0, 0);
                 }
-            }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // online softmax per query column; this lane holds keys k0 + 16 kt + 4 q4 + i
+    };
+    // online softmax of block kb per query column (this lane holds keys
+    // kb * 64 + 16 kt + 4 q4 + i); s becomes the probabilities.  Only blocks
+    // that reach past the workgroup's first query position need the causal
+    // mask.  The running maximum is raised only when a column's block
+    // maximum exceeds it by more than 2^8: the probabilities are taken
+    // against that reference (at most 2^8, no overflow) and O and the sum
+    // stay consistently scaled, so most blocks skip the rescale of O.
+    const int first_pos = a.start + qb * QB;
+    auto softmax = [&](int kb, f32x4 (&s)[4][kPQT]) {
+        const int k0 = kb * kPKB;
+        const bool diag = k0 + kPKB - 1 > first_pos;
 #pragma unroll
         for (int qt = 0; qt < kPQT; qt++) {
-            float mx = -INFINITY;
+            if (diag) {
+#pragma unroll
+                for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (k0 + 16 * kt + 4 * q4 + i > qpos[qt]) s[kt][qt][i] = -INFINITY;
+            }
+            float mx = s[0][qt][0];
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) mx = fmaxf(mx, s[kt][qt][i]);
+            mx = max_xor16_32(mx);  // finite: key 0 precedes every query
+            const bool raise = mx > m[qt] + 8.0f;
+            if (__builtin_amdgcn_ballot_w64(raise)) {
+                const float corr = raise ? __builtin_amdgcn_exp2f(m[qt] - mx) : 1.0f;
+                m[qt] = raise ? mx : m[qt];
+                l[qt] *= corr;
+#pragma unroll
+                for (int dt = 0; dt < 8; dt++) o[qt][dt] *= corr;
+            }
 #pragma unroll
             for (int kt = 0; kt < 4; kt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int kp = k0 + 16 * kt + 4 * q4 + i;
-                    const float x = kp <= qpos[qt] ? s[kt][qt][i] * sl2 : -INFINITY;
-                    s[kt][qt][i] = x;
-                    mx = fmaxf(mx, x);
-                }
-            mx = max_xor16_32(mx);
-            const float m_new = fmaxf(m[qt], mx);  // finite: key 0 precedes every query
-            const float corr = __builtin_amdgcn_exp2f(m[qt] - m_new);
-            m[qt] = m_new;
-            l[qt] *= corr;
-#pragma unroll
-            for (int dt = 0; dt < 8; dt++) o[qt][dt] *= corr;
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float p = __builtin_amdgcn_exp2f(s[kt][qt][i] - m_new);
+                    const float p = __builtin_amdgcn_exp2f(s[kt][qt][i] - m[qt]);
                     s[kt][qt][i] = p;
                     l[qt] += p;
                 }
         }
-        // O^T += V^T P^T, 32 keys per step: tiles 2 ks and 2 ks + 1
+    };
+    // O^T += V^T P^T of block kb (V ring stage kb & 1), 32 keys per step:
+    // tiles 2 ks and 2 ks + 1.  All 16 V^T fragments of a step are read
+    // before its MFMAs, which then wait only for the ones they use.
+    auto accumulate = [&](int kb, const f32x4 (&s)[4][kPQT]) {
+        const unsigned char *sV0 = sVring + (kb & 1) * kVStage, *sV1 = sV0 + kPVTile;
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
+            bf16x8 vf[8][2];
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                // keys 32 ks + 4 q4 .. +3 and 32 ks + 16 + 4 q4 .. +3: slots 32 ks + 8 q4 .. +7
+                const int dim = dt * 16 + r, vo = dim * 128 + vt_chunk(dim, 4 * ks + q4) * 16;
+                vf[dt][0] = *reinterpret_cast<const bf16x8 *>(sV0 + vo);
+                vf[dt][1] = *reinterpret_cast<const bf16x8 *>(sV1 + vo);
+            }
             bf16x8 ph[kPQT], pl[kPQT];
 #pragma unroll
             for (int qt = 0; qt < kPQT; qt++) {
@@ -309,21 +342,57 @@ __global__ __launch_bounds__(kPWaves * 64) void attn_prefill_kernel(const AttnAr
                                      s[2 * ks + 1][qt][2], s[2 * ks + 1][qt][3]};
                 split8(pv, ph[qt], pl[qt]);
             }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int dt = 0; dt < 8; dt++) {
-                // keys 32 ks + 4 q4 .. +3 and 32 ks + 16 + 4 q4 .. +3: slots 32 ks + 8 q4 .. +7
-                const int dim = dt * 16 + r, vo = dim * 128 + vt_chunk(dim, 4 * ks + q4) * 16;
-                const bf16x8 vh = *reinterpret_cast<const bf16x8 *>(sV0 + vo);
-                const bf16x8 vl = *reinterpret_cast<const bf16x8 *>(sV1 + vo);
+            for (int dt = 0; dt < 8; dt++)
 #pragma unroll
                 for (int qt = 0; qt < kPQT; qt++) {
-                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[qt], o[qt][dt], 0, 0, 0);
-                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl[qt], o[qt][dt], 0, 0, 0);
-                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph[qt], o[qt][dt], 0, 0, 0);
+                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[dt][0], ph[qt], o[qt][dt], 0, 0, 0);
+                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[dt][0], pl[qt], o[qt][dt], 0, 0, 0);
+                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[dt][1], ph[qt], o[qt][dt], 0, 0, 0);
                 }
-            }
+            __builtin_amdgcn_sched_barrier(0);
         }
+    };
+
+    // Software pipeline: iteration kb computes the scores of block kb + 1
+    // and the softmax of block kb, then O += V^T P^T of block kb.  The two
+    // wavefronts of a SIMD (w and w + 4) take those first two in opposite
+    // orders, so one's score MFMAs run while the other's softmax occupies
+    // the vector ALU.  K(kb + 1) and V(kb) are needed in iteration kb:
+    // issued in iteration kb - 1, waited for (vmcnt 0, only DMAs are
+    // outstanding) before the barrier that also retires every wave's reads
+    // of the stages K(kb + 2) and V(kb + 1) then overwrite.
+    issue_k(0);
+    issue_v(0);
+    if (nkb > 1) issue_k(1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    f32x4 sc[2][4][kPQT];
+    scores(0, sc[0]);
+    const bool scores_first = wave < 4;
+    auto iteration = [&](int kb, f32x4 (&cur)[4][kPQT], f32x4 (&nxt)[4][kPQT]) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kb + 2 < nkb) issue_k(kb + 2);
+        if (kb + 1 < nkb) issue_v(kb + 1);
+        if (scores_first) {
+            if (kb + 1 < nkb) scores(kb + 1, nxt);
+            softmax(kb, cur);
+        } else {
+            softmax(kb, cur);
+            if (kb + 1 < nkb) scores(kb + 1, nxt);
+        }
+        accumulate(kb, cur);
+    };
+    int kb = 0;
+    for (; kb + 1 < nkb; kb += 2) {
+        iteration(kb, sc[0], sc[1]);
+        iteration(kb + 1, sc[1], sc[0]);
     }
+    if (kb < nkb) iteration(kb, sc[0], sc[1]);
     // normalize and write the split-bf16 output: O^T rows dims 16 dt + 4 q4 + i
 #pragma unroll
     for (int qt = 0; qt < kPQT; qt++) {
