@@ -573,7 +573,8 @@ static int ensure_prefill(tmg_model *m, int T) {
         (rc = dev_alloc(m, &m->pf_q, (size_t)cap * m->qd)) || (rc = dev_alloc(m, &m->pf_hi, (size_t)cap * m->H)) ||
         (rc = dev_alloc(m, &m->pf_lo, (size_t)cap * m->H)) || (rc = dev_alloc(m, &m->pf_ahi, (size_t)cap * m->qd)) ||
         (rc = dev_alloc(m, &m->pf_alo, (size_t)cap * m->qd)) || (rc = dev_alloc(m, &m->pf_hhi, (size_t)cap * m->I)) ||
-        (rc = dev_alloc(m, &m->pf_hlo, (size_t)cap * m->I)))
+        (rc = dev_alloc(m, &m->pf_hlo, (size_t)cap * m->I)) ||
+        (rc = dev_alloc(m, &m->pf_nss, (size_t)cap * ((m->H + 63) / 64))))
         return rc;
     if (!m->pf_part) {
         const size_t nc = skinny_counters(std::max(std::max(m->qkv_rows, m->H), 2 * m->I));
@@ -612,11 +613,33 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
     TMG_HIP(hipMemcpyAsync(m->pf_tokens, m->pin, (size_t)T * 4, hipMemcpyHostToDevice, s));
     TMG_HIP(launch_embed_gather(m->pf_tokens, T, H, m->embed_bf16, m->embed_f32, m->pf_x, s));
     const int start = (int)c->len;
+    const float eps = m->cfg.rms_norm_eps;
+    // RMSNorm hand-off: the o_proj and down GEMMs write the next GEMM's
+    // operand (new residual times the norm weight, split-bf16) and per-64-row
+    // sums of squares, and QKV / gate-up apply the 1/rms scale in their
+    // epilogues, instead of a separate normalization pass over the residual
+    // (shapes permitting: hidden a multiple of 64, all four GEMMs on kernels
+    // with the staged epilogue)
+    const bool hand_off = H % 256 == 0 && H / 64 <= kMaxNormGroups && gemm_stages_output(m->qkv_rows, T, H) &&
+                          gemm_stages_output(H, T, qd) && gemm_stages_output(2 * I, T, H) &&
+                          gemm_stages_output(H, T, I);
+    auto norm_in = [&](GemmArgs &a) {  // consumer of a handed-off norm
+        a.nss_in = m->pf_nss;
+        a.ngroups = H / 64;
+        a.nrm_eps = eps;
+    };
+    auto norm_out = [&](GemmArgs &a, const float *w) {  // producer
+        a.nrm_w = w;
+        a.nss = m->pf_nss;
+        a.nx_hi = m->pf_hi;
+        a.nx_lo = m->pf_lo;
+    };
     for (int l = 0; l < m->L; l++) {
         const tmg_model::Layer &ly = m->layers[l];
         float *kc = c->k + (size_t)l * c->max_pos * kvd;
         float *vc = c->v + (size_t)l * c->max_pos * kvd;
-        TMG_HIP(launch_rmsnorm_split(m->pf_x, ly.in_norm, m->cfg.rms_norm_eps, T, H, m->pf_hi, m->pf_lo, s));
+        const bool in_handed = hand_off && l > 0;
+        if (!in_handed) TMG_HIP(launch_rmsnorm_split(m->pf_x, ly.in_norm, eps, T, H, m->pf_hi, m->pf_lo, s));
         GemmArgs g{};
         g.W = ly.qkv;
         g.Bhi = m->pf_hi;
@@ -636,6 +659,7 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         g.part = m->pf_part;
         g.cnt = m->pf_cnt;
         if (m->i8) g.wscale = ly.qkv_s;
+        if (in_handed) norm_in(g);
         TMG_HIP(launch_gemm(GEPI_QKV, g, s));
 
         AttnArgs aa{};
@@ -676,9 +700,10 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         o.part = m->pf_part;
         o.cnt = m->pf_cnt;
         if (m->i8) o.wscale = ly.o_s;
+        if (hand_off) norm_out(o, ly.post_norm);
         TMG_HIP(launch_gemm(GEPI_RESID, o, s));
 
-        TMG_HIP(launch_rmsnorm_split(m->pf_x, ly.post_norm, m->cfg.rms_norm_eps, T, H, m->pf_hi, m->pf_lo, s));
+        if (!hand_off) TMG_HIP(launch_rmsnorm_split(m->pf_x, ly.post_norm, eps, T, H, m->pf_hi, m->pf_lo, s));
         GemmArgs gu{};
         gu.W = ly.gu;
         gu.Bhi = m->pf_hi;
@@ -691,6 +716,7 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         gu.part = m->pf_part;
         gu.cnt = m->pf_cnt;
         if (m->i8) gu.wscale = ly.gu_s;
+        if (hand_off) norm_in(gu);
         TMG_HIP(launch_gemm(GEPI_SWIGLU, gu, s));
 
         GemmArgs d{};
@@ -704,6 +730,7 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         d.part = m->pf_part;
         d.cnt = m->pf_cnt;
         if (m->i8) d.wscale = ly.down_s;
+        if (hand_off && l + 1 < m->L) norm_out(d, m->layers[l + 1].in_norm);
         TMG_HIP(launch_gemm(GEPI_RESID, d, s));
     }
     // final norm of the last row (batch association) + lm_head + argmax

@@ -55,6 +55,7 @@ struct tmg_model {
              *pf_hlo = nullptr;
     // split-K partial tiles and arrival counters of the short-prompt GEMM
     float *pf_part = nullptr;
+    float *pf_nss = nullptr;  // per-64-row sums of squares of the residual handed to the next GEMM
     unsigned *pf_cnt = nullptr;
     // split-bf16 KV rows for the MFMA prefill attention (rows [0, kv_cap))
     int kv_cap = 0;

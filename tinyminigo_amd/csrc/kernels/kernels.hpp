@@ -210,6 +210,21 @@ struct GemmArgs {
     float *const *k_seq;
     float *const *v_seq;
     size_t kv_layer_off;
+    // RMSNorm handed from one GEMM to the next (prefill; kernels whose output
+    // goes through stage_epilogue, see gemm_stages_output).  Producer (RESID,
+    // M a multiple of 64): with nrm_w set it also writes the new residual
+    // rows times nrm_w as split-bf16 planes nx_hi / nx_lo [N][M] and, per
+    // token n and 64-row group g, the rows' sum of squares to
+    // nss[n * (M / 64) + g].  Consumer: with nss_in set (ngroups = K / 64, a
+    // multiple of 4 up to kMaxNormGroups) it scales its output by
+    // 1 / sqrt(sum of token n's partials in group order / K + nrm_eps) before
+    // the epilogue, so that its operand needs no separate normalization.
+    const float *nrm_w;
+    float *nss;
+    uint16_t *nx_hi, *nx_lo;
+    const float *nss_in;
+    int ngroups;
+    float nrm_eps;
     // split-K workspace of the short-prompt kernel: partial tiles and one
     // arrival counter per quarter tile (zero between launches; each launch
     // leaves them zero).  Null disables split-K.
@@ -222,6 +237,10 @@ struct GemmArgs {
 // multiple of 64) or the 16x64 streaming kernel.
 constexpr int kTiledMinTokens = 256;
 hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s);
+// Whether launch_gemm takes a kernel whose output goes through
+// stage_epilogue for these shapes (the only ones that honour nrm_w / nss_in).
+bool gemm_stages_output(int M, int N, int K);
+constexpr int kMaxNormGroups = 40;  // hidden sizes up to 2560 for the norm hand-off
 // Workspace the short-prompt kernel needs: floats of partials and counters
 // for any GEMM with at most `max_m` rows and fewer than kTiledMinTokens tokens.
 constexpr size_t kSkinnyPartFloats = (size_t)768 * 64 * 64;

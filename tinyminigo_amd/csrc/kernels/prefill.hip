@@ -19,6 +19,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 __global__ __launch_bounds__(kBlock) void embed_gather_kernel(const int *tokens, int H, const uint16_t *eb,
                                                              const float *ef, float *x) {
@@ -153,12 +154,17 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &a, int mb, int n, con
 // The epilogue of rows mb .. mb+3 (mb a multiple of 4) of token column n with
 // 16-, 8- or 4-byte accesses per lane; gemm_store at the edges and for the
 // shapes the vector forms do not cover (M or head_dim not a multiple of 4).
+//
+// Returns, for RESID with a norm hand-off (a.nrm_w), the sum of squares of the
+// four new residual values, after writing them times nrm_w as split-bf16 to
+// nx_hi / nx_lo; 0 otherwise.  The hand-off is only set up for M a multiple
+// of 64, so it never meets the per-element edge path.
 template <int EPI>
-__device__ __forceinline__ void gemm_store4(const GemmArgs &a, int mb, int n, const f32x4 &acc) {
-    if (n >= a.N) return;
+__device__ __forceinline__ float gemm_store4(const GemmArgs &a, int mb, int n, const f32x4 &acc) {
+    if (n >= a.N) return 0.0f;
     if (mb + 3 >= a.M || (a.M & 3) || (EPI == GEPI_QKV && (a.hd & 3))) {
         gemm_store<EPI>(a, mb, n, acc);
-        return;
+        return 0.0f;
     }
     f32x4 v = acc;
     if (a.wscale) {
@@ -174,6 +180,22 @@ __device__ __forceinline__ void gemm_store4(const GemmArgs &a, int mb, int n, co
 #pragma unroll
             for (int i = 0; i < 4; i++) y[i] = y[i] + v[i];
             *yr = y;
+            if (a.nrm_w) {
+                const f32x4 w = *reinterpret_cast<const f32x4 *>(a.nrm_w + mb);
+                uint32_t hi[2], lo[2];
+#pragma unroll
+                for (int pr = 0; pr < 2; pr++) {
+                    uint16_t h0, l0, h1, l1;
+                    split_bf16(y[2 * pr] * w[2 * pr], &h0, &l0);
+                    split_bf16(y[2 * pr + 1] * w[2 * pr + 1], &h1, &l1);
+                    hi[pr] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                    lo[pr] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+                }
+                const size_t o = (size_t)n * a.M + mb;
+                *reinterpret_cast<u32x2 *>(a.nx_hi + o) = u32x2{hi[0], hi[1]};
+                *reinterpret_cast<u32x2 *>(a.nx_lo + o) = u32x2{lo[0], lo[1]};
+                return (y[0] * y[0] + y[1] * y[1]) + (y[2] * y[2] + y[3] * y[3]);
+            }
         } else {
             *yr = v;
         }
@@ -218,6 +240,7 @@ __device__ __forceinline__ void gemm_store4(const GemmArgs &a, int mb, int n, co
         *reinterpret_cast<float2 *>(dst + j) = o0;
         *reinterpret_cast<float2 *>(dst + j + half) = o1;
     }
+    return 0.0f;
 }
 
 // The output of one wavefront's FI x FJ MFMA fragments (fragment (i, j): rows
@@ -236,8 +259,26 @@ template <int EPI, int FI, int FJ>
 __device__ __forceinline__ void stage_epilogue(const GemmArgs &a, float *buf, int mw, int nw,
                                                const f32x4 (&acc)[FI][FJ]) {
     static_assert(FI % 4 == 0, "64-row passes");
+    static_assert(FJ * 16 <= 64, "one token per lane for the norm scales");
     const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
     const int nsub = lane >> 4;
+    // norm hand-off, consumer side: lane l holds the scale of token
+    // nw + l % (16 FJ); the token's partial sums are contiguous and all of
+    // them are loaded at once (one memory round trip), then added in order
+    float inv_l = 1.0f;
+    if (a.nss_in) {
+        const int n = min(nw + (lane & (FJ * 16 - 1)), a.N - 1);
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(a.nss_in + (size_t)n * a.ngroups);
+        f32x4 p[kMaxNormGroups / 4];
+#pragma unroll
+        for (int i = 0; i < kMaxNormGroups / 4; i++)
+            if (4 * i < a.ngroups) p[i] = src[i];
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kMaxNormGroups / 4; i++)
+            if (4 * i < a.ngroups) ss = ((ss + p[i][0]) + p[i][1]) + (p[i][2] + p[i][3]);
+        inv_l = 1.0f / sqrtf(ss / (float)a.K + a.nrm_eps);
+    }
 #pragma unroll
     for (int h = 0; h < FI / 4; h++) {
 #pragma unroll
@@ -249,8 +290,22 @@ __device__ __forceinline__ void stage_epilogue(const GemmArgs &a, float *buf, in
 #pragma unroll
         for (int rr = 0; rr < FJ * 4; rr++) {
             const int nl = rr * 4 + nsub;
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(buf + nl * kStagePitch + ((r ^ (nl & 15)) * 4));
-            gemm_store4<EPI>(a, mw + h * 64 + r * 4, nw + nl, v);
+            f32x4 v = *reinterpret_cast<const f32x4 *>(buf + nl * kStagePitch + ((r ^ (nl & 15)) * 4));
+            if (a.nss_in) {
+                const float inv = __shfl(inv_l, nl);
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = v[i] * inv;
+            }
+            const float sq = gemm_store4<EPI>(a, mw + h * 64 + r * 4, nw + nl, v);
+            if constexpr (EPI == GEPI_RESID) {
+                // norm hand-off, producer side: the 16 lanes of token nl hold
+                // its 64 rows of this pass
+                if (a.nrm_w) {
+                    const float tot = group_sum<16>(sq);
+                    const int m64 = mw + h * 64, n = nw + nl;
+                    if (r == 0 && n < a.N && m64 < a.M) a.nss[(size_t)n * (a.M >> 6) + (m64 >> 6)] = tot;
+                }
+            }
         }
     }
 }
@@ -750,8 +805,17 @@ hipError_t launch_rmsnorm_split(const float *x, const float *w, float eps, int T
     return hipGetLastError();
 }
 
+bool gemm_stages_output(int M, int N, int K) {
+    if (K % 32 != 0 || M <= 0 || N <= 0) return false;
+    if (N >= kTiledMinTokens && ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN) >= 240) return true;
+    return K % 64 == 0;  // the 128 x 128 tiled or the split-K kernel
+}
+
 hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
     if (a.K % 32 != 0 || a.M <= 0 || a.N <= 0) return hipErrorInvalidValue;
+    if ((a.nrm_w || a.nss_in) && !gemm_stages_output(a.M, a.N, a.K)) return hipErrorInvalidValue;
+    if (a.nrm_w && (epi != GEPI_RESID || a.M % 64 != 0 || !a.nss || !a.nx_hi || !a.nx_lo)) return hipErrorInvalidValue;
+    if (a.nss_in && (a.ngroups <= 0 || a.ngroups > kMaxNormGroups || a.ngroups % 4)) return hipErrorInvalidValue;
     // the 256 x 256 tile once its grid is about a workgroup per CU
     if (a.N >= kTiledMinTokens && a.K % kBK == 0 && ((a.M + kBM - 1) / kBM) * ((a.N + kBN - 1) / kBN) >= 240) {
         const dim3 grid((a.M + kBM - 1) / kBM, (a.N + kBN - 1) / kBN);
