@@ -65,6 +65,9 @@ struct Batch {
     float *attn = nullptr, *h = nullptr;
     unsigned long long *parts = nullptr;
     int nparts = 0;
+    // the MFMA path's RMSNorm hand-off between GEMMs: per-64-row sums of
+    // squares [B][H / 64] (null: separate normalization passes)
+    float *nss = nullptr;
 };
 
 // A decode step for B <= kMtMaxSeq sequences: the decode GEMVs over all B
@@ -164,12 +167,29 @@ int enqueue_batch_step(tmg_model *m, const Batch &bt) {
     hipStream_t s = m->stream;
     const int B = bt.B, H = m->H, I = m->I, qd = m->qd, kvd = m->kvd;
     const float eps = m->cfg.rms_norm_eps;
+    // RMSNorm hand-off as in the prefill (o_proj / down epilogues produce the
+    // next GEMM's normalized operand up to its 1/rms scale, which QKV,
+    // gate/up and lm_head apply in their epilogues)
+    const bool hand_off = bt.nss != nullptr;
+    auto norm_in = [&](GemmArgs &a) {
+        a.nss_in = bt.nss;
+        a.ngroups = H / 64;
+        a.nrm_eps = eps;
+    };
+    auto norm_out = [&](GemmArgs &a, const float *w) {
+        a.nrm_w = w;
+        a.nss = bt.nss;
+        a.nx_hi = bt.hi;
+        a.nx_lo = bt.lo;
+    };
     TMG_HIPB(launch_embed_gather(bt.tokens, B, H, m->embed_bf16, m->embed_f32, bt.x, s));
     for (int l = 0; l < m->L; l++) {
         const tmg_model::Layer &ly = m->layers[l];
         const size_t layer_off = (size_t)l * bt.max_pos * kvd;
-        // forward_token's RMSNorm association, (v*inv)*w (src/tensor.rs:975)
-        TMG_HIPB(launch_rmsnorm_split(bt.x, ly.in_norm, eps, B, H, bt.hi, bt.lo, s, true));
+        // forward_token's RMSNorm association, (v*inv)*w (src/tensor.rs:975),
+        // when the norm is a separate pass
+        const bool in_handed = hand_off && l > 0;
+        if (!in_handed) TMG_HIPB(launch_rmsnorm_split(bt.x, ly.in_norm, eps, B, H, bt.hi, bt.lo, s, true));
         GemmArgs g{};
         g.W = ly.qkv;
         g.Bhi = bt.hi;
@@ -189,6 +209,7 @@ int enqueue_batch_step(tmg_model *m, const Batch &bt) {
         g.kv_layer_off = layer_off;
         g.part = m->pf_part;
         g.cnt = m->pf_cnt;
+        if (in_handed) norm_in(g);
         TMG_HIPB(launch_gemm(GEPI_QKV, g, s));
 
         AttnArgs aa{};
@@ -219,9 +240,10 @@ int enqueue_batch_step(tmg_model *m, const Batch &bt) {
         o.y = bt.x;
         o.part = m->pf_part;
         o.cnt = m->pf_cnt;
+        if (hand_off) norm_out(o, ly.post_norm);
         TMG_HIPB(launch_gemm(GEPI_RESID, o, s));
 
-        TMG_HIPB(launch_rmsnorm_split(bt.x, ly.post_norm, eps, B, H, bt.hi, bt.lo, s, true));
+        if (!hand_off) TMG_HIPB(launch_rmsnorm_split(bt.x, ly.post_norm, eps, B, H, bt.hi, bt.lo, s, true));
         GemmArgs gu{};
         gu.W = ly.gu;
         gu.Bhi = bt.hi;
@@ -233,6 +255,7 @@ int enqueue_batch_step(tmg_model *m, const Batch &bt) {
         gu.h_lo = bt.hlo;
         gu.part = m->pf_part;
         gu.cnt = m->pf_cnt;
+        if (hand_off) norm_in(gu);
         TMG_HIPB(launch_gemm(GEPI_SWIGLU, gu, s));
 
         GemmArgs d{};
@@ -245,9 +268,10 @@ int enqueue_batch_step(tmg_model *m, const Batch &bt) {
         d.y = bt.x;
         d.part = m->pf_part;
         d.cnt = m->pf_cnt;
+        if (hand_off) norm_out(d, l + 1 < m->L ? m->layers[l + 1].in_norm : m->final_norm);
         TMG_HIPB(launch_gemm(GEPI_RESID, d, s));
     }
-    TMG_HIPB(launch_rmsnorm_split(bt.x, m->final_norm, eps, B, H, bt.hi, bt.lo, s, true));
+    if (!hand_off) TMG_HIPB(launch_rmsnorm_split(bt.x, m->final_norm, eps, B, H, bt.hi, bt.lo, s, true));
     GemmArgs lm{};  // no split-K: the lm_head's row tiles alone fill the GPU
     lm.W = m->lm_head;
     lm.Bhi = bt.hi;
@@ -256,6 +280,7 @@ int enqueue_batch_step(tmg_model *m, const Batch &bt) {
     lm.N = B;
     lm.K = H;
     lm.y = bt.logits;
+    if (hand_off) norm_in(lm);
     TMG_HIPB(launch_gemm(GEPI_STORE, lm, s));
     BatchSelectArgs sa{bt.logits, m->V, B, bt.tokens, bt.pos, bt.plen, bt.out, bt.out_stride};
     TMG_HIPB(launch_batch_select(sa, s));
@@ -310,6 +335,12 @@ extern "C" int tmg_generate_batch(tmg_model *m, const uint32_t *const *prompts, 
         (rc = al.get(&bt.hlo, (size_t)B * m->I)) || (rc = al.get(&st, B)))
         return rc;
     const bool mt = B <= kMtMaxSeq;
+    const int H = m->H, I = m->I;
+    if (!mt && H % 256 == 0 && H / 64 <= kMaxNormGroups && gemm_stages_output(m->qkv_rows, B, H) &&
+        gemm_stages_output(H, B, m->qd) && gemm_stages_output(2 * I, B, H) && gemm_stages_output(H, B, I) &&
+        gemm_stages_output(m->V, B, H)) {
+        if ((rc = al.get(&bt.nss, (size_t)B * (H / 64)))) return rc;
+    }
     if (mt) {
         bt.nparts = gemv_mt_blocks(m->V, m->H, B);
         if ((rc = al.get(&bt.attn, (size_t)B * m->qd)) || (rc = al.get(&bt.h, (size_t)B * m->I)) ||
