@@ -151,53 +151,61 @@ __device__ __forceinline__ void gemm_store(const GemmArgs &a, int mb, int n, con
     }
 }
 
-// The epilogue of rows mb .. mb+3 (mb a multiple of 4) of token column n with
-// 16-, 8- or 4-byte accesses per lane; gemm_store at the edges and for the
-// shapes the vector forms do not cover (M or head_dim not a multiple of 4).
-//
-// Returns, for RESID with a norm hand-off (a.nrm_w), the sum of squares of the
-// four new residual values, after writing them times nrm_w as split-bf16 to
-// nx_hi / nx_lo; 0 otherwise.  The hand-off is only set up for M a multiple
-// of 64, so it never meets the per-element edge path.
+// The vector epilogue of rows mb .. mb+3 (mb a multiple of 4) of token column
+// n, in two phases so that a batch of tokens issues all its loads before any
+// of its stores (the compiler cannot reorder a token's loads above another
+// token's stores, so a one-phase epilogue pays one memory round trip per
+// token).  Used where the rows are inside M, M is a multiple of 4 and (QKV)
+// head_dim is a multiple of 4; gemm_store covers the rest element by element.
+struct Epi4Tok {
+    f32x4 y;      // RESID: the residual rows before the add
+    float2 c, s;  // QKV: RoPE cos / sin of the rotation pairs j, j+1
+    int pos;      // QKV: the token's position
+};
+
 template <int EPI>
-__device__ __forceinline__ float gemm_store4(const GemmArgs &a, int mb, int n, const f32x4 &acc) {
-    if (n >= a.N) return 0.0f;
-    if (mb + 3 >= a.M || (a.M & 3) || (EPI == GEPI_QKV && (a.hd & 3))) {
-        gemm_store<EPI>(a, mb, n, acc);
-        return 0.0f;
+__device__ __forceinline__ void epi4_load(const GemmArgs &a, int mb, int n, Epi4Tok &t) {
+    if constexpr (EPI == GEPI_RESID) t.y = *reinterpret_cast<const f32x4 *>(a.y + (size_t)n * a.M + mb);
+    if constexpr (EPI == GEPI_QKV) {
+        const int half = a.hd >> 1;
+        const int P = mb >> 1;
+        const int head = P / half, j = P - head * half;
+        t.pos = a.pos_seq ? a.pos_seq[n] : a.start + n;
+        if (head < a.nq + a.nkv) {
+            t.c = *reinterpret_cast<const float2 *>(a.rope_cos + (size_t)t.pos * half + j);
+            t.s = *reinterpret_cast<const float2 *>(a.rope_sin + (size_t)t.pos * half + j);
+        }
     }
-    f32x4 v = acc;
-    if (a.wscale) {
-#pragma clang fp contract(off)
-        const f32x4 sc = *reinterpret_cast<const f32x4 *>(a.wscale + mb);
+}
+
+// Phase two: v already carries the norm scale and the int8 row scale.
+// Returns, for RESID with a norm hand-off (a.nrm_w; nw = nrm_w[mb .. mb+3]),
+// the sum of squares of the four new residual values, after writing them
+// times nrm_w as split-bf16 to nx_hi / nx_lo; 0 otherwise.
+template <int EPI>
+__device__ __forceinline__ float epi4_finish(const GemmArgs &a, int mb, int n, const f32x4 &v, const Epi4Tok &t,
+                                             const f32x4 &nw) {
+    if constexpr (EPI == GEPI_STORE) {
+        *reinterpret_cast<f32x4 *>(a.y + (size_t)n * a.M + mb) = v;
+    } else if constexpr (EPI == GEPI_RESID) {
+        f32x4 y = t.y;
 #pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = v[i] * sc[i];
-    }
-    if constexpr (EPI == GEPI_STORE || EPI == GEPI_RESID) {
-        f32x4 *yr = reinterpret_cast<f32x4 *>(a.y + (size_t)n * a.M + mb);
-        if constexpr (EPI == GEPI_RESID) {
-            f32x4 y = *yr;
+        for (int i = 0; i < 4; i++) y[i] = y[i] + v[i];
+        const size_t o = (size_t)n * a.M + mb;
+        *reinterpret_cast<f32x4 *>(a.y + o) = y;
+        if (a.nrm_w) {
+            uint32_t hi[2], lo[2];
 #pragma unroll
-            for (int i = 0; i < 4; i++) y[i] = y[i] + v[i];
-            *yr = y;
-            if (a.nrm_w) {
-                const f32x4 w = *reinterpret_cast<const f32x4 *>(a.nrm_w + mb);
-                uint32_t hi[2], lo[2];
-#pragma unroll
-                for (int pr = 0; pr < 2; pr++) {
-                    uint16_t h0, l0, h1, l1;
-                    split_bf16(y[2 * pr] * w[2 * pr], &h0, &l0);
-                    split_bf16(y[2 * pr + 1] * w[2 * pr + 1], &h1, &l1);
-                    hi[pr] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-                    lo[pr] = (uint32_t)l0 | ((uint32_t)l1 << 16);
-                }
-                const size_t o = (size_t)n * a.M + mb;
-                *reinterpret_cast<u32x2 *>(a.nx_hi + o) = u32x2{hi[0], hi[1]};
-                *reinterpret_cast<u32x2 *>(a.nx_lo + o) = u32x2{lo[0], lo[1]};
-                return (y[0] * y[0] + y[1] * y[1]) + (y[2] * y[2] + y[3] * y[3]);
+            for (int pr = 0; pr < 2; pr++) {
+                uint16_t h0, l0, h1, l1;
+                split_bf16(y[2 * pr] * nw[2 * pr], &h0, &l0);
+                split_bf16(y[2 * pr + 1] * nw[2 * pr + 1], &h1, &l1);
+                hi[pr] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                lo[pr] = (uint32_t)l0 | ((uint32_t)l1 << 16);
             }
-        } else {
-            *yr = v;
+            *reinterpret_cast<u32x2 *>(a.nx_hi + o) = u32x2{hi[0], hi[1]};
+            *reinterpret_cast<u32x2 *>(a.nx_lo + o) = u32x2{lo[0], lo[1]};
+            return (y[0] * y[0] + y[1] * y[1]) + (y[2] * y[2] + y[3] * y[3]);
         }
     } else if constexpr (EPI == GEPI_SWIGLU) {
         // pairs (mb, mb+1) and (mb+2, mb+3) -> h[P], h[P+1], P = mb / 2
@@ -216,26 +224,23 @@ __device__ __forceinline__ float gemm_store4(const GemmArgs &a, int mb, int n, c
         const int half = a.hd >> 1;
         const int P = mb >> 1;
         const int head = P / half, j = P - head * half;
-        const int pos = a.pos_seq ? a.pos_seq[n] : a.start + n;
         const int kvd = a.nkv * a.hd;
         float *dst;
         float2 o0, o1;  // values at j, j+1 and at j+half, j+half+1
         if (head < a.nq + a.nkv) {
-            const float2 c = *reinterpret_cast<const float2 *>(a.rope_cos + (size_t)pos * half + j);
-            const float2 sn = *reinterpret_cast<const float2 *>(a.rope_sin + (size_t)pos * half + j);
-            rope_pair(v[0], v[1], c.x, sn.x, &o0.x, &o1.x);
-            rope_pair(v[2], v[3], c.y, sn.y, &o0.y, &o1.y);
+            rope_pair(v[0], v[1], t.c.x, t.s.x, &o0.x, &o1.x);
+            rope_pair(v[2], v[3], t.c.y, t.s.y, &o0.y, &o1.y);
             if (head < a.nq) {
                 dst = a.q_out + (size_t)n * a.nq * a.hd + head * a.hd;
             } else {
                 float *const kcache = a.k_seq ? a.k_seq[n] + a.kv_layer_off : a.k_cache;
-                dst = kcache + (size_t)pos * kvd + (head - a.nq) * a.hd;
+                dst = kcache + (size_t)t.pos * kvd + (head - a.nq) * a.hd;
             }
         } else {
             o0 = make_float2(v[0], v[2]);
             o1 = make_float2(v[1], v[3]);
             float *const vcache = a.v_seq ? a.v_seq[n] + a.kv_layer_off : a.v_cache;
-            dst = vcache + (size_t)pos * kvd + (head - a.nq - a.nkv) * a.hd;
+            dst = vcache + (size_t)t.pos * kvd + (head - a.nq - a.nkv) * a.hd;
         }
         *reinterpret_cast<float2 *>(dst + j) = o0;
         *reinterpret_cast<float2 *>(dst + j + half) = o1;
@@ -247,19 +252,25 @@ __device__ __forceinline__ float gemm_store4(const GemmArgs &a, int mb, int n, c
 // mw + 16 i + 4 (lane >> 4) .. +3 of token nw + 16 j + (lane & 15)) through
 // the wavefront's own LDS region `buf` (FJ 16 token rows of 64 floats), 64
 // rows at a time: written as [token][row], read back as four consecutive rows
-// per lane, so that 16 lanes cover 64 consecutive rows of one token for
-// gemm_store4.  The 16-byte chunk c of token t sits at chunk c ^ (t & 15):
-// both the fragment writes and the row reads are then free of bank conflicts
-// (measured; a padded 68-float pitch conflicts on the reads).  LDS accesses
-// of one wavefront execute in order, so no barrier separates the writes from
-// the reads.
+// per lane, so that 16 lanes cover 64 consecutive rows of one token.  The
+// 16-byte chunk c of token t sits at chunk c ^ (t & 15): both the fragment
+// writes and the row reads are then free of bank conflicts (measured; a
+// padded 68-float pitch conflicts on the reads).  LDS accesses of one
+// wavefront execute in order, so no barrier separates the writes from the
+// reads.  Tokens go through the epilogue in batches of NB, each batch's loads
+// (residual rows, RoPE tables) issued before its stores: the split-K
+// kernel's last-arriving wave, whose epilogue ends the GEMM, takes NB = 4
+// (64-token prefill 1.72 -> 1.70 ms); the tiled kernels, whose epilogues
+// overlap other workgroups' main loops, measured faster with NB = 1.
 constexpr int kStagePitch = 64;  // floats per staged token row
 
-template <int EPI, int FI, int FJ>
+template <int EPI, int FI, int FJ, int NB>
 __device__ __forceinline__ void stage_epilogue(const GemmArgs &a, float *buf, int mw, int nw,
                                                const f32x4 (&acc)[FI][FJ]) {
     static_assert(FI % 4 == 0, "64-row passes");
     static_assert(FJ * 16 <= 64, "one token per lane for the norm scales");
+    constexpr int NR = FJ * 4;  // token rows per lane per pass
+    static_assert(NR % NB == 0, "whole batches");
     const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
     const int nsub = lane >> 4;
     // norm hand-off, consumer side: lane l holds the scale of token
@@ -287,23 +298,54 @@ __device__ __forceinline__ void stage_epilogue(const GemmArgs &a, float *buf, in
             for (int j = 0; j < FJ; j++)
                 *reinterpret_cast<f32x4 *>(buf + (j * 16 + r) * kStagePitch + (((ii * 4 + q4) ^ r) * 4)) =
                     acc[4 * h + ii][j];
+        const int mb = mw + h * 64 + r * 4;
+        const bool rows_vec = mb + 3 < a.M && !(a.M & 3) && !(EPI == GEPI_QKV && (a.hd & 3));
+        // per-row inputs, the same for every token of the pass
+        f32x4 sc = {1.f, 1.f, 1.f, 1.f}, nrw = {0.f, 0.f, 0.f, 0.f};
+        if (rows_vec && a.wscale) sc = *reinterpret_cast<const f32x4 *>(a.wscale + mb);
+        if constexpr (EPI == GEPI_RESID)
+            if (rows_vec && a.nrm_w) nrw = *reinterpret_cast<const f32x4 *>(a.nrm_w + mb);
 #pragma unroll
-        for (int rr = 0; rr < FJ * 4; rr++) {
-            const int nl = rr * 4 + nsub;
-            f32x4 v = *reinterpret_cast<const f32x4 *>(buf + nl * kStagePitch + ((r ^ (nl & 15)) * 4));
-            if (a.nss_in) {
-                const float inv = __shfl(inv_l, nl);
+        for (int r0 = 0; r0 < NR; r0 += NB) {
+            f32x4 v[NB];
+            Epi4Tok tk[NB];
 #pragma unroll
-                for (int i = 0; i < 4; i++) v[i] = v[i] * inv;
+            for (int b = 0; b < NB; b++) {
+                const int nl = (r0 + b) * 4 + nsub;
+                v[b] = *reinterpret_cast<const f32x4 *>(buf + nl * kStagePitch + ((r ^ (nl & 15)) * 4));
+                if (a.nss_in) {
+                    const float inv = __shfl(inv_l, nl);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) v[b][i] = v[b][i] * inv;
+                }
+                if (rows_vec && nw + nl < a.N) epi4_load<EPI>(a, mb, nw + nl, tk[b]);
             }
-            const float sq = gemm_store4<EPI>(a, mw + h * 64 + r * 4, nw + nl, v);
-            if constexpr (EPI == GEPI_RESID) {
-                // norm hand-off, producer side: the 16 lanes of token nl hold
-                // its 64 rows of this pass
-                if (a.nrm_w) {
-                    const float tot = group_sum<16>(sq);
-                    const int m64 = mw + h * 64, n = nw + nl;
-                    if (r == 0 && n < a.N && m64 < a.M) a.nss[(size_t)n * (a.M >> 6) + (m64 >> 6)] = tot;
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                const int nl = (r0 + b) * 4 + nsub, n = nw + nl;
+                float sq = 0.0f;
+                if (n < a.N) {
+                    if (rows_vec) {
+                        f32x4 vv = v[b];
+                        if (a.wscale) {
+#pragma clang fp contract(off)
+#pragma unroll
+                            for (int i = 0; i < 4; i++) vv[i] = vv[i] * sc[i];
+                        }
+                        sq = epi4_finish<EPI>(a, mb, n, vv, tk[b], nrw);
+                    } else {
+                        gemm_store<EPI>(a, mb, n, v[b]);
+                    }
+                }
+                if constexpr (EPI == GEPI_RESID) {
+                    // norm hand-off, producer side: the 16 lanes of token nl
+                    // hold its 64 rows of this pass (the hand-off is set up
+                    // only for M a multiple of 64, so rows_vec holds there)
+                    if (a.nrm_w) {
+                        const float tot = group_sum<16>(sq);
+                        const int m64 = mw + h * 64;
+                        if (r == 0 && n < a.N && m64 < a.M) a.nss[(size_t)n * (a.M >> 6) + (m64 >> 6)] = tot;
+                    }
                 }
             }
         }
@@ -463,7 +505,7 @@ __global__ __launch_bounds__(kGWaves * 64) void gemm_dma_kernel(const GemmArgs a
     }
     // the ring is free once every wave is past its last fragment reads
     __builtin_amdgcn_s_barrier();
-    stage_epilogue<EPI, 4, NJ>(a, reinterpret_cast<float *>(smem) + wave * NJ * 16 * kStagePitch, m0 + wm * 64,
+    stage_epilogue<EPI, 4, NJ, 1>(a, reinterpret_cast<float *>(smem) + wave * NJ * 16 * kStagePitch, m0 + wm * 64,
                                n0 + wn * NJ * 16, acc);
 }
 
@@ -617,7 +659,7 @@ __global__ __launch_bounds__(kGWaves * 64) void gemm_big_kernel(const GemmArgs a
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fl[j], acc[i][j], 0, 0, 0);
     // the ring is free once every wave is past its last fragment reads
     __builtin_amdgcn_s_barrier();
-    stage_epilogue<EPI, FI, FJ>(a, reinterpret_cast<float *>(smem) + wave * FJ * 16 * kStagePitch, m0 + wm * 128,
+    stage_epilogue<EPI, FI, FJ, 1>(a, reinterpret_cast<float *>(smem) + wave * FJ * 16 * kStagePitch, m0 + wm * 128,
                                 n0 + wn * 64, acc);
 }
 
@@ -754,7 +796,7 @@ __global__ __launch_bounds__(kBlock, 2) void gemm_skinny_kernel(const GemmArgs a
         if (lane == 0) __hip_atomic_store(&a.cnt[slot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     const f32x4 out[4][1] = {{acc[0]}, {acc[1]}, {acc[2]}, {acc[3]}};
-    stage_epilogue<EPI, 4, 1>(a, reinterpret_cast<float *>(smem) + wave * 16 * kStagePitch, m0, n0 + wave * 16, out);
+    stage_epilogue<EPI, 4, 1, 4>(a, reinterpret_cast<float *>(smem) + wave * 16 * kStagePitch, m0, n0 + wave * 16, out);
 }
 
 hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
