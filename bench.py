@@ -208,12 +208,17 @@ def extra_long_context(T, W, m, sync):
     t = time.perf_counter()
     lg = m.forward_seq(prompt, c)
     sync()
-    prefill_s = time.perf_counter() - t
+    first_prefill_s = time.perf_counter() - t
     first = int(np.argmax(lg))
     m.decode_greedy(first, 4, c)
     c.reset()
+    # the timed prefill: the first one also grew the model's prefill scratch
+    # to 8192 tokens (device allocations, once per model)
+    sync()
+    t = time.perf_counter()
     m.forward_seq(prompt, c, want_logits=False)
     sync()
+    prefill_s = time.perf_counter() - t
     t = time.perf_counter()
     toks, ev_ms = m.decode_greedy(first, K, c)
     sync()
@@ -224,7 +229,8 @@ def extra_long_context(T, W, m, sync):
     per = kernel_table(m, c, int(toks[-1]))
     attn = per.get("attn_decode")
     c.close()
-    log(f"8k: prefill {prefill_s * 1e3:.1f} ms, decode {ms_step:.4f} ms/step")
+    log(f"8k: prefill {prefill_s * 1e3:.1f} ms (first, with scratch allocation: {first_prefill_s * 1e3:.1f} ms), "
+        f"decode {ms_step:.4f} ms/step")
     return {
         "workload": f"{wl.name}: {P}-token prompt, batched prefill, {K} greedy decode steps",
         "ms_per_step": round(ms_step, 4), "tok_s": round(K / wall, 1), "decode_ms_events": round(ev_ms, 3),
@@ -234,6 +240,7 @@ def extra_long_context(T, W, m, sync):
                          "GB_s": round(attn[1] / (attn[2] * 1e-3) / 1e9, 1)} if attn else None),
         "prefill_ms": round(prefill_s * 1e3, 2), "prefill_tok_s": round(P / prefill_s, 1),
         "prefill_tflops": round(wl.prefill_flops(P) / prefill_s / 1e12, 1),
+        "first_prefill_ms": round(first_prefill_s * 1e3, 2),
     }
 
 
