@@ -248,6 +248,52 @@ __device__ __forceinline__ float epi4_finish(const GemmArgs &a, int mb, int n, c
     return 0.0f;
 }
 
+// The inputs of a one-pass, one-batch epilogue (FI = 4, FJ = 1, NB = 4: the
+// split-K kernel) that do not depend on the tile's values: the tokens' norm
+// partials (consumer side of the hand-off), the rows' scales and next norm
+// weights, the residual rows or RoPE tables.  The split-K kernel loads them
+// before its partial exchange, so that they arrive during the exchange's
+// round trips instead of after them.
+template <int EPI, int NB>
+struct EpiPre {
+    f32x4 nss[kMaxNormGroups / 4];
+    f32x4 sc, nrw;
+    Epi4Tok tk[NB];
+};
+
+template <int EPI, int NB>
+__device__ __forceinline__ void epi_prefetch(const GemmArgs &a, int mw, int nw, EpiPre<EPI, NB> &p) {
+    const int lane = threadIdx.x & 63, r = lane & 15, nsub = lane >> 4;
+    if (a.nss_in) {
+        const int n = min(nw + r, a.N - 1);
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(a.nss_in + (size_t)n * a.ngroups);
+#pragma unroll
+        for (int i = 0; i < kMaxNormGroups / 4; i++)
+            if (4 * i < a.ngroups) p.nss[i] = src[i];
+    }
+    const int mb = mw + r * 4;
+    const bool rows_vec = mb + 3 < a.M && !(a.M & 3) && !(EPI == GEPI_QKV && (a.hd & 3));
+    p.sc = f32x4{1.f, 1.f, 1.f, 1.f};
+    p.nrw = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (rows_vec && a.wscale) p.sc = *reinterpret_cast<const f32x4 *>(a.wscale + mb);
+    if constexpr (EPI == GEPI_RESID)
+        if (rows_vec && a.nrm_w) p.nrw = *reinterpret_cast<const f32x4 *>(a.nrm_w + mb);
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const int nl = b * 4 + nsub;
+        if (rows_vec && nw + nl < a.N) epi4_load<EPI>(a, mb, nw + nl, p.tk[b]);
+    }
+}
+
+// 1 / rms of a token from its norm partials, added in group order
+__device__ __forceinline__ float nss_inv_rms(const GemmArgs &a, const f32x4 (&p)[kMaxNormGroups / 4]) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxNormGroups / 4; i++)
+        if (4 * i < a.ngroups) ss = ((ss + p[i][0]) + p[i][1]) + (p[i][2] + p[i][3]);
+    return 1.0f / sqrtf(ss / (float)a.K + a.nrm_eps);
+}
+
 // The output of one wavefront's FI x FJ MFMA fragments (fragment (i, j): rows
 // mw + 16 i + 4 (lane >> 4) .. +3 of token nw + 16 j + (lane & 15)) through
 // the wavefront's own LDS region `buf` (FJ 16 token rows of 64 floats), 64
@@ -264,13 +310,14 @@ __device__ __forceinline__ float epi4_finish(const GemmArgs &a, int mb, int n, c
 // overlap other workgroups' main loops, measured faster with NB = 1.
 constexpr int kStagePitch = 64;  // floats per staged token row
 
-template <int EPI, int FI, int FJ, int NB>
+template <int EPI, int FI, int FJ, int NB, bool PRE = false>
 __device__ __forceinline__ void stage_epilogue(const GemmArgs &a, float *buf, int mw, int nw,
-                                               const f32x4 (&acc)[FI][FJ]) {
+                                               const f32x4 (&acc)[FI][FJ], const EpiPre<EPI, NB> *pre = nullptr) {
     static_assert(FI % 4 == 0, "64-row passes");
     static_assert(FJ * 16 <= 64, "one token per lane for the norm scales");
     constexpr int NR = FJ * 4;  // token rows per lane per pass
     static_assert(NR % NB == 0, "whole batches");
+    static_assert(!PRE || (FI == 4 && FJ == 1 && NR == NB), "prefetched inputs cover one pass of one batch");
     const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
     const int nsub = lane >> 4;
     // norm hand-off, consumer side: lane l holds the scale of token
@@ -278,17 +325,17 @@ __device__ __forceinline__ void stage_epilogue(const GemmArgs &a, float *buf, in
     // them are loaded at once (one memory round trip), then added in order
     float inv_l = 1.0f;
     if (a.nss_in) {
-        const int n = min(nw + (lane & (FJ * 16 - 1)), a.N - 1);
-        const f32x4 *src = reinterpret_cast<const f32x4 *>(a.nss_in + (size_t)n * a.ngroups);
-        f32x4 p[kMaxNormGroups / 4];
+        if constexpr (PRE) {
+            inv_l = nss_inv_rms(a, pre->nss);
+        } else {
+            const int n = min(nw + (lane & (FJ * 16 - 1)), a.N - 1);
+            const f32x4 *src = reinterpret_cast<const f32x4 *>(a.nss_in + (size_t)n * a.ngroups);
+            f32x4 p[kMaxNormGroups / 4];
 #pragma unroll
-        for (int i = 0; i < kMaxNormGroups / 4; i++)
-            if (4 * i < a.ngroups) p[i] = src[i];
-        float ss = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kMaxNormGroups / 4; i++)
-            if (4 * i < a.ngroups) ss = ((ss + p[i][0]) + p[i][1]) + (p[i][2] + p[i][3]);
-        inv_l = 1.0f / sqrtf(ss / (float)a.K + a.nrm_eps);
+            for (int i = 0; i < kMaxNormGroups / 4; i++)
+                if (4 * i < a.ngroups) p[i] = src[i];
+            inv_l = nss_inv_rms(a, p);
+        }
     }
 #pragma unroll
     for (int h = 0; h < FI / 4; h++) {
@@ -302,9 +349,14 @@ __device__ __forceinline__ void stage_epilogue(const GemmArgs &a, float *buf, in
         const bool rows_vec = mb + 3 < a.M && !(a.M & 3) && !(EPI == GEPI_QKV && (a.hd & 3));
         // per-row inputs, the same for every token of the pass
         f32x4 sc = {1.f, 1.f, 1.f, 1.f}, nrw = {0.f, 0.f, 0.f, 0.f};
-        if (rows_vec && a.wscale) sc = *reinterpret_cast<const f32x4 *>(a.wscale + mb);
-        if constexpr (EPI == GEPI_RESID)
-            if (rows_vec && a.nrm_w) nrw = *reinterpret_cast<const f32x4 *>(a.nrm_w + mb);
+        if constexpr (PRE) {
+            sc = pre->sc;
+            nrw = pre->nrw;
+        } else {
+            if (rows_vec && a.wscale) sc = *reinterpret_cast<const f32x4 *>(a.wscale + mb);
+            if constexpr (EPI == GEPI_RESID)
+                if (rows_vec && a.nrm_w) nrw = *reinterpret_cast<const f32x4 *>(a.nrm_w + mb);
+        }
 #pragma unroll
         for (int r0 = 0; r0 < NR; r0 += NB) {
             f32x4 v[NB];
@@ -318,7 +370,10 @@ __device__ __forceinline__ void stage_epilogue(const GemmArgs &a, float *buf, in
 #pragma unroll
                     for (int i = 0; i < 4; i++) v[b][i] = v[b][i] * inv;
                 }
-                if (rows_vec && nw + nl < a.N) epi4_load<EPI>(a, mb, nw + nl, tk[b]);
+                if constexpr (PRE)
+                    tk[b] = pre->tk[b];
+                else if (rows_vec && nw + nl < a.N)
+                    epi4_load<EPI>(a, mb, nw + nl, tk[b]);
             }
 #pragma unroll
             for (int b = 0; b < NB; b++) {
@@ -756,6 +811,10 @@ __global__ __launch_bounds__(kBlock, 2) void gemm_skinny_kernel(const GemmArgs a
     }
     // the ring is free for the output staging once every wave is past its reads
     __builtin_amdgcn_s_barrier();
+    // the epilogue's other inputs are loaded now (by every wave: the last to
+    // arrive is not known yet), so they arrive during the exchange
+    EpiPre<EPI, 4> pre;
+    epi_prefetch<EPI, 4>(a, m0, n0 + wave * 16, pre);
     if (nsplit > 1) {
         // wave w's quarter of the tile (its 16 tokens) is reduced by the last
         // of the tile's nsplit waves w to arrive.  Partials move through
@@ -796,7 +855,8 @@ __global__ __launch_bounds__(kBlock, 2) void gemm_skinny_kernel(const GemmArgs a
         if (lane == 0) __hip_atomic_store(&a.cnt[slot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     const f32x4 out[4][1] = {{acc[0]}, {acc[1]}, {acc[2]}, {acc[3]}};
-    stage_epilogue<EPI, 4, 1, 4>(a, reinterpret_cast<float *>(smem) + wave * 16 * kStagePitch, m0, n0 + wave * 16, out);
+    stage_epilogue<EPI, 4, 1, 4, true>(a, reinterpret_cast<float *>(smem) + wave * 16 * kStagePitch, m0, n0 + wave * 16,
+                                       out, &pre);
 }
 
 hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
