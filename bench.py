@@ -370,6 +370,9 @@ def main():
     ap.add_argument("--top-k", type=int, default=None)
     ap.add_argument("--top-p", type=float, default=None)
     ap.add_argument("--repetition-penalty", type=float, default=None)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only copy MIB MiB device to device (hipMemcpy; ROCclr's copyBuffer kernel), twice: "
+                         "the known-size dispatch that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--model-dir", default=os.environ.get("TMG_MODEL_DIR",
                                                            os.path.join(tempfile.gettempdir(), "tmg_models")))
     args = ap.parse_args()
@@ -377,6 +380,19 @@ def main():
         print(f"bench.py measures one GPU only: this build runs the decode path on a single MI355X "
               f"(--gpus {args.gpus} requested)", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_calibration > 0:
+        from tinyminigo_amd import hip as H
+        nbytes = args.copy_calibration << 20
+        src, dst = H.DeviceBuffer(nbytes), H.DeviceBuffer(nbytes)
+        src.fill_byte(1)
+        for _ in range(2):
+            H.copy_device(dst, src, nbytes)
+        H.synchronize()
+        src.close()
+        dst.close()
+        log(f"copied {args.copy_calibration} MiB device to device twice ({nbytes} B read and written per copy)")
+        return None
 
     import numpy as np
 
