@@ -263,7 +263,11 @@ __device__ __forceinline__ void gemv_dot(const GemvArgs &a, const WeightRegs<KC,
         float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
         for (int c = 0; c < KC; c++) {
-            const u32x4 u = (c * kChunk + t * 8 < a.in) ? W.w[r][c] : u32x4{0u, 0u, 0u, 0u};
+            // the clamped loads of a partial last chunk are zeroed (a
+            // duplicated Inf or NaN weight would survive a zero activation);
+            // the test is uniform, so full chunks keep their registers
+            u32x4 u = W.w[r][c];
+            if ((c + 1) * kChunk > a.in && c * kChunk + t * 8 >= a.in) u = u32x4{0u, 0u, 0u, 0u};
             s0 = fmaf(xv[c][0], bf16_lo(u.x), s0);
             s1 = fmaf(xv[c][1], bf16_hi(u.x), s1);
             s0 = fmaf(xv[c][2], bf16_lo(u.y), s0);
