@@ -12,8 +12,8 @@
 // team keeps its own online-softmax state (running max, sum, output) over the
 // positions it visits, so the chunk loop has no block-wide synchronization;
 // K and V of a 64-position chunk are loaded together and the next chunk is
-// prefetched while the current one is computed.  Teams are merged in LDS at
-// the end.  PREFETCH = false drops the next-chunk double buffer (for the
+// prefetched while the current one is computed.  At the end the teams of a
+// wavefront are merged across lanes, then the wavefronts in LDS.  PREFETCH = false drops the next-chunk double buffer (for the
 // register budget of the persistent kernel).
 #pragma once
 
@@ -37,12 +37,14 @@ struct AttnGeom {
     static constexpr int CH = NTEAM * J;
 };
 
+// One merged (o, max, sum) state per wavefront: the teams of a wavefront are
+// merged across lanes before the wavefronts are merged through LDS.
 template <int HD, int GROUP, int NT = kBlock>
 struct AttnShared {
-    static constexpr int NTEAM = AttnGeom<HD, GROUP, NT>::NTEAM;
-    float o[NTEAM][GROUP][HD];
-    float m[NTEAM][GROUP];
-    float l[NTEAM][GROUP];
+    static constexpr int NWAVE = NT / 64;
+    float o[NWAVE][GROUP][HD];
+    float m[NWAVE][GROUP];
+    float l[NWAVE][GROUP];
 };
 
 // Split count of a decode attention row at context n_ctx: the same formula in
@@ -64,6 +66,28 @@ __device__ __forceinline__ int active_splits(int n_ctx, int nsplit) {
 // capacity a.cap), so the K/V loads do not wait for it; qpos and active are
 // then computed here and the arguments ignored.  Splits found inactive
 // return at once.
+// x combined with its copies in the lanes OFF, 2 OFF, ... < 64 apart (the
+// teams of a wavefront): the 16- and 32-lane exchanges are permlane swaps
+// (VALU), the others LDS-crossbar shuffles.
+template <int OFF, bool MAX>
+__device__ __forceinline__ float team_reduce(float x) {
+#pragma unroll
+    for (int off = OFF; off < 64; off <<= 1) {
+        float y;
+        if (off == 16 || off == 32) {
+            const auto r = off == 32 ? __builtin_amdgcn_permlane32_swap(as_u32(x), as_u32(x), false, false)
+                                     : __builtin_amdgcn_permlane16_swap(as_u32(x), as_u32(x), false, false);
+            // r[0] and r[1] hold x and its partner in one order or the other
+            x = from_u32<float>(r[0]);
+            y = from_u32<float>(r[1]);
+        } else {
+            y = __shfl_xor(x, off, 64);
+        }
+        x = MAX ? fmaxf(x, y) : x + y;
+    }
+    return x;
+}
+
 template <int HD, int GROUP, bool COH, bool PREFETCH = true, bool SPEC = false, int NT = kBlock>
 __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, int ti, int qpos, int active,
                                           AttnShared<HD, GROUP, NT> &sm) {
@@ -206,14 +230,25 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
         }
     }
 
-    // merge the NTEAM team states
+    // merge the team states: the 64 / TS teams of a wavefront (lanes TS
+    // apart) by cross-lane max and sums, then the wavefronts through LDS
+    constexpr int NWAVE = NT / 64;
+    const int wave = t >> 6, lane = t & 63;
 #pragma unroll
     for (int h = 0; h < GROUP; h++) {
+        const float M = team_reduce<TS, true>(m_run[h]);
+        const float w = (m_run[h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m_run[h] - M);
+        const float l = team_reduce<TS, false>(l_run[h] * w);
 #pragma unroll
-        for (int v = 0; v < VPL; v++) *reinterpret_cast<float4 *>(&sm.o[team][h][(v * TS + lt) * 4]) = o_acc[h][v];
-        if (lt == 0) {
-            sm.m[team][h] = m_run[h];
-            sm.l[team][h] = l_run[h];
+        for (int v = 0; v < VPL; v++) {
+            const float4 o = make_float4(
+                team_reduce<TS, false>(o_acc[h][v].x * w), team_reduce<TS, false>(o_acc[h][v].y * w),
+                team_reduce<TS, false>(o_acc[h][v].z * w), team_reduce<TS, false>(o_acc[h][v].w * w));
+            if (lane < TS) *reinterpret_cast<float4 *>(&sm.o[wave][h][(v * TS + lt) * 4]) = o;
+        }
+        if (lane == 0) {
+            sm.m[wave][h] = M;
+            sm.l[wave][h] = l;
         }
     }
     __syncthreads();
@@ -223,11 +258,11 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
     for (int idx = t; idx < GROUP * HD; idx += NT) {
         const int h = idx / HD, d = idx % HD;
         float M = -INFINITY;
-#pragma unroll 8
-        for (int tm = 0; tm < NTEAM; tm++) M = fmaxf(M, sm.m[tm][h]);
+#pragma unroll
+        for (int tm = 0; tm < NWAVE; tm++) M = fmaxf(M, sm.m[tm][h]);
         float L = 0.0f, O = 0.0f;
-#pragma unroll 8
-        for (int tm = 0; tm < NTEAM; tm++) {
+#pragma unroll
+        for (int tm = 0; tm < NWAVE; tm++) {
             const float mt = sm.m[tm][h];
             const float w = (mt == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mt - M);
             L = fmaf(sm.l[tm][h], w, L);
