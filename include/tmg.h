@@ -3,7 +3,7 @@
  *
  * This is the drop-in boundary for the reference crate's public model API
  * (reference src/lib.rs:1-6).  A Rust `extern "C"` block can bind every
- * entry point one-to-one; INTEGRATION.md shows that binding.
+ * entry point one-to-one, with the structs below mirrored as #[repr(C)].
  *
  * Conventions
  *  - Every function returns an int status (TMG_OK == 0, negative = error
