@@ -377,7 +377,7 @@ def main():
                                                            os.path.join(tempfile.gettempdir(), "tmg_models")))
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only: this build runs the decode path on a single MI355X "
+        print(f"bench.py measures one GPU only: the decode path runs on a single MI355X "
               f"(--gpus {args.gpus} requested)", file=sys.stderr)
         sys.exit(2)
 
