@@ -67,6 +67,29 @@ def test_gemv_bf16_vs_oracle(T, O, out, inp):
     assert np.abs(got - want).max() <= 1e-4
 
 
+@pytest.mark.parametrize("inp", [136, 2056])
+def test_gemv_partial_chunk_inf_weight(T, O, inp):
+    """A row's last weight is +Inf and the activation there is 1: the dot is
+    +Inf, as matmul_w gives.  In a partial last chunk the lanes past the row
+    end load a clamped copy of the row's last 16 bytes; they must add nothing
+    (an unmasked copy would add Inf * 0 = NaN)."""
+    from tinyminigo_amd.hip import DeviceBuffer, synchronize
+    out = 16
+    w = T.synth_normal_bf16(2, f"winf{inp}", out * inp, 0.02).reshape(out, inp).copy()
+    w[:, inp - 1] = 0x7F80  # +Inf in BF16
+    x = T.synth_normal_f32(2, f"xinf{inp}", inp, 1.0).copy()
+    x[inp - 1] = 1.0
+    want = O.matmul_w(x, w.reshape(-1), out, inp)
+    assert np.all(np.isposinf(want))
+    wd, xd = DeviceBuffer.from_array(w.reshape(-1)), DeviceBuffer.from_array(x)
+    yd = DeviceBuffer(out * 4)
+    yd.fill_byte(0)
+    T.gemv_bf16(wd.addr, xd.addr, yd.addr, out, inp)
+    synchronize()
+    got = yd.to_array(np.float32, out)
+    assert np.all(np.isposinf(got)), got
+
+
 def test_gemv_small_golden(T):
     from tinyminigo_amd.hip import DeviceBuffer, synchronize
     z = np.load(os.path.join(GOLD, "gemv_small.npz"))
