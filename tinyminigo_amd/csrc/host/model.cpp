@@ -344,9 +344,9 @@ bool LaunchRecorder::want(const char *name, double b) {
 
 // The split-K merge runs in the o_proj GEMV prologue when the splits are few
 // (at most 8) and the attention output is at most 4096 wide: every o_proj
-// workgroup re-reads the active partials, which for the 4B shape (4096-wide
-// output, 2560 rows) makes o_proj 3.0 us slower but saves the 2.7 us merge
-// kernel and its launch (501 -> 507 tok/s sampled).
+// workgroup re-reads the partials, which for the 4B shape (4096-wide output,
+// 2560 rows, 16 rows per workgroup) makes o_proj 1.7 us slower but saves the
+// 2.7 us merge kernel and its launch (sampled 4B 501 -> 518 tok/s).
 static bool fused_merge(const tmg_model *m, const tmg_cache *c) {
     return c->attn_nsplit > 1 && c->attn_nsplit <= kFusedSplits && m->qd <= 4096;
 }
