@@ -740,10 +740,19 @@ constexpr int kSkTile = 64 * 128;  // bytes of one 64 x 64 bf16 tile
 constexpr int kSkOps = 6;          // DMA instructions per wave per step
 constexpr int kSkMaxSplit = 8;
 
-template <int EPI>
-__global__ __launch_bounds__(kBlock, 2) void gemm_skinny_kernel(const GemmArgs a, int nsplit, int n_tiles) {
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[kSkStages * 3 * kSkTile];
+// PAIR: eight wavefronts, waves 4-7 taking the odd K steps (their partials
+// added to waves 0-3's through LDS), with a ring of step pairs (144 KB, one
+// workgroup per CU).  Used where the grid is at most one workgroup per CU
+// and K is not split (the gate/up shape at 64 tokens: 18.2 -> 17.1 us):
+// two wavefronts per SIMD then hide each other's LDS and barrier waits.
+template <int EPI, bool PAIR>
+__global__ __launch_bounds__(PAIR ? 2 * kBlock : kBlock, PAIR ? 1 : 2) void gemm_skinny_kernel(const GemmArgs a,
+                                                                                                  int nsplit,
+                                                                                                  int n_tiles) {
+    constexpr int NPAR = PAIR ? 2 : 1;  // K steps per ring stage
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[kSkStages * NPAR * 3 * kSkTile];
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int wq = wave & 3, par = PAIR ? wave >> 2 : 0;  // token quarter, step parity
     const int r = lane & 15, q = lane >> 4;
     const int m_tiles = (a.M + 63) >> 6;
     const int rest = blockIdx.x >> 3;
@@ -754,43 +763,52 @@ __global__ __launch_bounds__(kBlock, 2) void gemm_skinny_kernel(const GemmArgs a
     const int K = a.K, nk = K >> 6;
     const int s0 = ks * nk / nsplit, ns = (ks + 1) * nk / nsplit - s0;
     const int m0 = mt * 64, n0 = nt * 64;
-    // DMA: wave w fills row groups 2w, 2w+1 (8 rows of 128 B) of each tile;
-    // lane l writes physical chunk l & 7 of row (l >> 3), i.e. logical chunk
-    // (l & 7) ^ (row & 7)
+    // DMA: wave w fills row groups 2 wq, 2 wq + 1 (8 rows of 128 B) of each
+    // tile of its steps; lane l writes physical chunk l & 7 of row (l >> 3),
+    // i.e. logical chunk (l & 7) ^ (row & 7)
     const uint16_t *src[3][2];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-        const int row = (2 * wave + i) * 8 + (lane >> 3);
+        const int row = (2 * wq + i) * 8 + (lane >> 3);
         const int lc = (lane & 7) ^ (row & 7);
         const size_t kofs = (size_t)s0 * 64 + lc * 8;
         src[0][i] = a.W + (size_t)min(m0 + row, a.M - 1) * K + kofs;
         src[1][i] = a.Bhi + (size_t)min(n0 + row, a.N - 1) * K + kofs;
         src[2][i] = a.Blo + (size_t)min(n0 + row, a.N - 1) * K + kofs;
     }
-    auto issue = [&](int j) {
-        unsigned char *dst = smem + (j % kSkStages) * 3 * kSkTile;
+    // stage p % kSkStages holds steps NPAR p .. NPAR p + NPAR - 1; this wave
+    // loads and multiplies step NPAR p + par
+    auto has = [&](int p) { return NPAR * p + par < ns; };
+    auto stage = [&](int p) { return smem + ((p % kSkStages) * NPAR + par) * 3 * kSkTile; };
+    auto issue = [&](int p) {
+        const int j = NPAR * p + par;
+        unsigned char *dst = stage(p);
 #pragma unroll
         for (int x = 0; x < 3; x++)
 #pragma unroll
             for (int i = 0; i < 2; i++)
-                __builtin_amdgcn_global_load_lds(src[x][i] + j * 64, dst + x * kSkTile + (2 * wave + i) * 1024, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(src[x][i] + j * 64, dst + x * kSkTile + (2 * wq + i) * 1024, 16, 0, 0);
     };
-    for (int j = 0; j < kSkStages - 1 && j < ns; j++) issue(j);
+    static_assert(kSkStages == 3, "wait counts assume one stage in flight behind the current one");
+    const int np = (ns + NPAR - 1) / NPAR;
+    if (has(0)) issue(0);
+    if (has(1)) issue(1);
     f32x4 acc[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int rb = wave * 16 + r;
-    for (int j = 0; j < ns; j++) {
-        // step j's DMAs are complete once at most the next step's are
-        // outstanding (vector memory completes in issue order)
-        static_assert(kSkStages == 3, "wait counts assume one step in flight behind the current one");
-        if (j + 1 < ns)
+    const int rb = wq * 16 + r;
+    for (int p = 0; p < np; p++) {
+        // stage p's DMAs of this wave are complete once at most stage p + 1's
+        // are outstanding (only DMAs are outstanding: they complete in issue
+        // order)
+        if (has(p + 1))
             __builtin_amdgcn_s_waitcnt(0x0F70 | kSkOps);  // vmcnt(kSkOps)
         else
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-        __builtin_amdgcn_s_barrier();  // every wave's DMAs of step j landed; step j-1's reads are done
-        if (j + kSkStages - 1 < ns) issue(j + kSkStages - 1);
-        const unsigned char *sa = smem + (j % kSkStages) * 3 * kSkTile;
+        __builtin_amdgcn_s_barrier();  // every wave's DMAs of stage p landed; stage p-1's reads are done
+        if (has(p + 2)) issue(p + 2);
+        if (!has(p)) continue;
+        const unsigned char *sa = stage(p);
         const unsigned char *sh = sa + kSkTile, *sl = sa + 2 * kSkTile;
 #pragma unroll
         for (int kk = 0; kk < 2; kk++) {
@@ -811,10 +829,29 @@ __global__ __launch_bounds__(kBlock, 2) void gemm_skinny_kernel(const GemmArgs a
     }
     // the ring is free for the output staging once every wave is past its reads
     __builtin_amdgcn_s_barrier();
+    if constexpr (PAIR) {
+        // the odd steps' partials to the even-step waves of the same tokens,
+        // through the LDS region that is the receiving wave's own staging
+        // buffer below (its LDS accesses complete in order)
+        f32x4 *hand =reinterpret_cast<f32x4 *>(smem) + (wq * 64 + lane) * 4;
+        if (par) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) hand[i] = acc[i];
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        if (par) return;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const f32x4 o = hand[i];
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[i][e] += o[e];
+        }
+    }
     // the epilogue's other inputs are loaded now (by every wave: the last to
     // arrive is not known yet), so they arrive during the exchange
     EpiPre<EPI, 4> pre;
-    epi_prefetch<EPI, 4>(a, m0, n0 + wave * 16, pre);
+    epi_prefetch<EPI, 4>(a, m0, n0 + wq * 16, pre);
     if (nsplit > 1) {
         // wave w's quarter of the tile (its 16 tokens) is reduced by the last
         // of the tile's nsplit waves w to arrive.  Partials move through
@@ -822,7 +859,7 @@ __global__ __launch_bounds__(kBlock, 2) void gemm_skinny_kernel(const GemmArgs a
         // and each wave's stores are complete before its counter increment,
         // so no cache write-back or invalidation is needed; a per-wave
         // counter needs no workgroup barrier.
-        const int slot = (nt * m_tiles + mt) * 4 + wave;
+        const int slot = (nt * m_tiles + mt) * 4 + wq;
         float *part = a.part + ((size_t)slot * nsplit + ks) * 1024 + lane;
 #pragma unroll
         for (int i = 0; i < 4; i++)
@@ -855,7 +892,7 @@ __global__ __launch_bounds__(kBlock, 2) void gemm_skinny_kernel(const GemmArgs a
         if (lane == 0) __hip_atomic_store(&a.cnt[slot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     const f32x4 out[4][1] = {{acc[0]}, {acc[1]}, {acc[2]}, {acc[3]}};
-    stage_epilogue<EPI, 4, 1, 4, true>(a, reinterpret_cast<float *>(smem) + wave * 16 * kStagePitch, m0, n0 + wave * 16,
+    stage_epilogue<EPI, 4, 1, 4, true>(a, reinterpret_cast<float *>(smem) + wq * 16 * kStagePitch, m0, n0 + wq * 16,
                                        out, &pre);
 }
 
@@ -877,11 +914,23 @@ hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
     }
     if (nsplit > 1 && (size_t)m_tiles * n_tiles * nsplit * 4096 > kSkinnyPartFloats) return hipErrorInvalidValue;
     const dim3 grid((m_tiles * nsplit + 7) / 8 * n_tiles * 8);
+    // eight wavefronts per workgroup (step pairs) where K is not split and the
+    // grid is at most one workgroup per CU
+    if (nsplit == 1 && m_tiles * n_tiles <= 256) {
+        switch (epi) {
+            case GEPI_STORE: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_STORE, true>), grid, dim3(2 * kBlock), 0, s, a, nsplit, n_tiles); break;
+            case GEPI_RESID: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_RESID, true>), grid, dim3(2 * kBlock), 0, s, a, nsplit, n_tiles); break;
+            case GEPI_SWIGLU: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_SWIGLU, true>), grid, dim3(2 * kBlock), 0, s, a, nsplit, n_tiles); break;
+            case GEPI_QKV: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_QKV, true>), grid, dim3(2 * kBlock), 0, s, a, nsplit, n_tiles); break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     switch (epi) {
-        case GEPI_STORE: hipLaunchKernelGGL(gemm_skinny_kernel<GEPI_STORE>, grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
-        case GEPI_RESID: hipLaunchKernelGGL(gemm_skinny_kernel<GEPI_RESID>, grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
-        case GEPI_SWIGLU: hipLaunchKernelGGL(gemm_skinny_kernel<GEPI_SWIGLU>, grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
-        case GEPI_QKV: hipLaunchKernelGGL(gemm_skinny_kernel<GEPI_QKV>, grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
+        case GEPI_STORE: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_STORE, false>), grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
+        case GEPI_RESID: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_RESID, false>), grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
+        case GEPI_SWIGLU: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_SWIGLU, false>), grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
+        case GEPI_QKV: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_QKV, false>), grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
