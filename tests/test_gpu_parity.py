@@ -501,6 +501,27 @@ def test_prefill_k_not_multiple_of_64(T, O, W):
             close_logits(g.forward_token(ids[i], gc), o.forward_token(ids[i], oc), f"decode at {i}")
 
 
+def test_short_prompt_odd_k_steps_vs_oracle(T, O, W):
+    # hidden 192: QKV, o_proj and gate/up have three 64-wide K steps and a grid
+    # of at most 10 tiles, so they run unsplit as eight waves over step pairs,
+    # the odd-step waves idle in the last pair; down (K = 320, five steps)
+    # splits 2 + 3 steps.  Prompts of 40 and 64 tokens, then decode steps.
+    import dataclasses
+    wl = dataclasses.replace(W.TINY, name="tiny-llama-h192-kv6-i320-s17", hidden_size=192, num_attention_heads=12,
+                             num_key_value_heads=6, intermediate_size=320, weight_seed=17)
+    p = W.ensure_model(wl, model_root())
+    g, o = T.Model.load(p), O.OracleModel.load(p)
+    ids = [int(t) for t in T.synth_tokens(67, 72, wl.vocab_size)]
+    for n in (40, 64):
+        gc, oc = T.KvCache(g, 80), o.new_cache()
+        close_logits(g.forward_seq(ids[:n], gc), o.forward_seq(ids[:n], oc), f"prefill {n}")
+        for layer in range(wl.num_hidden_layers):
+            assert np.abs(gc.keys_flat(layer) - oc.keys_flat(layer)).max() < 1e-4
+            assert np.abs(gc.values_flat(layer) - oc.values_flat(layer)).max() < 1e-4
+        for i in range(n, n + 4):
+            close_logits(g.forward_token(ids[i], gc), o.forward_token(ids[i], oc), f"decode at {i}")
+
+
 def test_long_prefill_chunks_vs_oracle(T, O, W, one_b):
     # 1B model: a 700-token prefill, a second 333-token chunk starting at 700
     # (MFMA attention with start > 0, partial query blocks), then decode steps
