@@ -110,7 +110,8 @@ int tmg_tmb_config(const char *tmb_path, tmg_config *out);
  * caches are freed (Rust drops struct fields in declaration order): the
  * model's device memory and stream are then released by the last
  * tmg_cache_free.  After this call the model handle itself must not be used
- * again; its caches may still be read, reset and freed. */
+ * again; its caches may still be read, reset and freed.  The model and its
+ * caches may be freed from different threads. */
 void tmg_model_free(tmg_model *model);
 int tmg_model_config(const tmg_model *model, tmg_config *out);
 

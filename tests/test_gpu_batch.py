@@ -77,6 +77,29 @@ def test_batch_of_more_than_eight_takes_the_gemm_path(T, O, untied):
     assert lo + hi == got
 
 
+def test_batch_of_more_than_eight_with_norm_hand_off(T, O, W):
+    """More than 8 sequences on a model whose hidden size is a multiple of
+    256: the MFMA GEMM step hands the RMSNorm from the o_proj / down
+    epilogues to the next GEMM (the residual times the norm weight, then
+    1/rms on the consumer's dot products), a different rounding from
+    forward_token's.  Every sequence's ids must still be the oracle's
+    generate, and the library's single-sequence generate for a few."""
+    import dataclasses
+    wl = dataclasses.replace(W.TINY, name="tiny-llama-h256-q4-k2-d64-i512-s23", hidden_size=256,
+                             num_attention_heads=4, num_key_value_heads=2, head_dim=64, intermediate_size=512,
+                             tied_lm_head=False, weight_seed=23, rms_norm_eps=1e-5)
+    p = W.ensure_model(wl, model_root())
+    g, o = T.Model.load(p), O.OracleModel.load(p)
+    lens = [1, 4, 9, 16, 25, 36, 2, 3, 40, 7, 11]
+    prompts = [[int(t) for t in T.synth_tokens(140 + i, n, wl.vocab_size)] for i, n in enumerate(lens)]
+    print("batch hidden 256 x11", flush=True)
+    got, _ = T.generate_batch(g, prompts, 20)
+    for b, pr in enumerate(prompts):
+        assert got[b] == O.generate(o, pr, 20).tokens, f"sequence {b}"
+    for b in (0, 5, 10):
+        assert got[b] == T.generate(g, prompts[b], T.GenParams(max_tokens=20)).tokens, f"sequence {b} alone"
+
+
 def test_batch_tied_and_k_not_multiple_of_64(T, O, W, tiny_path):
     import dataclasses
     wl = dataclasses.replace(W.TINY, name="tiny-llama-h96-kv3-i160-s13", hidden_size=96, num_attention_heads=6,

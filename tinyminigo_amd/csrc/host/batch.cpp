@@ -186,8 +186,14 @@ int enqueue_batch_step(tmg_model *m, const Batch &bt) {
     for (int l = 0; l < m->L; l++) {
         const tmg_model::Layer &ly = m->layers[l];
         const size_t layer_off = (size_t)l * bt.max_pos * kvd;
-        // forward_token's RMSNorm association, (v*inv)*w (src/tensor.rs:975),
-        // when the norm is a separate pass
+        // Without the hand-off the norm is a separate pass with
+        // forward_token's association, (v*inv)*w (src/tensor.rs:975).  With
+        // it (more than kMtMaxSeq sequences, hidden a multiple of 256) the
+        // residual is multiplied by the norm weight in the producing
+        // epilogue and 1/rms is applied to the consumer's dot products, so
+        // the rounding differs from both of the reference's associations;
+        // the results stay within the logit tolerance and the greedy ids are
+        // the reference's (tests/test_gpu_batch.py, hidden 256 and 1B)
         const bool in_handed = hand_off && l > 0;
         if (!in_handed) TMG_HIPB(launch_rmsnorm_split(bt.x, ly.in_norm, eps, B, H, bt.hi, bt.lo, s, true));
         GemmArgs g{};

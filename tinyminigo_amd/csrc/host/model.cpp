@@ -804,9 +804,12 @@ extern "C" int tmg_model_load(const char *path, int device, tmg_model **out) {
 
 extern "C" void tmg_model_free(tmg_model *m) {
     if (!m) return;
-    if (m->live_caches > 0) {
-        m->free_requested = true;  // released by the last tmg_cache_free
-        return;
+    {
+        std::lock_guard<std::mutex> lk(m->life_mu);
+        if (m->live_caches > 0) {
+            m->free_requested = true;  // released by the last tmg_cache_free
+            return;
+        }
     }
     model_release(m);
 }
@@ -822,10 +825,13 @@ extern "C" int tmg_cache_new(tmg_model *m, uint32_t max_pos, tmg_cache **out) {
     if (!m || !out || max_pos == 0) return set_error(TMG_E_INVALID, "bad argument to tmg_cache_new");
     *out = nullptr;
     (void)hipSetDevice(m->device);
-    if (m->free_requested) return set_error(TMG_E_INVALID, "model handle already freed");
+    {
+        std::lock_guard<std::mutex> lk(m->life_mu);
+        if (m->free_requested) return set_error(TMG_E_INVALID, "model handle already freed");
+        m->live_caches++;
+    }
     tmg_cache *c = new tmg_cache();
     c->model = m;
-    m->live_caches++;
     c->max_pos = max_pos;
     c->attn_nsplit = (int)std::min<uint32_t>(kMaxSplits, (max_pos + kAttnBlock - 1) / kAttnBlock);
     const size_t n = (size_t)m->L * max_pos * m->kvd;
@@ -893,7 +899,12 @@ extern "C" void tmg_cache_free(tmg_cache *c) {
     (void)hipHostFree(c->history);
     tmg_model *m = c->model;
     delete c;
-    if (--m->live_caches == 0 && m->free_requested) model_release(m);
+    bool release;
+    {
+        std::lock_guard<std::mutex> lk(m->life_mu);
+        release = --m->live_caches == 0 && m->free_requested;
+    }
+    if (release) model_release(m);
 }
 
 extern "C" int tmg_cache_len(const tmg_cache *c, uint32_t layer, uint32_t *len) {

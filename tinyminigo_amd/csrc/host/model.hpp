@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <string>
+#include <mutex>
 #include <vector>
 
 #include "../kernels/kernels.hpp"
@@ -70,6 +71,9 @@ struct tmg_model {
     // Caches created on this model and not yet freed.  tmg_model_free with
     // live caches only marks the model; the last tmg_cache_free releases it
     // (a cache uses the model's stream, device and weights until it is freed).
+    // Both fields change under life_mu, so frees on different threads
+    // release the model exactly once.
+    std::mutex life_mu;
     int live_caches = 0;
     bool free_requested = false;
 };

@@ -1,23 +1,23 @@
-// GQA attention over the f32 KV cache as a device function shared by the
-// standalone attention kernel (decode.hip) and the persistent decode kernel.
+// GQA attention over the f32 KV cache as a device function of the decode
+// attention kernel (decode.hip), also used for the per-row prefill attention
+// of short prompts.
 //
 // Reference: decode attention src/model.rs:434-459, attention_batch
 // src/tensor.rs:1099-1139, softmax src/tensor.rs:1055-1060.
 //
 // One call handles one (query row, KV head, split) item: the split's
-// 64-position blocks of the row's context, for all GROUP query heads of the KV head, so
-// every K/V load serves GROUP heads.  TS = HD/(4 VPL) lanes own one position
-// (VPL float4s of K and of V each, interleaved so one load instruction covers
-// TS x 16 contiguous bytes); the 256 threads form NTEAM such teams.  Each
-// team keeps its own online-softmax state (running max, sum, output) over the
-// positions it visits, so the chunk loop has no block-wide synchronization;
-// K and V of a 64-position chunk are loaded together and the next chunk is
-// prefetched while the current one is computed.  At the end the teams of a
-// wavefront are merged across lanes, then the wavefronts in LDS.  PREFETCH = false drops the next-chunk double buffer (for the
-// register budget of the persistent kernel).
+// 64-position blocks of the row's context, for all GROUP query heads of the
+// KV head, so every K/V load serves GROUP heads.  TS = HD/(4 VPL) lanes own
+// one position (VPL float4s of K and of V each, interleaved so one load
+// instruction covers TS x 16 contiguous bytes); the NT threads form NTEAM
+// such teams.  Each team keeps its own online-softmax state (running max,
+// sum, output) over the positions it visits, so the chunk loop has no
+// block-wide synchronization; K and V of a 64-position chunk are loaded
+// together and the next chunk is prefetched while the current one is
+// computed.  At the end the teams of a wavefront are merged across lanes,
+// then the wavefronts in LDS.
 #pragma once
 
-#include "coh.cuh"
 #include "common.cuh"
 #include "kernels.hpp"
 
@@ -88,7 +88,7 @@ __device__ __forceinline__ float team_reduce(float x) {
     return x;
 }
 
-template <int HD, int GROUP, bool COH, bool PREFETCH = true, bool SPEC = false, int NT = kBlock>
+template <int HD, int GROUP, bool SPEC = false, int NT = kBlock>
 __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, int ti, int qpos, int active,
                                           AttnShared<HD, GROUP, NT> &sm) {
     using G = AttnGeom<HD, GROUP, NT>;
@@ -107,7 +107,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
 #pragma unroll
     for (int h = 0; h < GROUP; h++)
 #pragma unroll
-        for (int v = 0; v < VPL; v++) qv[h][v] = ldf4<COH>(qrow + (g * GROUP + h) * HD + (v * TS + lt) * 4);
+        for (int v = 0; v < VPL; v++) qv[h][v] = *reinterpret_cast<const float4 *>(qrow + (g * GROUP + h) * HD + (v * TS + lt) * 4);
 
     static_assert(CH == 64, "the split partition deals 64-position blocks");
     float4 kr[J][VPL], vr[J][VPL];
@@ -154,7 +154,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
     for (int c0 = c_first; c0 < n_ctx; c0 += c_step) {
         float4 kn[J][VPL], vn[J][VPL];
         const bool more = c0 + c_step < n_ctx;
-        if (PREFETCH && more) load_kv(kn, vn, c0 + c_step, last);
+        if (more) load_kv(kn, vn, c0 + c_step, last);
         // scores of this team's positions (every lane of the team gets them)
         float s[J][GROUP];
 #pragma unroll
@@ -215,18 +215,13 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
             for (int v = 0; v < VPL; v++) o_acc[h][v] = o[v];
         }
         if (more) {
-            if constexpr (PREFETCH) {
 #pragma unroll
-                for (int j = 0; j < J; j++)
+            for (int j = 0; j < J; j++)
 #pragma unroll
-                    for (int v = 0; v < VPL; v++) {
-                        kr[j][v] = kn[j][v];
-                        vr[j][v] = vn[j][v];
-                    }
-            } else {
-                // load the next chunk after this one is consumed (fewer registers)
-                load_kv(kr, vr, c0 + c_step, last);
-            }
+                for (int v = 0; v < VPL; v++) {
+                    kr[j][v] = kn[j][v];
+                    vr[j][v] = vn[j][v];
+                }
         }
     }
 
@@ -270,13 +265,13 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
         }
         if (direct) {
             const float o = O / L;
-            if (a.out_f32) stf<COH>(a.out_f32 + row_hd + idx, o);
+            if (a.out_f32) a.out_f32[row_hd + idx] = o;
             if (a.out_hi) split_bf16(o, a.out_hi + row_hd + idx, a.out_lo + row_hd + idx);
         } else {
-            stf<COH>(a.part + (pbase + h) * HD + d, O);
+            a.part[(pbase + h) * HD + d] = O;
             if (d == 0) {
-                stf<COH>(a.part_ml + (pbase + h) * 2 + 0, M);
-                stf<COH>(a.part_ml + (pbase + h) * 2 + 1, L);
+                a.part_ml[(pbase + h) * 2 + 0] = M;
+                a.part_ml[(pbase + h) * 2 + 1] = L;
             }
         }
     }

@@ -29,8 +29,8 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(const GemvArgs a) {
         // the gathered row depends on the token id: weights first
         gemv_load<KC, R>(a, blockIdx.x, W);
         const int pos = EPI == EPI_QKV ? *a.pos : 0;
-        gemv_prologue<KC, PRO, false>(a, *a.token, pos, xv, scratch, blockIdx.x == 0);
-        gemv_finish<KC, R, EPI, false>(a, blockIdx.x, pos, W, xv, red);
+        gemv_embed_prologue<KC>(a, *a.token, xv, scratch, blockIdx.x == 0);
+        gemv_finish<KC, R, EPI>(a, blockIdx.x, pos, W, xv, red);
     } else {
         // activation-side loads, then the weights (see gemv.cuh)
         ActIn<KC, PRO> in;
@@ -44,7 +44,7 @@ __global__ __launch_bounds__(kBlock) void gemv_kernel(const GemvArgs a) {
         const int pos = (EPI == EPI_QKV || PRO == PRO_ATTN_COMBINE) ? *a.pos : 0;
         if constexpr (EPI == EPI_QKV) epi_load_rope<R>(a, blockIdx.x, pos, pre);
         act_finish<KC, PRO>(a, pos, in, xv, scratch);
-        gemv_finish<KC, R, EPI, false, true>(a, blockIdx.x, pos, W, xv, red, pre);
+        gemv_finish<KC, R, EPI, true>(a, blockIdx.x, pos, W, xv, red, pre);
     }
 }
 
@@ -63,7 +63,7 @@ __global__ __launch_bounds__(kBlock) void gemv_i8_kernel(const GemvArgs a) {
         gemv_load8<KC, R>(a, blockIdx.x, W);
         epi_issue_scale<R, EPI>(a, blockIdx.x, pre);
         if constexpr (EPI == EPI_QKV) pos = *a.pos;
-        gemv_prologue<KC, PRO, false>(a, *a.token, pos, xv, scratch, blockIdx.x == 0);
+        gemv_embed_prologue<KC>(a, *a.token, xv, scratch, blockIdx.x == 0);
         if constexpr (EPI == EPI_QKV) epi_load_rope<R>(a, blockIdx.x, pos, pre);
     } else {
         ActIn<KC, PRO> in;
@@ -80,7 +80,7 @@ __global__ __launch_bounds__(kBlock) void gemv_i8_kernel(const GemvArgs a) {
     const float xs = quantize_act<KC>(xv, xq, scratch);
     gemv_dot8<KC, R>(W, xq, red);
     __syncthreads();
-    gemv_epilogue<R, EPI, false, true, true>(a, blockIdx.x, pos, red, pre, xs);
+    gemv_epilogue<R, EPI, true, true>(a, blockIdx.x, pos, red, pre, xs);
 }
 
 template <int KC, int PRO, int EPI>
@@ -238,14 +238,14 @@ __global__ __launch_bounds__(NT) void attn_kernel(const AttnArgs a) {
     const int split = blockIdx.x, g = blockIdx.y, ti = blockIdx.z;
     if constexpr (SPEC) {
         if (split < kSpecSplits) {
-            attn_item<HD, GROUP, false, true, true, NT>(a, split, g, ti, 0, 0, sm);
+            attn_item<HD, GROUP, true, NT>(a, split, g, ti, 0, 0, sm);
             return;
         }
     }
     const int qpos = a.pos_seq ? a.pos_seq[ti] : (a.pos_dev ? *a.pos_dev : a.start) + ti;
     const int active = active_splits(qpos + 1, a.nsplit);
     if (split >= active) return;
-    attn_item<HD, GROUP, false, true, false, NT>(a, split, g, ti, qpos, active, sm);
+    attn_item<HD, GROUP, false, NT>(a, split, g, ti, qpos, active, sm);
 }
 
 // Merge of the split-K partials of decode row 0, one workgroup per query

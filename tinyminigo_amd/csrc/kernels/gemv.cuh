@@ -1,5 +1,6 @@
-// The BF16 decode GEMV as device functions shared by the standalone kernels
-// (decode.hip) and the persistent decode kernel (persistent.hip).
+// The BF16 decode GEMV as device functions of the decode kernels
+// (decode.hip): weight loads, activation prologues, dots, the block
+// reduction and the fused epilogues.
 //
 // Reference: matmul_w_into (src/tensor.rs:331-460), hot loop dot_bf16_avx2
 // (src/tensor.rs:78-96).  A 256-thread workgroup owns R output rows ("a
@@ -9,13 +10,9 @@
 // prologue (they do not depend on it), the activation lives in registers, and
 // the per-row reduction is a transposed shuffle butterfly plus a 4-wave LDS
 // sum.
-//
-// COH selects device-coherent (sc1) accesses for activations, for use inside a
-// persistent kernel where other workgroups wrote them in the same launch.
 #pragma once
 
 #include "attn.cuh"
-#include "coh.cuh"
 #include "common.cuh"
 #include "kernels.hpp"
 
@@ -55,7 +52,7 @@ __device__ __forceinline__ void gemv_load(const GemvArgs &a, int blk, WeightRegs
     }
 }
 
-template <int KC, bool COH>
+template <int KC>
 __device__ __forceinline__ void load_act(const float *src, const uint16_t *src_bf, int in, float (&xv)[KC][8]) {
     const int t = threadIdx.x;
 #pragma unroll
@@ -73,8 +70,8 @@ __device__ __forceinline__ void load_act(const float *src, const uint16_t *src_b
                 xv[c][6] = bf16_lo(u.w);
                 xv[c][7] = bf16_hi(u.w);
             } else {
-                const float4 p = ldf4<COH>(src + k);
-                const float4 q = ldf4<COH>(src + k + 4);
+                const float4 p = *reinterpret_cast<const float4 *>(src + k);
+                const float4 q = *reinterpret_cast<const float4 *>(src + k + 4);
                 xv[c][0] = p.x;
                 xv[c][1] = p.y;
                 xv[c][2] = p.z;
@@ -88,45 +85,6 @@ __device__ __forceinline__ void load_act(const float *src, const uint16_t *src_b
 #pragma unroll
             for (int j = 0; j < 8; j++) xv[c][j] = 0.0f;
         }
-    }
-}
-
-// The attention output for this thread's 8 consecutive dims (one head),
-// merged from the active splits: o = sum_s e^(m_s-M) o_s / sum_s e^(m_s-M) l_s.
-template <int KC, bool COH>
-__device__ __forceinline__ void load_attn(const GemvArgs &a, int pos, float (&xv)[KC][8]) {
-    const int t = threadIdx.x;
-    const int active = active_splits(pos + 1, a.nsplit);
-#pragma unroll
-    for (int c = 0; c < KC; c++) {
-        const int k = c * kChunk + t * 8;
-#pragma unroll
-        for (int j = 0; j < 8; j++) xv[c][j] = 0.0f;
-        if (k >= a.in) continue;
-        const int h = k / a.hd, d = k - h * a.hd;
-        const int g = h / a.group, hq = h - g * a.group;
-        const size_t base = (size_t)g * a.nsplit * a.group + hq;  // + split * group
-        float M = -INFINITY;
-        for (int sp = 0; sp < active; sp++) M = fmaxf(M, ldf<COH>(a.part_ml + (base + (size_t)sp * a.group) * 2));
-        float L = 0.0f;
-        for (int sp = 0; sp < active; sp++) {
-            const size_t pi = base + (size_t)sp * a.group;
-            const float m = ldf<COH>(a.part_ml + pi * 2);
-            const float w = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - M);
-            L = fmaf(ldf<COH>(a.part_ml + pi * 2 + 1), w, L);
-            const float4 o0 = ldf4<COH>(a.part + pi * a.hd + d);
-            const float4 o1 = ldf4<COH>(a.part + pi * a.hd + d + 4);
-            xv[c][0] = fmaf(o0.x, w, xv[c][0]);
-            xv[c][1] = fmaf(o0.y, w, xv[c][1]);
-            xv[c][2] = fmaf(o0.z, w, xv[c][2]);
-            xv[c][3] = fmaf(o0.w, w, xv[c][3]);
-            xv[c][4] = fmaf(o1.x, w, xv[c][4]);
-            xv[c][5] = fmaf(o1.y, w, xv[c][5]);
-            xv[c][6] = fmaf(o1.z, w, xv[c][6]);
-            xv[c][7] = fmaf(o1.w, w, xv[c][7]);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j++) xv[c][j] = xv[c][j] / L;
     }
 }
 
@@ -182,40 +140,31 @@ __device__ __forceinline__ void rms_scale(const GemvArgs &a, float (&xv)[KC][8],
     }
 }
 
-// Activation prologue: gather / load, then RMSNorm when PRO asks for it
-// (reference rms_norm_into, src/tensor.rs:969-977; batch association
-// src/tensor.rs:946-954).  `scratch` holds 4 floats of LDS.  `tok` and `pos`
-// are the step's token and position (read once by the caller).
-template <int KC, int PRO, bool COH>
-__device__ __forceinline__ void gemv_prologue(const GemvArgs &a, int tok, int pos, float (&xv)[KC][8], float *scratch,
-                                              bool store_x) {
+// Prologue of the layer-0 QKV GEMV: the embedding row of token `tok`
+// (src/model.rs:401-403; BF16 rows widen exactly), stored as the residual
+// stream by one workgroup, then RMSNorm (rms_norm_into, src/tensor.rs:969-977).
+// `scratch` holds 4 floats of LDS.
+template <int KC>
+__device__ __forceinline__ void gemv_embed_prologue(const GemvArgs &a, int tok, float (&xv)[KC][8], float *scratch,
+                                                    bool store_x) {
     const int t = threadIdx.x;
     const int in = a.in;
-    if constexpr (PRO == PRO_ATTN_COMBINE) {
-        load_attn<KC, COH>(a, pos, xv);
-        return;
-    } else if constexpr (PRO == PRO_EMBED_NORM) {
-        if (a.embed_bf16)
-            load_act<KC, false>(nullptr, a.embed_bf16 + (size_t)tok * in, in, xv);
-        else
-            load_act<KC, false>(a.embed_f32 + (size_t)tok * in, nullptr, in, xv);
-        if (store_x) {
+    if (a.embed_bf16)
+        load_act<KC>(nullptr, a.embed_bf16 + (size_t)tok * in, in, xv);
+    else
+        load_act<KC>(a.embed_f32 + (size_t)tok * in, nullptr, in, xv);
+    if (store_x) {
 #pragma unroll
-            for (int c = 0; c < KC; c++) {
-                const int k = c * kChunk + t * 8;
-                if (k < in)
+        for (int c = 0; c < KC; c++) {
+            const int k = c * kChunk + t * 8;
+            if (k < in)
 #pragma unroll
-                    for (int j = 0; j < 8; j++) stf<COH>(a.x_store + k + j, xv[c][j]);
-            }
+                for (int j = 0; j < 8; j++) a.x_store[k + j] = xv[c][j];
         }
-    } else {
-        load_act<KC, COH>(a.x, nullptr, in, xv);
     }
-    if constexpr (PRO != PRO_PLAIN) {
-        float wv[KC][8];
-        load_norm_w<KC>(a, wv);
-        rms_scale<KC, PRO>(a, xv, wv, scratch);
-    }
+    float wv[KC][8];
+    load_norm_w<KC>(a, wv);
+    rms_scale<KC, PRO_NORM>(a, xv, wv, scratch);
 }
 
 // Epilogue inputs loaded ahead of the weights: the residual of row blk*R+t
@@ -288,7 +237,7 @@ __device__ __forceinline__ void gemv_dot(const GemvArgs &a, const WeightRegs<KC,
 // __syncthreads).  With PRE the residual / RoPE inputs come from `pre`
 // instead of memory; with Q8 the rows are int8 (row scales in pre.sc, xs the
 // activation scale).
-template <int R, int EPI, bool COH, bool PRE, bool Q8>
+template <int R, int EPI, bool PRE, bool Q8>
 __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int blk, int pos, float (*red)[R], const EpiIn &pre,
                                               float xs) {
     const int t = threadIdx.x;
@@ -300,7 +249,7 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int blk, int po
             const bool ok = row < a.out;
             if (ok) {
                 if constexpr (EPI == EPI_RESID)
-                    stf<COH>(a.y + row, (PRE ? pre.resid : ldf<COH>(a.y + row)) + v);
+                    a.y[row] = (PRE ? pre.resid : a.y[row]) + v;
                 else
                     a.y[row] = v;  // logits / plain output: read after the launch
             }
@@ -312,7 +261,7 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int blk, int po
                         const unsigned long long o = shfl_xor_u64(key, off);
                         key = o > key ? o : key;
                     }
-                    if (t == 0) stu64<COH>(a.argmax_part + blk, key);
+                    if (t == 0) a.argmax_part[blk] = key;
                 }
             }
         }
@@ -323,7 +272,7 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int blk, int po
             const float vb = row_value<R, Q8>(red, 2 * t + 1, xs, pre.sc[1]);
             if (2 * P + 1 < a.out) {
                 if constexpr (EPI == EPI_SWIGLU) {
-                    stf<COH>(a.y + P, swiglu(va, vb));
+                    a.y[P] = swiglu(va, vb);
                 } else {  // EPI_QKV: pair (j, j + hd/2) of head P / (hd/2)
                     const int half = a.hd >> 1;
                     const int head = P / half, j = P - head * half;
@@ -334,17 +283,17 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int blk, int po
                         const float rs = !PRE ? a.rope_sin[(size_t)pos * half + j] : R == 16 ? pre.rs[0] : pick4(pre.rs, t);
                         rope_pair(va, vb, rc, rs, &oa, &ob);
                         if (head < a.nq) {
-                            stf<COH>(a.q_out + head * a.hd + j, oa);
-                            stf<COH>(a.q_out + head * a.hd + j + half, ob);
+                            a.q_out[head * a.hd + j] = oa;
+                            a.q_out[head * a.hd + j + half] = ob;
                         } else {
                             float *kr = a.k_cache + (size_t)pos * kvd + (head - a.nq) * a.hd;
-                            stf<COH>(kr + j, oa);
-                            stf<COH>(kr + j + half, ob);
+                            kr[j] = oa;
+                            kr[j + half] = ob;
                         }
                     } else {
                         float *vr = a.v_cache + (size_t)pos * kvd + (head - a.nq - a.nkv) * a.hd;
-                        stf<COH>(vr + j, va);
-                        stf<COH>(vr + j + half, vb);
+                        vr[j] = va;
+                        vr[j + half] = vb;
                     }
                 }
             }
@@ -356,12 +305,12 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int blk, int po
 // `red` is LDS of 4*R floats.  Returns after the epilogue; the caller
 // separates consecutive calls with a __syncthreads (red is reused).  With
 // PRE the residual / RoPE inputs come from `pre` instead of memory.
-template <int KC, int R, int EPI, bool COH, bool PRE = false>
+template <int KC, int R, int EPI, bool PRE = false>
 __device__ __forceinline__ void gemv_finish(const GemvArgs &a, int blk, int pos, const WeightRegs<KC, R> &W,
                                             const float (&xv)[KC][8], float (*red)[R], const EpiIn &pre = EpiIn{}) {
     gemv_dot<KC, R>(a, W, xv, red);
     __syncthreads();
-    gemv_epilogue<R, EPI, COH, PRE, false>(a, blk, pos, red, pre, 0.0f);
+    gemv_epilogue<R, EPI, PRE, false>(a, blk, pos, red, pre, 0.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -536,12 +485,12 @@ __device__ __forceinline__ void act_issue(const GemvArgs &a, ActIn<KC, PRO> &in)
             }
         }
     } else {
-        load_act<KC, false>(a.x, nullptr, a.in, in.xv);
+        load_act<KC>(a.x, nullptr, a.in, in.xv);
         if constexpr (ActIn<KC, PRO>::kNorm) load_norm_w<KC>(a, in.wv);
     }
 }
 
-// Same arithmetic, in the same order, as gemv_prologue / load_attn.
+// The prologue's arithmetic: the split merge, or the copy of x and its RMSNorm.
 template <int KC, int PRO>
 __device__ __forceinline__ void act_finish(const GemvArgs &a, int pos, ActIn<KC, PRO> &in, float (&xv)[KC][8],
                                            float *scratch) {

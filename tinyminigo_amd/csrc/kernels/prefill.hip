@@ -864,7 +864,7 @@ __global__ __launch_bounds__(PAIR ? 2 * kBlock : kBlock, PAIR ? 1 : 2) void gemm
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) stf<true>(part + (i * 4 + e) * 64, acc[i][e]);
+            for (int e = 0; e < 4; e++) st_dev(part + (i * 4 + e) * 64, acc[i][e]);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         unsigned old = 0;
         if (lane == 0) old = __hip_atomic_fetch_add(&a.cnt[slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -877,7 +877,7 @@ __global__ __launch_bounds__(PAIR ? 2 * kBlock : kBlock, PAIR ? 1 : 2) void gemm
         for (int sp = 0; sp < kSkMaxSplit; sp++)
             if (sp < nsplit)
 #pragma unroll
-                for (int e = 0; e < 16; e++) pv[sp][e] = ldf<true>(p0 + (size_t)sp * 1024 + e * 64);
+                for (int e = 0; e < 16; e++) pv[sp][e] = ld_dev(p0 + (size_t)sp * 1024 + e * 64);
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
