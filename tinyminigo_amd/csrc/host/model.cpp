@@ -403,6 +403,7 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
         aa.pos_dev = &c->st->pos;
         aa.scale = 1.0f / sqrtf((float)m->hd);
         aa.nsplit = c->attn_nsplit;
+        aa.block = c->attn_block;
         aa.cap = (int)c->max_pos;
         aa.part = m->attn_part;
         aa.part_ml = m->attn_ml;
@@ -425,6 +426,7 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
             oa.part_ml = m->attn_ml;
             oa.pos = &c->st->pos;
             oa.nsplit = c->attn_nsplit;
+            oa.attn_block = c->attn_block;
             oa.hd = m->hd;
             oa.group = m->nq / m->nkv;
         }
@@ -833,7 +835,16 @@ extern "C" int tmg_cache_new(tmg_model *m, uint32_t max_pos, tmg_cache **out) {
     tmg_cache *c = new tmg_cache();
     c->model = m;
     c->max_pos = max_pos;
-    c->attn_nsplit = (int)std::min<uint32_t>(kMaxSplits, (max_pos + kAttnBlock - 1) / kAttnBlock);
+    // Short caches deal the context to at most kFusedSplits splits in small
+    // blocks: at 64-320 positions (1B) 5-8 workgroups per KV head of 16-40
+    // positions each instead of 2-5 of 64, the merge still fused into o_proj.
+    if (max_pos <= (uint32_t)kShortAttnCache) {
+        c->attn_block = attn_chunk(m->hd, m->nq / m->nkv, kAttnThreads, kAttnBlockShort);
+        c->attn_nsplit = (int)std::min<uint32_t>(kFusedSplits, (max_pos + c->attn_block - 1) / c->attn_block);
+    } else {
+        c->attn_block = kAttnBlockLong;
+        c->attn_nsplit = (int)std::min<uint32_t>(kMaxSplits, (max_pos + kAttnBlockLong - 1) / kAttnBlockLong);
+    }
     const size_t n = (size_t)m->L * max_pos * m->kvd;
     int rc = TMG_OK;
     void *k = nullptr, *v = nullptr, *st = nullptr, *hist = nullptr;

@@ -89,6 +89,7 @@ struct tmg_cache {
     int *history = nullptr;
     uint32_t len = 0;                  // host mirror of st->pos
     int attn_nsplit = 1;               // split-K width of decode attention for this cache
+    int attn_block = tmg::kAttnBlockLong;  // positions per block of its split partition
     unsigned *seen = nullptr;          // bitmap of generated ids (repetition penalty)
     unsigned long long *cand = nullptr;  // sampler candidates
     float *draws = nullptr;              // [max_pos + 2] uniform draw per step (sampling)
@@ -101,10 +102,10 @@ struct tmg_cache {
 
 namespace tmg {
 
-// Decode attention: the context is dealt to the splits in kAttnBlock-position
-// blocks; a cache of max_pos rows uses up to ceil(max_pos / kAttnBlock)
-// splits (at most kMaxSplits).  Up to kFusedSplits the merge runs in the
-// o_proj GEMV prologue; above that a combine kernel runs first.
+// Decode attention: the context is dealt to the splits in blocks of
+// attn_block positions; a cache of max_pos rows uses up to
+// ceil(max_pos / attn_block) splits (at most kMaxSplits).  Up to kFusedSplits
+// the merge runs in the o_proj prologue, above in attn_combine_kernel.
 constexpr int kMaxSplits = 32;
 // Sequences per tmg_generate_batch call (the short-prompt GEMM takes up to
 // 255 token rows; the bound keeps the per-call KV allocation in view).

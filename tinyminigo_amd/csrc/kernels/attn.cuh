@@ -28,13 +28,14 @@ namespace tmg {
 // head_dim 128 halve the cross-lane reduction steps per score against one
 // (measured faster with two query heads per KV head, slower with four, where
 // the doubled accumulator registers cost more than the reductions saved).
-template <int HD, int GROUP, int NT = kBlock>
+template <int HD, int GROUP, int NT = kBlock, int CHW = kAttnBlockLong>
 struct AttnGeom {
-    static constexpr int VPL = (HD >= 128 && GROUP <= 2) ? 2 : 1;
+    static constexpr int VPL = attn_vpl(HD, GROUP);
     static constexpr int TS = HD / (4 * VPL);
     static constexpr int NTEAM = NT / TS;
-    static constexpr int J = NTEAM >= 64 ? 1 : 64 / NTEAM;
+    static constexpr int J = CHW > NTEAM ? CHW / NTEAM : 1;
     static constexpr int CH = NTEAM * J;
+    static_assert(CH == attn_chunk(HD, GROUP, NT, CHW), "host and device chunk widths agree");
 };
 
 // One merged (o, max, sum) state per wavefront: the teams of a wavefront are
@@ -49,19 +50,19 @@ struct AttnShared {
 
 // Split count of a decode attention row at context n_ctx: the same formula in
 // the attention kernel, its combine kernel and the fused combine prologue.
-__device__ __forceinline__ int active_splits(int n_ctx, int nsplit) {
-    return min(nsplit, (n_ctx + kAttnBlock - 1) / kAttnBlock);
+__device__ __forceinline__ int active_splits(int n_ctx, int nsplit, int block) {
+    return min(nsplit, (n_ctx + block - 1) / block);
 }
 
-// Partition of a row's context [0, n_ctx) over the splits: 64-position
-// blocks (one chunk of the lane geometry) dealt round robin, split s taking
-// blocks s, s + nsplit, s + 2 nsplit, ...  So split s always starts at
-// position 64 s, and the active splits are min(nsplit, ceil(n_ctx / 64)).
+// Partition of a row's context [0, n_ctx) over the splits: blocks of CH
+// positions (one chunk of the lane geometry) dealt round robin, split s
+// taking blocks s, s + nsplit, s + 2 nsplit, ...  So split s always starts at
+// position CH s, and the active splits are min(nsplit, ceil(n_ctx / CH)).
 
 // With out_f32/out_hi null, or more than one active split, writes (o, max,
 // sum) partials (a split without positions writes max = -inf, sum = 0);
 // otherwise writes the normalized row.
-// With SPEC (decode), the split's first chunk [64 split, + 64) is loaded
+// With SPEC (decode), the split's first chunk [CH split, + CH) is loaded
 // before the position is read from a.pos_dev (rows clamped to the cache
 // capacity a.cap), so the K/V loads do not wait for it; qpos and active are
 // then computed here and the arguments ignored.  Splits found inactive
@@ -88,10 +89,10 @@ __device__ __forceinline__ float team_reduce(float x) {
     return x;
 }
 
-template <int HD, int GROUP, bool SPEC = false, int NT = kBlock>
+template <int HD, int GROUP, bool SPEC = false, int NT = kBlock, int CHW = kAttnBlockLong>
 __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, int ti, int qpos, int active,
                                           AttnShared<HD, GROUP, NT> &sm) {
-    using G = AttnGeom<HD, GROUP, NT>;
+    using G = AttnGeom<HD, GROUP, NT, CHW>;
     constexpr int VPL = G::VPL, TS = G::TS, NTEAM = G::NTEAM;
     constexpr int J = G::J;  // positions per team per chunk
     constexpr int CH = G::CH;
@@ -109,7 +110,6 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
 #pragma unroll
         for (int v = 0; v < VPL; v++) qv[h][v] = *reinterpret_cast<const float4 *>(qrow + (g * GROUP + h) * HD + (v * TS + lt) * 4);
 
-    static_assert(CH == 64, "the split partition deals 64-position blocks");
     float4 kr[J][VPL], vr[J][VPL];
     auto load_kv = [&](float4(&kd)[J][VPL], float4(&vd)[J][VPL], int c0, int lim) {
 #pragma unroll
@@ -130,7 +130,7 @@ __device__ __forceinline__ void attn_item(const AttnArgs &a, int split, int g, i
         // compiler sinks them behind it (into the branch that uses them)
         asm volatile("" ::: "memory");
         qpos = pos0 + ti;
-        active = active_splits(qpos + 1, a.nsplit);
+        active = active_splits(qpos + 1, a.nsplit, CH);
         if (split >= active) return;
     }
     const int n_ctx = qpos + 1;

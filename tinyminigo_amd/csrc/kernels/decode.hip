@@ -232,20 +232,20 @@ __global__ __launch_bounds__(kBlock) void quantize_i8_kernel(uint16_t *w, int in
 
 // SPEC (decode): splits below kSpecSplits load their first chunk before the
 // position is read (see attn_item).
-template <int HD, int GROUP, bool SPEC, int NT = kBlock>
+template <int HD, int GROUP, bool SPEC, int NT = kBlock, int CHW = kAttnBlockLong>
 __global__ __launch_bounds__(NT) void attn_kernel(const AttnArgs a) {
     __shared__ AttnShared<HD, GROUP, NT> sm;
     const int split = blockIdx.x, g = blockIdx.y, ti = blockIdx.z;
     if constexpr (SPEC) {
         if (split < kSpecSplits) {
-            attn_item<HD, GROUP, true, NT>(a, split, g, ti, 0, 0, sm);
+            attn_item<HD, GROUP, true, NT, CHW>(a, split, g, ti, 0, 0, sm);
             return;
         }
     }
     const int qpos = a.pos_seq ? a.pos_seq[ti] : (a.pos_dev ? *a.pos_dev : a.start) + ti;
-    const int active = active_splits(qpos + 1, a.nsplit);
+    const int active = active_splits(qpos + 1, a.nsplit, AttnGeom<HD, GROUP, NT, CHW>::CH);
     if (split >= active) return;
-    attn_item<HD, GROUP, false, NT>(a, split, g, ti, qpos, active, sm);
+    attn_item<HD, GROUP, false, NT, CHW>(a, split, g, ti, qpos, active, sm);
 }
 
 // Merge of the split-K partials of decode row 0, one workgroup per query
@@ -260,7 +260,7 @@ __global__ __launch_bounds__(kBlock) void attn_combine_kernel(const AttnArgs a) 
     const int h = blockIdx.x, t = threadIdx.x;
     const int group = a.nq / a.nkv;
     const int g = h / group, hq = h - g * group;
-    const int active = active_splits(*a.pos_dev + 1, a.nsplit);
+    const int active = active_splits(*a.pos_dev + 1, a.nsplit, a.block ? a.block : kAttnBlockLong);
     const size_t base = (size_t)g * a.nsplit * group + hq;
     float m = -INFINITY, l = 0.0f;
     if (t < active) {
@@ -289,6 +289,23 @@ __global__ __launch_bounds__(kBlock) void attn_combine_kernel(const AttnArgs a) 
 }
 
 constexpr int kWideAttnSplits = 32;
+static_assert(kAttnThreads == kBlock, "the host sizes the attention partition for kBlock threads");
+
+// The instantiation whose chunk (= partition block) is a.block positions:
+// the short-context width (decode only) or kAttnBlockLong.
+template <int HD, int GROUP, bool SPEC>
+hipError_t launch_attn_group(const AttnArgs &a, dim3 grid, hipStream_t s) {
+    const int blk = a.block ? a.block : kAttnBlockLong;
+    if (blk == attn_chunk(HD, GROUP, kBlock, kAttnBlockLong)) {
+        hipLaunchKernelGGL((attn_kernel<HD, GROUP, SPEC, kBlock, kAttnBlockLong>), grid, dim3(kBlock), 0, s, a);
+    } else if (SPEC && blk == attn_chunk(HD, GROUP, kBlock, kAttnBlockShort)) {
+        if constexpr (SPEC)
+            hipLaunchKernelGGL((attn_kernel<HD, GROUP, SPEC, kBlock, kAttnBlockShort>), grid, dim3(kBlock), 0, s, a);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
 
 template <int HD, bool SPEC>
 hipError_t launch_attn_hd(const AttnArgs &a, hipStream_t s) {
@@ -298,19 +315,18 @@ hipError_t launch_attn_hd(const AttnArgs &a, hipStream_t s) {
     // SIMD -- 15.6 against 16.0 us per layer at 8K positions; at short
     // contexts 256 threads are faster (4.5 against 4.7 us).
     if constexpr (HD == 128 && SPEC) {
-        if (a.nsplit >= kWideAttnSplits && a.nq / a.nkv == 2) {
+        if (a.nsplit >= kWideAttnSplits && a.nq / a.nkv == 2 && (a.block ? a.block : kAttnBlockLong) == kAttnBlockLong) {
             hipLaunchKernelGGL((attn_kernel<HD, 2, SPEC, 512>), grid, dim3(512), 0, s, a);
             return hipGetLastError();
         }
     }
     switch (a.nq / a.nkv) {
-        case 1: hipLaunchKernelGGL((attn_kernel<HD, 1, SPEC>), grid, dim3(kBlock), 0, s, a); break;
-        case 2: hipLaunchKernelGGL((attn_kernel<HD, 2, SPEC>), grid, dim3(kBlock), 0, s, a); break;
-        case 4: hipLaunchKernelGGL((attn_kernel<HD, 4, SPEC>), grid, dim3(kBlock), 0, s, a); break;
-        case 8: hipLaunchKernelGGL((attn_kernel<HD, 8, SPEC>), grid, dim3(kBlock), 0, s, a); break;
+        case 1: return launch_attn_group<HD, 1, SPEC>(a, grid, s);
+        case 2: return launch_attn_group<HD, 2, SPEC>(a, grid, s);
+        case 4: return launch_attn_group<HD, 4, SPEC>(a, grid, s);
+        case 8: return launch_attn_group<HD, 8, SPEC>(a, grid, s);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------

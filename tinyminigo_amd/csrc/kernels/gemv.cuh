@@ -496,7 +496,7 @@ __device__ __forceinline__ void act_finish(const GemvArgs &a, int pos, ActIn<KC,
                                            float *scratch) {
     const int t = threadIdx.x;
     if constexpr (PRO == PRO_ATTN_COMBINE) {
-        const int active = active_splits(pos + 1, a.nsplit);
+        const int active = active_splits(pos + 1, a.nsplit, a.attn_block);
 #pragma unroll
         for (int c = 0; c < KC; c++) {
             const int k = c * kChunk + t * 8;

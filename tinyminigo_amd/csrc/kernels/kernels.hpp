@@ -60,7 +60,7 @@ struct GemvArgs {
     // PRO_ATTN_COMBINE: the activation is the attention output, merged from
     // the split-K partials of the decode attention kernel (see AttnArgs)
     const float *part, *part_ml;
-    int nsplit, group;
+    int nsplit, group, attn_block;
     // several sequences (launch_gemv_mt): nb activation rows x[b * in], outputs
     // y[b * out] (RESID) / y[b * out / 2] (SWIGLU) / q_out[b * nq * hd] (QKV),
     // argmax keys argmax_part[b * blocks + block] (LOGITS); sequence b is at
@@ -104,6 +104,7 @@ struct AttnArgs {
     const int *pos_dev;
     float scale;      // 1/sqrt(hd)
     int nsplit;       // grid.x
+    int block;        // positions per block of the split partition (decode; 0 means kAttnBlockLong)
     int cap;          // rows of k_cache / v_cache (bounds the speculative first-chunk loads; 0 disables them)
     float *part;      // [T][nkv][nsplit][group][hd] partial outputs
     float *part_ml;   // [T][nkv][nsplit][group][2] (max of the log2-scaled scores, sum)
@@ -254,9 +255,25 @@ hipError_t launch_copy_row(const float *x, int row, int H, float *dst, hipStream
 // Decode attention with at most this many splits is merged in the o_proj
 // GEMV prologue; with more, by attn_combine_kernel.
 constexpr int kFusedSplits = 8;
-// Decode attention deals the context to its splits in blocks of this many
-// positions (split s takes blocks s, s + nsplit, ...).
-constexpr int kAttnBlock = 64;
+// Decode attention deals the context to its splits in blocks of positions,
+// round robin (split s takes blocks s, s + nsplit, ...); a block is one chunk
+// of the kernel's lane geometry.  Caches of at most kShortAttnCache rows use
+// blocks of about kAttnBlockShort positions over at most kFusedSplits
+// splits (more, smaller workgroups at short contexts, merged in the o_proj
+// prologue); longer caches use kAttnBlockLong.
+constexpr int kAttnBlockLong = 64;
+constexpr int kAttnBlockShort = 16;
+constexpr int kShortAttnCache = 512;
+constexpr int kAttnThreads = 256;  // workgroup size of the decode attention (except the 512-thread long form)
+// Positions per chunk of the decode attention's lane geometry for head_dim
+// hd, `group` query heads per KV head, nt threads, a requested chunk width
+// chw: TS = hd / (4 VPL) lanes per position (VPL float4s of K and of V per
+// lane), NTEAM = nt / TS teams, J = max(1, chw / NTEAM) positions per team.
+__host__ __device__ constexpr int attn_vpl(int hd, int group) { return (hd >= 128 && group <= 2) ? 2 : 1; }
+__host__ __device__ constexpr int attn_nteam(int hd, int group, int nt) { return nt / (hd / (4 * attn_vpl(hd, group))); }
+__host__ __device__ constexpr int attn_chunk(int hd, int group, int nt, int chw) {
+    return attn_nteam(hd, group, nt) * (chw > attn_nteam(hd, group, nt) ? chw / attn_nteam(hd, group, nt) : 1);
+}
 // Splits below this index load their first block before reading the
 // position (speculatively: most of them are active at any context); the
 // others read it first, so a long cache at a short context does not stream
