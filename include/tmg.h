@@ -178,6 +178,10 @@ int tmg_stdrng_uniform(uint64_t seed, size_t n, float *out);
  * default stream).  in must be a multiple of 8 and W 16-byte aligned. */
 int tmg_gemv_bf16(const uint16_t *w_dev, const float *x_dev, float *y_dev, uint32_t out, uint32_t in,
                   void *stream);
+/* The same with W f32 row-major (matmul_w_into's WMat::F32 arm,
+ * src/tensor.rs:387-420: `dot` per row).  in must be a multiple of 8, W and x
+ * 16-byte aligned. */
+int tmg_gemv_f32(const float *w_dev, const float *x_dev, float *y_dev, uint32_t out, uint32_t in, void *stream);
 
 /* Kernel level: tensor::argmax (src/tensor.rs:1063-1073) of x[0, n), a DEVICE
  * f32 vector, written to *out_dev (a DEVICE uint32): the index of the first

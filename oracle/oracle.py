@@ -78,6 +78,8 @@ def _load_lib():
         "om_dot_i8": (C.c_int32, [PI8, PI8, S]),
         "om_matmul_w_i8": (None, [PF, PI8, PF, S, S, PF]),
         "om_matmul_batch_w_i8": (None, [PF, PI8, PF, S, S, S, PF]),
+        "om_matmul_w_f32": (None, [PF, PF, S, S, PF]),
+        "om_matmul_batch_w_f32": (None, [PF, PF, S, S, S, PF]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -142,6 +144,23 @@ def matmul_batch_w(x, w_bf16: np.ndarray, out: int, inp: int, T: int) -> np.ndar
     x, w = f32(x), np.ascontiguousarray(w_bf16, dtype=np.uint16)
     y = np.empty(T * out, np.float32)
     lib.om_matmul_batch_w(fp(x), u16p(w), out, inp, T, fp(y))
+    return y
+
+
+def matmul_w_f32(x, w: np.ndarray, out: int, inp: int) -> np.ndarray:
+    """matmul_w_into for WMat::F32 (src/tensor.rs:387-420): dot per row."""
+    x, w = f32(x), f32(w)
+    y = np.empty(out, np.float32)
+    lib.om_matmul_w_f32(fp(x), fp(w), out, inp, fp(y))
+    return y
+
+
+def matmul_batch_w_f32(x, w: np.ndarray, out: int, inp: int, T: int) -> np.ndarray:
+    """matmul_batch_w_into for WMat::F32 (src/tensor.rs:573-760): dot per
+    element, as gemm_tile_avx2 computes it."""
+    x, w = f32(x), f32(w)
+    y = np.empty(T * out, np.float32)
+    lib.om_matmul_batch_w_f32(fp(x), fp(w), out, inp, T, fp(y))
     return y
 
 
@@ -474,6 +493,7 @@ class _Weights(C.Structure):
         ("wd", C.POINTER(C.c_void_p)), ("in_norm", C.POINTER(C.c_void_p)), ("post_norm", C.POINTER(C.c_void_p)),
         ("final_norm", C.c_void_p), ("embed", C.c_void_p), ("lm_bf16", C.c_void_p),
         ("q8", C.POINTER(C.c_void_p) * 7), ("s8", C.POINTER(C.c_void_p) * 7),
+        ("wf", C.POINTER(C.c_void_p) * 7), ("lm_f32", C.c_void_p),
     ]
 
 
@@ -541,14 +561,12 @@ class OracleModel:
         H, I, V = c.hidden_size, c.intermediate_size, c.vocab_size
         qd, kvd = c.num_attention_heads * c.head_dim, c.num_key_value_heads * c.head_dim
 
-        def need(name, numel, bf16=False):
+        def need(name, numel):
             t = tensors.get(name)
             if t is None:
                 raise OracleError(f"missing tensor `{name}` in safetensors file")
             if int(np.prod(t.shape)) != numel:
                 raise OracleError(f"tensor `{name}` has the wrong size")
-            if bf16 and t.dtype != "BF16":
-                raise OracleError(f"oracle expects BF16 for {name}")
             return t
 
         self._keep = []  # arrays the C side points into
@@ -561,6 +579,10 @@ class OracleModel:
         wkeys = ("wq", "wk", "wv", "wo", "wg", "wu", "wd")
         q8 = {k: (C.c_void_p * L)() for k in wkeys}
         s8 = {k: (C.c_void_p * L)() for k in wkeys}
+        # WMat::F32 (src/model.rs:49-55): an F32 or F16 matrix is converted to
+        # f32 at load; its layer entry goes here instead of the BF16 table
+        wf = {k: (C.c_void_p * L)() for k in wkeys}
+        any_f32 = False
         shapes = {"wq": (qd, H), "wk": (kvd, H), "wv": (kvd, H), "wo": (H, qd), "wg": (I, H), "wu": (I, H),
                   "wd": (H, I)}
         for l in range(L):
@@ -570,11 +592,22 @@ class OracleModel:
                     ("wg", "mlp.gate_proj.weight", I * H), ("wu", "mlp.up_proj.weight", I * H),
                     ("wd", "mlp.down_proj.weight", H * I)]
             for key, name, numel in spec:
-                a = np.ascontiguousarray(need(p + name, numel, bf16=True).data)
-                self._keep.append(a)
-                arrs[key][l] = a.ctypes.data
+                t = need(p + name, numel)
+                if t.dtype == "BF16":
+                    a = np.ascontiguousarray(t.data)
+                    self._keep.append(a)
+                    arrs[key][l] = a.ctypes.data
+                    qa_src = bf16_to_f32(a) if i8 else None
+                else:
+                    a = np.ascontiguousarray(t.data, dtype=np.float32)
+                    self._keep.append(a)
+                    wf[key][l] = a.ctypes.data
+                    any_f32 = True
+                    qa_src = a if i8 else None
                 if i8:
-                    qa, sa = quantize_i8_bf16(a, *shapes[key])
+                    # wmat_maybe_i8 (src/model.rs:60-76): quantize the widened
+                    # BF16 values or the f32 values
+                    qa, sa = quantize_i8(qa_src, *shapes[key])
                     self._keep += [qa, sa]
                     q8[key][l] = qa.ctypes.data
                     s8[key][l] = sa.ctypes.data
@@ -585,15 +618,26 @@ class OracleModel:
         fnorm = _f32vec(need("model.norm.weight", H))
         self._keep.append(fnorm)
         lm = tensors.get("lm_head.weight")
-        lm_arr = None
+        lm_arr = lm_f = None
         if lm is not None:
-            lm_arr = np.ascontiguousarray(need("lm_head.weight", V * H, bf16=True).data)
-            self._keep.append(lm_arr)
+            t = need("lm_head.weight", V * H)
+            if t.dtype == "BF16":
+                lm_arr = np.ascontiguousarray(t.data)
+                self._keep.append(lm_arr)
+            else:
+                lm_f = np.ascontiguousarray(t.data, dtype=np.float32)
+                self._keep.append(lm_f)
         self.tied = lm is None
         w = _Weights(H, L, c.num_attention_heads, c.num_key_value_heads, c.head_dim, I, V, c.rms_norm_eps,
                      c.rope_theta, arrs["wq"], arrs["wk"], arrs["wv"], arrs["wo"], arrs["wg"], arrs["wu"],
                      arrs["wd"], arrs["in_norm"], arrs["post_norm"], fnorm.ctypes.data, embed.ctypes.data,
                      None if lm_arr is None else lm_arr.ctypes.data)
+        if lm_f is not None:
+            w.lm_f32 = lm_f.ctypes.data
+        if any_f32 and not i8:
+            for f, key in enumerate(wkeys):
+                w.wf[f] = C.cast(wf[key], C.POINTER(C.c_void_p))
+            self._keep.append(wf)
         if i8:
             for f, key in enumerate(wkeys):
                 w.q8[f] = C.cast(q8[key], C.POINTER(C.c_void_p))

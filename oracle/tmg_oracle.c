@@ -189,6 +189,73 @@ OM_API void om_matmul_w(const float *x, const uint16_t *w, size_t out, size_t in
     for (size_t i = 0; i < nt; i++) pthread_join(th[i], NULL);
 }
 
+/* matmul_w_into for WMat::F32 (src/tensor.rs:387-420): `dot` (dot_f32_avx2,
+ * src/tensor.rs:58-74) per row, threaded like the BF16 arm. */
+typedef struct {
+    const float *x, *w;
+    float *y;
+    size_t in, start, end;
+} gemv_f32_job;
+
+static void *gemv_f32_worker(void *p) {
+    gemv_f32_job *j = (gemv_f32_job *)p;
+    for (size_t o = j->start; o < j->end; o++) j->y[o] = om_dot(j->x, j->w + o * j->in, j->in);
+    return NULL;
+}
+
+OM_API void om_matmul_w_f32(const float *x, const float *w, size_t out, size_t in, float *y) {
+    size_t nthreads = (size_t)num_threads() / 4;
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > out) nthreads = out;
+    if (nthreads <= 1 || out < 64) {
+        for (size_t o = 0; o < out; o++) y[o] = om_dot(x, w + o * in, in);
+        return;
+    }
+    size_t chunk = (out + nthreads - 1) / nthreads;
+    pthread_t th[256];
+    gemv_f32_job jobs[256];
+    size_t nt = 0;
+    for (size_t s = 0; s < out && nt < 256; s += chunk, nt++) {
+        jobs[nt] = (gemv_f32_job){x, w, y, in, s, s + chunk < out ? s + chunk : out};
+        pthread_create(&th[nt], NULL, gemv_f32_worker, &jobs[nt]);
+    }
+    for (size_t i = 0; i < nt; i++) pthread_join(th[i], NULL);
+}
+
+/* matmul_batch_w_into for WMat::F32 (src/tensor.rs:573-760): on an AVX2
+ * host gemm_tile_avx2 loads f32 weight lanes where the BF16 arm widens
+ * (load_w_m256, src/tensor.rs:899-904) and keeps dot's order per element,
+ * so every element equals dot(x_t, w_o) (src/tensor.rs:734-738); the
+ * scalar fallback is that dot too.  Rows are split over the cores. */
+typedef struct {
+    const float *x, *w;
+    float *y;
+    size_t out, in, T, start, end;
+} gemm_f32_job;
+
+static void *gemm_f32_worker(void *p) {
+    gemm_f32_job *j = (gemm_f32_job *)p;
+    for (size_t o = j->start; o < j->end; o++)
+        for (size_t t = 0; t < j->T; t++) j->y[t * j->out + o] = om_dot(j->x + t * j->in, j->w + o * j->in, j->in);
+    return NULL;
+}
+
+OM_API void om_matmul_batch_w_f32(const float *x, const float *w, size_t out, size_t in, size_t T, float *y) {
+    size_t nthreads = (size_t)num_threads();
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > out) nthreads = out;
+    if (nthreads > 256) nthreads = 256;
+    size_t chunk = (out + nthreads - 1) / nthreads;
+    pthread_t th[256];
+    gemm_f32_job jobs[256];
+    size_t nt = 0;
+    for (size_t s = 0; s < out && nt < 256; s += chunk, nt++) {
+        jobs[nt] = (gemm_f32_job){x, w, y, out, in, T, s, s + chunk < out ? s + chunk : out};
+        pthread_create(&th[nt], NULL, gemm_f32_worker, &jobs[nt]);
+    }
+    for (size_t i = 0; i < nt; i++) pthread_join(th[i], NULL);
+}
+
 /* ------------------------------------------------------------------------ */
 /* A7: prefill GEMM Y[T,out] = X[T,in] W^T (src/tensor.rs:573-858)           */
 /* ------------------------------------------------------------------------ */
@@ -920,6 +987,11 @@ typedef struct {
      * BF16 mode.  lm_head, norms and the embedding stay as above. */
     const int8_t **q8[7];
     const float **s8[7];
+    /* WMat::F32 matrices (src/model.rs:49-55: F32 or F16 tensors converted
+     * at load): per-layer f32 [out,in] rows of q, k, v, o, gate, up, down;
+     * a NULL table, or a NULL entry, means that layer's matrix is BF16 */
+    const float **wf[7];
+    const float *lm_f32; /* untied f32 lm_head [V,H], or NULL */
 } om_weights;
 
 enum { W_Q, W_K, W_V, W_O, W_G, W_U, W_D };
@@ -929,10 +1001,14 @@ static const uint16_t *w_bf16(const om_weights *w, int which, int l) {
     return t[which][l];
 }
 
+static const float *w_f32(const om_weights *w, int which, int l) { return w->wf[which] ? w->wf[which][l] : NULL; }
+
 /* matmul_w_into / matmul_batch_w_into dispatch on the WMat variant. */
 static void lin(const om_weights *w, int which, int l, const float *x, size_t out, size_t in, float *y) {
     if (w->q8[which])
         om_matmul_w_i8(x, w->q8[which][l], w->s8[which][l], out, in, y);
+    else if (w_f32(w, which, l))
+        om_matmul_w_f32(x, w_f32(w, which, l), out, in, y);
     else
         om_matmul_w(x, w_bf16(w, which, l), out, in, y);
 }
@@ -941,6 +1017,8 @@ static void lin_batch(const om_weights *w, int which, int l, const float *x, siz
                       float *y) {
     if (w->q8[which])
         om_matmul_batch_w_i8(x, w->q8[which][l], w->s8[which][l], out, in, T, y);
+    else if (w_f32(w, which, l))
+        om_matmul_batch_w_f32(x, w_f32(w, which, l), out, in, T, y);
     else
         om_matmul_batch_w(x, w_bf16(w, which, l), out, in, T, y);
 }
@@ -1081,6 +1159,8 @@ static void lm_head(const om_model *m, const float *x, float *logits) {
     const om_weights *w = &m->w;
     if (w->lm_bf16) {
         om_matmul_w(x, w->lm_bf16, (size_t)w->vocab, (size_t)w->hidden, logits);
+    } else if (w->lm_f32) {
+        om_matmul_w_f32(x, w->lm_f32, (size_t)w->vocab, (size_t)w->hidden, logits);
     } else {
         /* tied: WMat::F32(embed) (src/model.rs:230-233) -> matmul_w_into's f32
          * dot path, threaded the same way as the BF16 path. */

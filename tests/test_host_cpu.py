@@ -66,8 +66,9 @@ def test_config_defaults_and_errors(tmp_path):
         T.ModelConfig.load(str(tmp_path / "missing.json"))
 
 
-def _copy_model(src_dir, dst_dir, mutate=None, drop=None, dtype_of=None):
-    """Rewrite a synthetic model with one tensor dropped or retyped."""
+def _copy_model(src_dir, dst_dir, mutate=None, drop=None, dtype_of=None, dtype_to="F32"):
+    """Rewrite a synthetic model with one tensor dropped or retyped (its BF16
+    values widened to f32 and labelled `dtype_to`)."""
     with open(os.path.join(src_dir, "model.safetensors"), "rb") as f:
         n = struct.unpack("<Q", f.read(8))[0]
         hdr = json.loads(f.read(n))
@@ -80,7 +81,7 @@ def _copy_model(src_dir, dst_dir, mutate=None, drop=None, dtype_of=None):
         dt = meta["dtype"]
         if name == dtype_of:
             raw = (np.frombuffer(raw, np.uint16).astype(np.uint32) << 16).view(np.float32).tobytes()
-            dt = "F32"
+            dt = dtype_to
         out_hdr[name] = {"dtype": dt, "shape": meta["shape"], "data_offsets": [off, off + len(raw)]}
         blobs.append(raw)
         off += len(raw)
@@ -102,10 +103,18 @@ def test_model_load_error_paths(tiny_path, tmp_path):
     p = _copy_model(src, str(tmp_path / "a"), drop="model.layers.1.mlp.up_proj.weight")
     with pytest.raises(T.TmgError, match="missing tensor `model.layers.1.mlp.up_proj.weight`"):
         T.Model.load(p)
-    # weight matrix not BF16: the GPU path streams raw BF16 only
-    p = _copy_model(src, str(tmp_path / "b"), dtype_of="model.layers.0.self_attn.q_proj.weight")
-    with pytest.raises(T.TmgError, match="TMG_E_DTYPE"):
+    # a weight matrix of a dtype the reference does not read
+    # (src/safetensors_loader.rs:137-142)
+    p = _copy_model(src, str(tmp_path / "b"), dtype_of="model.layers.0.self_attn.q_proj.weight", dtype_to="I32")
+    with pytest.raises(T.TmgError, match="TMG_E_DTYPE.*unsupported dtype I32"):
         T.Model.load(p)
+    # an F32 weight matrix is read (WMat::F32, src/model.rs:49-55): validation
+    # passes, and without a GPU the load stops at the device
+    p = _copy_model(src, str(tmp_path / "b2"), dtype_of="model.layers.0.self_attn.q_proj.weight")
+    try:
+        T.Model.load(p).close()
+    except T.TmgError as e:
+        assert "TMG_E_DTYPE" not in str(e), str(e)
     # config.json must sit next to the weights (src/config.rs:174-184)
     os.makedirs(tmp_path / "c", exist_ok=True)
     with open(tmp_path / "c" / "model.safetensors", "wb") as f:

@@ -120,6 +120,7 @@ SIGNATURES = {
     "tmg_tmb_repack": (C.c_int, [C.c_char_p, C.c_char_p]),
     "tmg_tmb_config": (C.c_int, [C.c_char_p, C.POINTER(tmg_config)]),
     "tmg_gemv_bf16": (C.c_int, [P, P, P, C.c_uint32, C.c_uint32, P]),
+    "tmg_gemv_f32": (C.c_int, [P, P, P, C.c_uint32, C.c_uint32, P]),
     "tmg_argmax_f32": (C.c_int, [P, C.c_uint32, P, P]),
     "tmg_argmax_f32_noalloc": (C.c_int, [P, C.c_uint32, P, P]),
     "tmg_stdrng_uniform": (C.c_int, [C.c_uint64, C.c_size_t, PF]),

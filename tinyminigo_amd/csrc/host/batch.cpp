@@ -314,6 +314,8 @@ extern "C" int tmg_generate_batch(tmg_model *m, const uint32_t *const *prompts, 
     }
     if (m->i8)
         return set_error(TMG_E_INVALID, "batched decode multiplies BF16 weights: load the model without TMG_I8");
+    if (m->any_f32)
+        return set_error(TMG_E_INVALID, "batched decode multiplies BF16 weights: the model has f32 weight matrices");
     if (decode_ms) *decode_ms = 0.0f;
     if (max_tokens == 0) return TMG_OK;
     (void)hipSetDevice(m->device);

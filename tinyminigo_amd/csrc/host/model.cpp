@@ -102,16 +102,6 @@ static int need(const SafeTensorsFile &f, const std::string &name, const std::ve
     return TMG_OK;
 }
 
-static int need_bf16(const SafeTensorsFile &f, const std::string &name, const std::vector<uint64_t> &shape,
-                     const TensorEntry **out) {
-    int rc = need(f, name, shape, out);
-    if (rc) return rc;
-    if ((*out)->dtype != DType::BF16)
-        return set_error(TMG_E_DTYPE, "tensor " + name + " is " + (*out)->dtype_name +
-                                          ": the GPU decode path streams raw BF16 weight matrices only");
-    return TMG_OK;
-}
-
 static int upload_f32(tmg_model *m, const SafeTensorsFile &f, const TensorEntry *e, float **dst) {
     std::vector<float> v;
     int rc = tensor_to_f32(f, *e, &v);
@@ -126,6 +116,21 @@ static int upload_raw(tmg_model *m, const void *src, size_t bytes, uint16_t **ds
     if ((rc = dev_alloc(m, dst, bytes / 2))) return rc;
     TMG_HIP(hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice));
     return TMG_OK;
+}
+
+static int upload_floats(tmg_model *m, const std::vector<float> &v, float **dst) {
+    int rc;
+    if ((rc = dev_alloc(m, dst, v.size()))) return rc;
+    TMG_HIP(hipMemcpy(*dst, v.data(), v.size() * 4, hipMemcpyHostToDevice));
+    return TMG_OK;
+}
+
+// Releases one allocation of the model before the model itself.
+static void dev_free(tmg_model *m, void *p) {
+    auto it = std::find(m->allocs.begin(), m->allocs.end(), p);
+    if (it == m->allocs.end()) return;
+    m->allocs.erase(it);
+    (void)hipFree(p);
 }
 
 // Host-only phase: config.json + every tensor's presence, shape and dtype,
@@ -169,35 +174,23 @@ static int validate_files(tmg_model *m, const std::string &path, SafeTensorsFile
     const uint64_t H = m->H, I = m->I, V = m->V, qd = m->qd, kvd = m->kvd;
     const TensorEntry *e;
     if ((rc = need(*f, "model.embed_tokens.weight", {V, H}, &e))) return rc;
+    // weight matrices: BF16 kept raw; F32 / F16 become f32 rows (WMat::F32,
+    // src/model.rs:49-55); any other dtype is an error (need)
     for (int l = 0; l < m->L; l++) {
         const std::string p = "model.layers." + std::to_string(l) + ".";
-        if ((rc = need_bf16(*f, p + "self_attn.q_proj.weight", {qd, H}, &e)) ||
-            (rc = need_bf16(*f, p + "self_attn.k_proj.weight", {kvd, H}, &e)) ||
-            (rc = need_bf16(*f, p + "self_attn.v_proj.weight", {kvd, H}, &e)) ||
-            (rc = need_bf16(*f, p + "self_attn.o_proj.weight", {H, qd}, &e)) ||
-            (rc = need_bf16(*f, p + "mlp.gate_proj.weight", {I, H}, &e)) ||
-            (rc = need_bf16(*f, p + "mlp.up_proj.weight", {I, H}, &e)) ||
-            (rc = need_bf16(*f, p + "mlp.down_proj.weight", {H, I}, &e)) ||
+        if ((rc = need(*f, p + "self_attn.q_proj.weight", {qd, H}, &e)) ||
+            (rc = need(*f, p + "self_attn.k_proj.weight", {kvd, H}, &e)) ||
+            (rc = need(*f, p + "self_attn.v_proj.weight", {kvd, H}, &e)) ||
+            (rc = need(*f, p + "self_attn.o_proj.weight", {H, qd}, &e)) ||
+            (rc = need(*f, p + "mlp.gate_proj.weight", {I, H}, &e)) ||
+            (rc = need(*f, p + "mlp.up_proj.weight", {I, H}, &e)) ||
+            (rc = need(*f, p + "mlp.down_proj.weight", {H, I}, &e)) ||
             (rc = need(*f, p + "input_layernorm.weight", {H}, &e)) ||
             (rc = need(*f, p + "post_attention_layernorm.weight", {H}, &e)))
             return rc;
     }
     if ((rc = need(*f, "model.norm.weight", {H}, &e))) return rc;
-    if (f->find("lm_head.weight")) {
-        if ((rc = need_bf16(*f, "lm_head.weight", {V, H}, &e))) return rc;
-    } else if (f->find("model.embed_tokens.weight")->dtype != DType::BF16) {
-        // a tied lm_head streams the table as BF16: an F16/F32 table is
-        // accepted when every value is a BF16 value (a TMB file stores the
-        // embedding widened to f32)
-        std::vector<float> v;
-        if ((rc = tensor_to_f32(*f, *f->find("model.embed_tokens.weight"), &v))) return rc;
-        for (float x : v) {
-            uint32_t u;
-            memcpy(&u, &x, 4);
-            if (u & 0xFFFFu)
-                return set_error(TMG_E_DTYPE, "tied lm_head needs an embedding table of BF16 values on the GPU path");
-        }
-    }
+    if (f->find("lm_head.weight") && (rc = need(*f, "lm_head.weight", {V, H}, &e))) return rc;
     return TMG_OK;
 }
 
@@ -240,61 +233,123 @@ static int load_model(tmg_model *m, const SafeTensorsFile &f) {
 
     const int half = m->hd / 2;
     std::vector<uint16_t> stage;
+    std::vector<float> stagef;
     m->layers.resize(m->L);
     for (int l = 0; l < m->L; l++) {
         const std::string p = "model.layers." + std::to_string(l) + ".";
         const TensorEntry *wq, *wk, *wv, *wo, *wg, *wu, *wd, *n1, *n2;
-        if ((rc = need_bf16(f, p + "self_attn.q_proj.weight", {qd, H}, &wq)) ||
-            (rc = need_bf16(f, p + "self_attn.k_proj.weight", {kvd, H}, &wk)) ||
-            (rc = need_bf16(f, p + "self_attn.v_proj.weight", {kvd, H}, &wv)) ||
-            (rc = need_bf16(f, p + "self_attn.o_proj.weight", {H, qd}, &wo)) ||
-            (rc = need_bf16(f, p + "mlp.gate_proj.weight", {I, H}, &wg)) ||
-            (rc = need_bf16(f, p + "mlp.up_proj.weight", {I, H}, &wu)) ||
-            (rc = need_bf16(f, p + "mlp.down_proj.weight", {H, I}, &wd)) ||
+        if ((rc = need(f, p + "self_attn.q_proj.weight", {qd, H}, &wq)) ||
+            (rc = need(f, p + "self_attn.k_proj.weight", {kvd, H}, &wk)) ||
+            (rc = need(f, p + "self_attn.v_proj.weight", {kvd, H}, &wv)) ||
+            (rc = need(f, p + "self_attn.o_proj.weight", {H, qd}, &wo)) ||
+            (rc = need(f, p + "mlp.gate_proj.weight", {I, H}, &wg)) ||
+            (rc = need(f, p + "mlp.up_proj.weight", {I, H}, &wu)) ||
+            (rc = need(f, p + "mlp.down_proj.weight", {H, I}, &wd)) ||
             (rc = need(f, p + "input_layernorm.weight", {H}, &n1)) ||
             (rc = need(f, p + "post_attention_layernorm.weight", {H}, &n2)))
             return rc;
         tmg_model::Layer &ly = m->layers[l];
+        // A device matrix keeps raw BF16 rows when all its file tensors are
+        // BF16 (WMat::BF16); otherwise it holds f32 rows (WMat::F32: F32 and
+        // F16 tensors converted as the reference converts them, BF16 parts
+        // widened exactly), in the same row order.
+        auto bf16 = [](std::initializer_list<const TensorEntry *> es) {
+            for (const TensorEntry *e : es)
+                if (e->dtype != DType::BF16) return false;
+            return true;
+        };
         // QKV: logical rows [q; k; v]; physical row 2P = (head, j), 2P+1 = (head, j+hd/2)
-        stage.resize((size_t)m->qkv_rows * H);
-        const uint16_t *src[3] = {(const uint16_t *)f.data(*wq), (const uint16_t *)f.data(*wk),
-                                  (const uint16_t *)f.data(*wv)};
         const int sec_rows[3] = {m->qd, m->kvd, m->kvd};
-        int P = 0;
-        for (int sct = 0; sct < 3; sct++)
-            for (int hh = 0; hh < sec_rows[sct] / m->hd; hh++)
-                for (int j = 0; j < half; j++, P++) {
-                    memcpy(&stage[(size_t)(2 * P) * H], src[sct] + ((size_t)hh * m->hd + j) * H, H * 2);
-                    memcpy(&stage[(size_t)(2 * P + 1) * H], src[sct] + ((size_t)hh * m->hd + j + half) * H, H * 2);
-                }
-        if ((rc = upload_raw(m, stage.data(), stage.size() * 2, &ly.qkv))) return rc;
-        if ((rc = upload_raw(m, f.data(*wo), H * qd * 2, &ly.o))) return rc;
-        stage.resize((size_t)2 * I * H);
-        const uint16_t *g = (const uint16_t *)f.data(*wg), *u = (const uint16_t *)f.data(*wu);
-        for (uint64_t r = 0; r < I; r++) {
-            memcpy(&stage[(2 * r) * H], g + r * H, H * 2);
-            memcpy(&stage[(2 * r + 1) * H], u + r * H, H * 2);
+        if (bf16({wq, wk, wv})) {
+            stage.resize((size_t)m->qkv_rows * H);
+            const uint16_t *src[3] = {(const uint16_t *)f.data(*wq), (const uint16_t *)f.data(*wk),
+                                      (const uint16_t *)f.data(*wv)};
+            int P = 0;
+            for (int sct = 0; sct < 3; sct++)
+                for (int hh = 0; hh < sec_rows[sct] / m->hd; hh++)
+                    for (int j = 0; j < half; j++, P++) {
+                        memcpy(&stage[(size_t)(2 * P) * H], src[sct] + ((size_t)hh * m->hd + j) * H, H * 2);
+                        memcpy(&stage[(size_t)(2 * P + 1) * H], src[sct] + ((size_t)hh * m->hd + j + half) * H,
+                               H * 2);
+                    }
+            if ((rc = upload_raw(m, stage.data(), stage.size() * 2, &ly.qkv))) return rc;
+        } else {
+            std::vector<float> sf[3];
+            if ((rc = tensor_to_f32(f, *wq, &sf[0])) || (rc = tensor_to_f32(f, *wk, &sf[1])) ||
+                (rc = tensor_to_f32(f, *wv, &sf[2])))
+                return rc;
+            stagef.resize((size_t)m->qkv_rows * H);
+            int P = 0;
+            for (int sct = 0; sct < 3; sct++)
+                for (int hh = 0; hh < sec_rows[sct] / m->hd; hh++)
+                    for (int j = 0; j < half; j++, P++) {
+                        memcpy(&stagef[(size_t)(2 * P) * H], sf[sct].data() + ((size_t)hh * m->hd + j) * H, H * 4);
+                        memcpy(&stagef[(size_t)(2 * P + 1) * H],
+                               sf[sct].data() + ((size_t)hh * m->hd + j + half) * H, H * 4);
+                    }
+            if ((rc = upload_floats(m, stagef, &ly.qkv_f))) return rc;
         }
-        if ((rc = upload_raw(m, stage.data(), stage.size() * 2, &ly.gu))) return rc;
-        if ((rc = upload_raw(m, f.data(*wd), H * I * 2, &ly.down))) return rc;
+        if (bf16({wo})) {
+            if ((rc = upload_raw(m, f.data(*wo), H * qd * 2, &ly.o))) return rc;
+        } else if ((rc = upload_f32(m, f, wo, &ly.o_f))) {
+            return rc;
+        }
+        if (bf16({wg, wu})) {
+            stage.resize((size_t)2 * I * H);
+            const uint16_t *g = (const uint16_t *)f.data(*wg), *u = (const uint16_t *)f.data(*wu);
+            for (uint64_t r = 0; r < I; r++) {
+                memcpy(&stage[(2 * r) * H], g + r * H, H * 2);
+                memcpy(&stage[(2 * r + 1) * H], u + r * H, H * 2);
+            }
+            if ((rc = upload_raw(m, stage.data(), stage.size() * 2, &ly.gu))) return rc;
+        } else {
+            std::vector<float> g, u;
+            if ((rc = tensor_to_f32(f, *wg, &g)) || (rc = tensor_to_f32(f, *wu, &u))) return rc;
+            stagef.resize((size_t)2 * I * H);
+            for (uint64_t r = 0; r < I; r++) {
+                memcpy(&stagef[(2 * r) * H], g.data() + r * H, H * 4);
+                memcpy(&stagef[(2 * r + 1) * H], u.data() + r * H, H * 4);
+            }
+            if ((rc = upload_floats(m, stagef, &ly.gu_f))) return rc;
+        }
+        if (bf16({wd})) {
+            if ((rc = upload_raw(m, f.data(*wd), H * I * 2, &ly.down))) return rc;
+        } else if ((rc = upload_f32(m, f, wd, &ly.down_f))) {
+            return rc;
+        }
+        if (ly.qkv_f || ly.o_f || ly.gu_f || ly.down_f) m->any_f32 = true;
         if ((rc = upload_f32(m, f, n1, &ly.in_norm)) || (rc = upload_f32(m, f, n2, &ly.post_norm))) return rc;
         if (m->i8) {
-            // per-row quantization commutes with the row permutations above
+            // per-row quantization commutes with the row permutations above;
+            // f32 rows are quantized from their f32 values (wmat_maybe_i8,
+            // src/model.rs:69-72), their codes then kept as BF16 for prefill
+            // and the f32 rows released
             struct {
-                uint16_t *w;
+                uint16_t **w;
+                float **wf;
                 int rows, in;
                 int8_t **q8;
                 float **sc;
-            } mats[4] = {{ly.qkv, m->qkv_rows, m->H, &ly.qkv8, &ly.qkv_s},
-                         {ly.o, m->H, m->qd, &ly.o8, &ly.o_s},
-                         {ly.gu, 2 * m->I, m->H, &ly.gu8, &ly.gu_s},
-                         {ly.down, m->H, m->I, &ly.down8, &ly.down_s}};
+            } mats[4] = {{&ly.qkv, &ly.qkv_f, m->qkv_rows, m->H, &ly.qkv8, &ly.qkv_s},
+                         {&ly.o, &ly.o_f, m->H, m->qd, &ly.o8, &ly.o_s},
+                         {&ly.gu, &ly.gu_f, 2 * m->I, m->H, &ly.gu8, &ly.gu_s},
+                         {&ly.down, &ly.down_f, m->H, m->I, &ly.down8, &ly.down_s}};
             for (auto &mt : mats) {
                 if ((rc = dev_alloc(m, mt.q8, (size_t)mt.rows * mt.in)) || (rc = dev_alloc(m, mt.sc, (size_t)mt.rows)))
                     return rc;
-                TMG_HIP(launch_quantize_i8(mt.w, mt.rows, mt.in, *mt.q8, *mt.sc, true, m->stream));
+                if (*mt.wf) {
+                    if ((rc = dev_alloc(m, mt.w, (size_t)mt.rows * mt.in))) return rc;
+                    TMG_HIP(launch_quantize_i8_f32(*mt.wf, mt.rows, mt.in, *mt.q8, *mt.sc, *mt.w, m->stream));
+                } else {
+                    TMG_HIP(launch_quantize_i8(*mt.w, mt.rows, mt.in, *mt.q8, *mt.sc, true, m->stream));
+                }
             }
             TMG_HIP(hipStreamSynchronize(m->stream));
+            for (auto &mt : mats)
+                if (*mt.wf) {
+                    dev_free(m, *mt.wf);
+                    *mt.wf = nullptr;
+                }
         }
     }
     const TensorEntry *fn;
@@ -305,15 +360,23 @@ static int load_model(tmg_model *m, const SafeTensorsFile &f) {
     // the reference's f32 copy element for element.
     if (f.find("lm_head.weight")) {
         const TensorEntry *lm;
-        if ((rc = need_bf16(f, "lm_head.weight", {V, H}, &lm))) return rc;
-        if ((rc = upload_raw(m, f.data(*lm), V * H * 2, &m->lm_head))) return rc;
+        if ((rc = need(f, "lm_head.weight", {V, H}, &lm))) return rc;
+        if (lm->dtype == DType::BF16) {
+            if ((rc = upload_raw(m, f.data(*lm), V * H * 2, &m->lm_head))) return rc;
+        } else if ((rc = upload_f32(m, f, lm, &m->lm_head_f))) {
+            return rc;
+        }
         m->cfg.tied_lm_head = 0;
     } else {
-        if (!m->embed_bf16)
-            return set_error(TMG_E_DTYPE, "tied lm_head needs a BF16 embedding table on the GPU path");
-        m->lm_head = m->embed_bf16;
+        // WMat::F32(embed): the BF16 table when the file's values are BF16
+        // values (exact), else the f32 table
+        if (m->embed_bf16)
+            m->lm_head = m->embed_bf16;
+        else
+            m->lm_head_f = m->embed_f32;
         m->cfg.tied_lm_head = 1;
     }
+    if (m->lm_head_f) m->any_f32 = true;
 
     // decode scratch
     if ((rc = dev_alloc(m, &m->x, H)) || (rc = dev_alloc(m, &m->q, qd)) || (rc = dev_alloc(m, &m->attn_out, qd)) ||
@@ -322,7 +385,7 @@ static int load_model(tmg_model *m, const SafeTensorsFile &f) {
     if ((rc = dev_alloc(m, &m->attn_part, (size_t)m->nkv * kMaxSplits * group * m->hd)) ||
         (rc = dev_alloc(m, &m->attn_ml, (size_t)m->nkv * kMaxSplits * group * 2)))
         return rc;
-    m->argmax_nparts = gemv_blocks(m->V, m->H);
+    m->argmax_nparts = gemv_blocks(m->V, m->H, m->lm_head_f != nullptr);
     if ((rc = dev_alloc(m, &m->argmax_part, (size_t)m->argmax_nparts))) return rc;
     if ((rc = ensure_rope(m, 64))) return rc;
     if ((rc = pinned(m, (size_t)std::max<uint64_t>(V * 4, 1 << 16)))) return rc;
@@ -386,11 +449,12 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
             qa.embed_f32 = m->embed_f32;
             qa.x_store = m->x;
         }
+        qa.Wf = ly.qkv_f;
         if (m->i8) {
             qa.W8 = ly.qkv8;
             qa.wscale = ly.qkv_s;
         }
-        if (!rec || rec->want("gemv_qkv_rope", (double)m->qkv_rows * (H * wb + sb) + H * 8.0 + (qd + 2 * kvd) * 4.0)) TMG_HIP(launch_gemv(pro, EPI_QKV, qa, s));
+        if (!rec || rec->want("gemv_qkv_rope", (double)m->qkv_rows * (H * (ly.qkv_f ? 4.0 : wb) + sb) + H * 8.0 + (qd + 2 * kvd) * 4.0)) TMG_HIP(launch_gemv(pro, EPI_QKV, qa, s));
 
         AttnArgs aa{};
         aa.q = m->q;
@@ -430,11 +494,12 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
             oa.hd = m->hd;
             oa.group = m->nq / m->nkv;
         }
+        oa.Wf = ly.o_f;
         if (m->i8) {
             oa.W8 = ly.o8;
             oa.wscale = ly.o_s;
         }
-        if (!rec || rec->want("gemv_o_resid", (double)H * (qd * wb + sb) + qd * 4.0 + H * 8.0)) TMG_HIP(launch_gemv(fused ? PRO_ATTN_COMBINE : PRO_PLAIN, EPI_RESID, oa, s));
+        if (!rec || rec->want("gemv_o_resid", (double)H * (qd * (ly.o_f ? 4.0 : wb) + sb) + qd * 4.0 + H * 8.0)) TMG_HIP(launch_gemv(fused ? PRO_ATTN_COMBINE : PRO_PLAIN, EPI_RESID, oa, s));
 
         GemvArgs ga{};
         ga.W = ly.gu;
@@ -444,11 +509,12 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
         ga.norm_w = ly.post_norm;
         ga.eps = m->cfg.rms_norm_eps;
         ga.y = m->h;
+        ga.Wf = ly.gu_f;
         if (m->i8) {
             ga.W8 = ly.gu8;
             ga.wscale = ly.gu_s;
         }
-        if (!rec || rec->want("gemv_gateup_swiglu", 2.0 * I * (H * wb + sb) + H * 8.0 + I * 4.0)) TMG_HIP(launch_gemv(PRO_NORM, EPI_SWIGLU, ga, s));
+        if (!rec || rec->want("gemv_gateup_swiglu", 2.0 * I * (H * (ly.gu_f ? 4.0 : wb) + sb) + H * 8.0 + I * 4.0)) TMG_HIP(launch_gemv(PRO_NORM, EPI_SWIGLU, ga, s));
 
         GemvArgs da{};
         da.W = ly.down;
@@ -456,14 +522,16 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
         da.in = I;
         da.x = m->h;
         da.y = m->x;
+        da.Wf = ly.down_f;
         if (m->i8) {
             da.W8 = ly.down8;
             da.wscale = ly.down_s;
         }
-        if (!rec || rec->want("gemv_down_resid", (double)H * (I * wb + sb) + I * 4.0 + H * 8.0)) TMG_HIP(launch_gemv(PRO_PLAIN, EPI_RESID, da, s));
+        if (!rec || rec->want("gemv_down_resid", (double)H * (I * (ly.down_f ? 4.0 : wb) + sb) + I * 4.0 + H * 8.0)) TMG_HIP(launch_gemv(PRO_PLAIN, EPI_RESID, da, s));
     }
     GemvArgs la{};
     la.W = m->lm_head;
+    la.Wf = m->lm_head_f;
     la.out = m->V;
     la.in = H;
     la.x = m->x;
@@ -471,7 +539,7 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
     la.eps = m->cfg.rms_norm_eps;
     la.y = m->logits;
     la.argmax_part = mode == SEL_ARGMAX ? m->argmax_part : nullptr;
-    if (!rec || rec->want("gemv_lmhead_argmax", (double)m->V * H * 2 + H * 8.0 + m->V * 4.0)) TMG_HIP(launch_gemv(PRO_NORM, EPI_LOGITS, la, s));
+    if (!rec || rec->want("gemv_lmhead_argmax", (double)m->V * H * (m->lm_head_f ? 4 : 2) + H * 8.0 + m->V * 4.0)) TMG_HIP(launch_gemv(PRO_NORM, EPI_LOGITS, la, s));
     int rc = TMG_OK;
     if (!rec || rec->want(mode == SEL_ARGMAX ? "finalize" : "sample", mode == SEL_ARGMAX ? 0.0 : m->V * 4.0)) rc = enqueue_select(m, c, mode, 1);
     return rc;
@@ -623,7 +691,10 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
     // epilogues, instead of a separate normalization pass over the residual
     // (shapes permitting: hidden a multiple of 64, all four GEMMs on kernels
     // with the staged epilogue)
-    const bool hand_off = H % 256 == 0 && H / 64 <= kMaxNormGroups && gemm_stages_output(m->qkv_rows, T, H) &&
+    // (f32 weight matrices run a per-element epilogue: no hand-off)
+    bool f32_mats = false;
+    for (const tmg_model::Layer &ly : m->layers) f32_mats = f32_mats || ly.qkv_f || ly.o_f || ly.gu_f || ly.down_f;
+    const bool hand_off = !f32_mats && H % 256 == 0 && H / 64 <= kMaxNormGroups && gemm_stages_output(m->qkv_rows, T, H) &&
                           gemm_stages_output(H, T, qd) && gemm_stages_output(2 * I, T, H) &&
                           gemm_stages_output(H, T, I);
     auto norm_in = [&](GemmArgs &a) {  // consumer of a handed-off norm
@@ -645,6 +716,7 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         if (!in_handed) TMG_HIP(launch_rmsnorm_split(m->pf_x, ly.in_norm, eps, T, H, m->pf_hi, m->pf_lo, s));
         GemmArgs g{};
         g.W = ly.qkv;
+        g.Wf = ly.qkv_f;
         g.Bhi = m->pf_hi;
         g.Blo = m->pf_lo;
         g.M = m->qkv_rows;
@@ -694,6 +766,7 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
 
         GemmArgs o{};
         o.W = ly.o;
+        o.Wf = ly.o_f;
         o.Bhi = m->pf_ahi;
         o.Blo = m->pf_alo;
         o.M = H;
@@ -709,6 +782,7 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
         if (!hand_off) TMG_HIP(launch_rmsnorm_split(m->pf_x, ly.post_norm, eps, T, H, m->pf_hi, m->pf_lo, s));
         GemmArgs gu{};
         gu.W = ly.gu;
+        gu.Wf = ly.gu_f;
         gu.Bhi = m->pf_hi;
         gu.Blo = m->pf_lo;
         gu.M = 2 * I;
@@ -724,6 +798,7 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
 
         GemmArgs d{};
         d.W = ly.down;
+        d.Wf = ly.down_f;
         d.Bhi = m->pf_hhi;
         d.Blo = m->pf_hlo;
         d.M = H;
@@ -739,6 +814,7 @@ int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n) {
     // final norm of the last row (batch association) + lm_head + argmax
     GemvArgs la{};
     la.W = m->lm_head;
+    la.Wf = m->lm_head_f;
     la.out = m->V;
     la.in = H;
     la.x = m->pf_x + (size_t)(T - 1) * H;
@@ -995,6 +1071,20 @@ extern "C" int tmg_gemv_bf16(const uint16_t *w, const float *x, float *y, uint32
     if (((uintptr_t)w & 15) || ((uintptr_t)x & 15)) return set_error(TMG_E_INVALID, "W and x must be 16-byte aligned");
     GemvArgs a{};
     a.W = w;
+    a.out = (int)out;
+    a.in = (int)in;
+    a.x = x;
+    a.y = y;
+    TMG_HIP(launch_gemv(PRO_PLAIN, EPI_STORE, a, (hipStream_t)stream));
+    return TMG_OK;
+}
+
+extern "C" int tmg_gemv_f32(const float *w, const float *x, float *y, uint32_t out, uint32_t in, void *stream) {
+    if (!w || !x || !y || out == 0 || in == 0) return set_error(TMG_E_INVALID, "bad argument to tmg_gemv_f32");
+    if (in % 8 != 0 || in > 16384) return set_error(TMG_E_INVALID, "in must be a multiple of 8 and <= 16384");
+    if (((uintptr_t)w & 15) || ((uintptr_t)x & 15)) return set_error(TMG_E_INVALID, "W and x must be 16-byte aligned");
+    GemvArgs a{};
+    a.Wf = w;
     a.out = (int)out;
     a.in = (int)in;
     a.x = x;

@@ -26,6 +26,10 @@ struct tmg_model {
         // (then qkv/o/gu/down above hold the int8 codes as BF16, for prefill)
         int8_t *qkv8 = nullptr, *o8 = nullptr, *gu8 = nullptr, *down8 = nullptr;
         float *qkv_s = nullptr, *o_s = nullptr, *gu_s = nullptr, *down_s = nullptr;
+        // f32 rows in the same order instead of the BF16 ones (WMat::F32: a
+        // matrix whose file tensors are not all BF16, src/model.rs:49-55);
+        // then the BF16 pointer is null
+        float *qkv_f = nullptr, *o_f = nullptr, *gu_f = nullptr, *down_f = nullptr;
     };
     // int8 weight-only mode (TMG_I8=1 at load, reference src/model.rs:57-76)
     bool i8 = false;
@@ -36,6 +40,8 @@ struct tmg_model {
     uint16_t *embed_bf16 = nullptr;  // [V, H] when the file stores BF16
     float *embed_f32 = nullptr;      // [V, H] otherwise (converted like the reference)
     uint16_t *lm_head = nullptr;     // [V, H]; the embedding when tied
+    float *lm_head_f = nullptr;      // f32 lm_head instead (F32/F16 tensor, or tied to an f32 table)
+    bool any_f32 = false;            // some layer matrix or the lm_head has f32 rows
 
     // RoPE cos/sin tables [npos][hd/2], built on the host with libm exactly
     // like the reference's Rope (src/tensor.rs:1005-1023) and uploaded.

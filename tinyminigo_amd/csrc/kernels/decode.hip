@@ -83,6 +83,35 @@ __global__ __launch_bounds__(kBlock) void gemv_i8_kernel(const GemvArgs a) {
     gemv_epilogue<R, EPI, true, true>(a, blockIdx.x, pos, red, pre, xs);
 }
 
+// The same GEMV over f32 rows (GemvArgs::Wf): prologues and epilogues
+// shared with gemv_kernel, two 16-byte weight loads per chunk and row.
+template <int KC, int R, int PRO, int EPI>
+__global__ __launch_bounds__(kBlock) void gemv_f32_kernel(const GemvArgs a) {
+    __shared__ float red[4][R];
+    __shared__ float scratch[4];
+    WeightRegsF<KC, R> W;
+    float xv[KC][8];
+    EpiIn pre{};
+    int pos = 0;
+    if constexpr (PRO == PRO_EMBED_NORM) {
+        gemv_loadf<KC, R>(a, blockIdx.x, W);
+        if constexpr (EPI == EPI_QKV) pos = *a.pos;
+        gemv_embed_prologue<KC>(a, *a.token, xv, scratch, blockIdx.x == 0);
+    } else {
+        ActIn<KC, PRO> in;
+        act_issue<KC, PRO>(a, in);
+        if constexpr (EPI == EPI_RESID) epi_issue_resid<R>(a, blockIdx.x, pre);
+        gemv_loadf<KC, R>(a, blockIdx.x, W);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (EPI == EPI_QKV || PRO == PRO_ATTN_COMBINE) pos = *a.pos;
+        if constexpr (EPI == EPI_QKV) epi_load_rope<R>(a, blockIdx.x, pos, pre);
+        act_finish<KC, PRO>(a, pos, in, xv, scratch);
+    }
+    gemv_dotf<KC, R>(a, W, xv, red);
+    __syncthreads();
+    gemv_epilogue<R, EPI, PRO != PRO_EMBED_NORM, false>(a, blockIdx.x, pos, red, pre, 0.0f);
+}
+
 template <int KC, int PRO, int EPI>
 hipError_t launch_kc(const GemvArgs &a, hipStream_t s) {
     // the split-merge prologue re-reads every split's partials per
@@ -91,7 +120,17 @@ hipError_t launch_kc(const GemvArgs &a, hipStream_t s) {
     // 2048 slower (1B 4.3 -> 4.6 us)
     constexpr int R = (PRO == PRO_ATTN_COMBINE && KC == 2) ? 16 : gemv_rows<KC>();
     const int grid = (a.out + R - 1) / R;
-    if (a.W8) {
+    if (!a.W8 && a.Wf) {
+        // (the split-merge prologue is fused only over attention outputs of
+        // at most 4096, i.e. two chunks)
+        if constexpr (PRO == PRO_ATTN_COMBINE && KC > 2) {
+            return hipErrorInvalidValue;
+        } else {
+            constexpr int RF = gemv_rows_f32<KC>();
+            hipLaunchKernelGGL((gemv_f32_kernel<KC, RF, PRO, EPI>), dim3((a.out + RF - 1) / RF), dim3(kBlock), 0, s,
+                               a);
+        }
+    } else if (a.W8) {
         if constexpr (EPI == EPI_LOGITS || PRO == PRO_NORM_BATCH) {
             return hipErrorInvalidValue;  // lm_head keeps BF16 rows
         } else {
@@ -218,6 +257,41 @@ __global__ __launch_bounds__(kBlock) void quantize_i8_kernel(uint16_t *w, int in
         }
         *reinterpret_cast<uint2 *>(qr + k) = make_uint2(packed[0], packed[1]);
         if (rewrite) *reinterpret_cast<uint4 *>(wr + k) = make_uint4(codes[0], codes[1], codes[2], codes[3]);
+    }
+    if (threadIdx.x == 0) scale[row] = sc;
+}
+
+// quantize_i8 of f32 rows, one workgroup per row: the same steps as
+// quantize_i8_kernel on the row's f32 values; the codes also go to `codes`
+// as BF16 (exact, |q| <= 127).
+__global__ __launch_bounds__(kBlock) void quantize_i8_f32_kernel(const float *w, int in, int8_t *q8, float *scale,
+                                                                 uint16_t *codes) {
+    __shared__ float scratch[4];
+    const int row = blockIdx.x;
+    const float *wr = w + (size_t)row * in;
+    int8_t *qr = q8 + (size_t)row * in;
+    uint16_t *cr = codes + (size_t)row * in;
+    float m[1] = {0.0f};
+    for (int k = threadIdx.x * 8; k < in; k += kBlock * 8) {
+        const float4 a = *reinterpret_cast<const float4 *>(wr + k), b = *reinterpret_cast<const float4 *>(wr + k + 4);
+        m[0] = fmaxf(m[0], fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+        m[0] = fmaxf(m[0], fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+    }
+    block_max_n<1>(m, scratch);
+    const float sc = m[0] > 0.0f ? __fdiv_rn(m[0], 127.0f) : 1.0f;
+    for (int k = threadIdx.x * 8; k < in; k += kBlock * 8) {
+        const float4 a = *reinterpret_cast<const float4 *>(wr + k), b = *reinterpret_cast<const float4 *>(wr + k + 4);
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint32_t packed[2] = {0u, 0u}, cw[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float r = roundf(__fdiv_rn(v[j], sc));
+            const int q = r == r ? (int)fminf(fmaxf(r, -127.0f), 127.0f) : 0;
+            packed[j >> 2] |= ((uint32_t)q & 0xffu) << (8 * (j & 3));
+            cw[j >> 1] |= (uint32_t)f32_to_bf16_rne((float)q) << (16 * (j & 1));
+        }
+        *reinterpret_cast<uint2 *>(qr + k) = make_uint2(packed[0], packed[1]);
+        *reinterpret_cast<uint4 *>(cr + k) = make_uint4(cw[0], cw[1], cw[2], cw[3]);
     }
     if (threadIdx.x == 0) scale[row] = sc;
 }
@@ -514,6 +588,13 @@ hipError_t launch_quantize_i8(uint16_t *w, int rows, int in, int8_t *q8, float *
     return hipGetLastError();
 }
 
+hipError_t launch_quantize_i8_f32(const float *w, int rows, int in, int8_t *q8, float *scale, uint16_t *codes,
+                                  hipStream_t s) {
+    if (rows <= 0 || in <= 0 || in % 8) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(quantize_i8_f32_kernel, dim3(rows), dim3(kBlock), 0, s, w, in, q8, scale, codes);
+    return hipGetLastError();
+}
+
 hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {
     const bool spec = a.pos_dev && a.cap > 0 && a.T == 1;
     switch (a.hd) {
@@ -532,9 +613,10 @@ hipError_t launch_attn_combine(const AttnArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-int gemv_blocks(int out, int in) {
+int gemv_blocks(int out, int in, bool f32) {
     const int kc = (in + kChunk - 1) / kChunk;
-    const int R = kc <= 3 ? 8 : 4;  // gemv_rows<KC>()
+    const int R = f32 ? (kc <= 1 ? 8 : kc <= 3 ? 4 : 2)  // gemv_rows_f32<KC>()
+                      : (kc <= 3 ? 8 : 4);                // gemv_rows<KC>()
     return (out + R - 1) / R;
 }
 

@@ -314,6 +314,73 @@ __device__ __forceinline__ void gemv_finish(const GemvArgs &a, int blk, int pos,
 }
 
 // ---------------------------------------------------------------------------
+// f32 rows (WMat::F32: F32 or F16 weight matrices converted to f32 at load,
+// reference src/model.rs:49-55; dot_f32_avx2, src/tensor.rs:58-74).  Same
+// element mapping as the BF16 rows -- thread t takes elements c*2048 + 8t ..
+// +7 of every row -- as two 16-byte loads; fewer rows per workgroup, as each
+// row holds twice the registers.
+// ---------------------------------------------------------------------------
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+template <int KC>
+__host__ __device__ constexpr int gemv_rows_f32() {
+    return KC <= 1 ? 8 : KC <= 3 ? 4 : 2;
+}
+
+template <int KC, int R>
+struct WeightRegsF {
+    f32x4v w[R][KC][2];
+};
+
+template <int KC, int R>
+__device__ __forceinline__ void gemv_loadf(const GemvArgs &a, int blk, WeightRegsF<KC, R> &W) {
+    const int t = threadIdx.x;
+    const int row0 = blk * R;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int row = min(row0 + r, a.out - 1);
+        const f32x4v *wr = reinterpret_cast<const f32x4v *>(a.Wf + (size_t)row * a.in);
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            // clamped like gemv_load; gemv_dotf zeroes the chunks past the row end
+            const int k = min(c * kChunk + t * 8, a.in - 8) >> 2;
+            W.w[r][c][0] = __builtin_nontemporal_load(wr + k);
+            W.w[r][c][1] = __builtin_nontemporal_load(wr + k + 1);
+        }
+    }
+}
+
+template <int KC, int R>
+__device__ __forceinline__ void gemv_dotf(const GemvArgs &a, const WeightRegsF<KC, R> &W, const float (&xv)[KC][8],
+                                          float (*red)[R]) {
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int c = 0; c < KC; c++) {
+            f32x4v u0 = W.w[r][c][0], u1 = W.w[r][c][1];
+            if ((c + 1) * kChunk > a.in && c * kChunk + t * 8 >= a.in) u0 = u1 = f32x4v{0.f, 0.f, 0.f, 0.f};
+            s0 = fmaf(xv[c][0], u0.x, s0);
+            s1 = fmaf(xv[c][1], u0.y, s1);
+            s0 = fmaf(xv[c][2], u0.z, s0);
+            s1 = fmaf(xv[c][3], u0.w, s1);
+            s0 = fmaf(xv[c][4], u1.x, s0);
+            s1 = fmaf(xv[c][5], u1.y, s1);
+            s0 = fmaf(xv[c][6], u1.z, s0);
+            s1 = fmaf(xv[c][7], u1.w, s1);
+        }
+        acc[r] = s0 + s1;
+    }
+    constexpr int LR = R == 16 ? 4 : R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
+    const float sum = multi_wave_sum<R>(acc, lane);
+    if ((lane & ((64 >> LR) - 1)) == 0) red[wave][lane >> (6 - LR)] = sum;
+}
+
+// ---------------------------------------------------------------------------
 // int8 rows (the TMG_I8 weight-only mode, reference src/model.rs:57-76):
 // W8 [out, in] int8 with one f32 scale per row.  Same element mapping as the
 // BF16 rows -- thread t takes elements c*2048 + 8t .. +7 of every row -- with

@@ -38,6 +38,9 @@ struct GemvArgs {
     // scales, same row order as W; null selects the BF16 rows
     const int8_t *W8;
     const float *wscale;
+    // f32 rows instead (WMat::F32: F32 / F16 matrices converted at load),
+    // same row order as W; used when set and W8 is null
+    const float *Wf;
     int out, in;
     const float *x;       // activation (PRO_PLAIN) or residual stream (PRO_NORM*)
     const float *norm_w;  // [in] f32 RMSNorm weight
@@ -92,8 +95,13 @@ int gemv_mt_blocks(int out, int in, int nb);
 // dequantized weight up to the row scale, for the prefill GEMMs.
 hipError_t launch_quantize_i8(uint16_t *w, int rows, int in, int8_t *q8, float *scale, bool rewrite,
                               hipStream_t s);
-// Workgroups (= argmax partials) of a GEMV launch with `out` rows of `in`.
-int gemv_blocks(int out, int in);
+// The same from f32 rows (quantize_i8 of WMat::F32 values, src/model.rs:69-72):
+// q8 codes, scales, and the codes as BF16 in `codes` [rows, in].
+hipError_t launch_quantize_i8_f32(const float *w, int rows, int in, int8_t *q8, float *scale, uint16_t *codes,
+                                  hipStream_t s);
+// Workgroups (= argmax partials) of a GEMV launch with `out` rows of `in`
+// (BF16 rows, or f32 rows with f32).
+int gemv_blocks(int out, int in, bool f32 = false);
 
 struct AttnArgs {
     const float *q;  // [T][nq*hd], RoPE applied
@@ -192,6 +200,7 @@ enum GemmEpi { GEPI_STORE = 0, GEPI_RESID = 1, GEPI_SWIGLU = 2, GEPI_QKV = 3 };
 
 struct GemmArgs {
     const uint16_t *W;  // [M, K] BF16
+    const float *Wf;    // [M, K] f32 weights instead (WMat::F32), or null
     const float *wscale;  // [M] row scales applied before the epilogue (int8 weights held as BF16 codes), or null
     const uint16_t *Bhi, *Blo;  // [N, K] split-bf16 activations
     int M, N, K;

@@ -460,6 +460,60 @@ __global__ __launch_bounds__(kBlock) void gemm_kernel(const GemmArgs a) {
     gemm_store<EPI>(a, mb, n, v);
 }
 
+// The same product over f32 weights (WMat::F32; matmul_batch_w_into's F32
+// arm, src/tensor.rs:573-760) on the fp32 MFMA v_mfma_f32_16x16x4_f32, whose
+// output layout is the bf16 one's: lane l supplies A row (l & 15) and B
+// column (l & 15) at k = l >> 4 and receives D rows 4 (l >> 4) .. +3 of
+// column (l & 15).  The activation is hi + lo, exact in f32.  Each lane
+// loads 4 consecutive k of its weight row and of its token (16 and 2 x 8
+// bytes), which serve 4 MFMAs: MFMA j takes the j-th of them from every lane,
+// the same k set on both operands.  Workgroup tile 16 rows x 64 tokens, the
+// four wavefronts on interleaved 16-wide K blocks, summed through LDS.
+template <int EPI>
+__global__ __launch_bounds__(kBlock) void gemm_f32w_kernel(const GemmArgs a) {
+    constexpr int NB = 4;  // 16-token column blocks per workgroup
+    __shared__ f32x4 s_acc[4][NB][64];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int m0 = blockIdx.x * 16, n0 = blockIdx.y * 16 * NB;
+    const int K = a.K;
+    const int r = lane & 15, kq = (lane >> 4) * 4;
+    const float *Ap = a.Wf + (size_t)min(m0 + r, a.M - 1) * K + kq;
+    const uint16_t *Bh[NB], *Bl[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+        const int n = min(n0 + nb * 16 + r, a.N - 1);
+        Bh[nb] = a.Bhi + (size_t)n * K + kq;
+        Bl[nb] = a.Blo + (size_t)n * K + kq;
+    }
+    f32x4 acc[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k = wave * 16; k < K; k += 64) {
+        const f32x4 av = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(Ap + k));
+        u32x2 bh[NB], bl[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+            bh[nb] = *reinterpret_cast<const u32x2 *>(Bh[nb] + k);
+            bl[nb] = *reinterpret_cast<const u32x2 *>(Bl[nb] + k);
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) {
+            const float x[4] = {bf16_lo(bh[nb].x) + bf16_lo(bl[nb].x), bf16_hi(bh[nb].x) + bf16_hi(bl[nb].x),
+                                bf16_lo(bh[nb].y) + bf16_lo(bl[nb].y), bf16_hi(bh[nb].y) + bf16_hi(bl[nb].y)};
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j], x[j], acc[nb], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) s_acc[wave][nb][lane] = acc[nb];
+    __syncthreads();
+    const int nb = wave;
+    const f32x4 v = (s_acc[0][nb][lane] + s_acc[1][nb][lane]) + (s_acc[2][nb][lane] + s_acc[3][nb][lane]);
+    const int n = n0 + nb * 16 + (lane & 15);
+    const int mb = m0 + (lane >> 4) * 4;  // rows mb .. mb+3
+    gemm_store<EPI>(a, mb, n, v);
+}
+
 // Tiled MFMA GEMM for prompts of at least kTiledMinTokens tokens: workgroup
 // tile 128 weight rows x 128 tokens, K in steps of 64; each of the four
 // wavefronts owns a 64 x 64 quarter (4 x 4 MFMA fragments).
@@ -964,6 +1018,19 @@ bool gemm_stages_output(int M, int N, int K) {
 
 hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
     if (a.K % 32 != 0 || a.M <= 0 || a.N <= 0) return hipErrorInvalidValue;
+    if (a.Wf) {
+        // f32 weights: the per-element epilogue only (no norm hand-off, no row scales)
+        if (a.nrm_w || a.nss_in || a.wscale) return hipErrorInvalidValue;
+        const dim3 grid((a.M + 15) / 16, (a.N + 63) / 64);
+        switch (epi) {
+            case GEPI_STORE: hipLaunchKernelGGL(gemm_f32w_kernel<GEPI_STORE>, grid, dim3(kBlock), 0, s, a); break;
+            case GEPI_RESID: hipLaunchKernelGGL(gemm_f32w_kernel<GEPI_RESID>, grid, dim3(kBlock), 0, s, a); break;
+            case GEPI_SWIGLU: hipLaunchKernelGGL(gemm_f32w_kernel<GEPI_SWIGLU>, grid, dim3(kBlock), 0, s, a); break;
+            case GEPI_QKV: hipLaunchKernelGGL(gemm_f32w_kernel<GEPI_QKV>, grid, dim3(kBlock), 0, s, a); break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     if ((a.nrm_w || a.nss_in) && !gemm_stages_output(a.M, a.N, a.K)) return hipErrorInvalidValue;
     if (a.nrm_w && (epi != GEPI_RESID || a.M % 64 != 0 || !a.nss || !a.nx_hi || !a.nx_lo)) return hipErrorInvalidValue;
     if (a.nss_in && (a.ngroups <= 0 || a.ngroups > kMaxNormGroups || a.ngroups % 4)) return hipErrorInvalidValue;

@@ -275,6 +275,13 @@ def gemv_bf16(w_dev: int, x_dev: int, y_dev: int, out: int, in_: int, stream: in
                             C.c_void_p(stream)))
 
 
+def gemv_f32(w_dev: int, x_dev: int, y_dev: int, out: int, in_: int, stream: int = 0) -> None:
+    """tensor::matmul_w over a WMat::F32 matrix (src/tensor.rs:387-420) on
+    device pointers."""
+    check(lib.tmg_gemv_f32(C.c_void_p(w_dev), C.c_void_p(x_dev), C.c_void_p(y_dev), out, in_,
+                           C.c_void_p(stream)))
+
+
 def argmax_f32(x_dev: int, n: int, out_dev: int, stream: int = 0) -> None:
     """tensor::argmax (src/tensor.rs:1063-1073) of n device floats into a
     device uint32."""
