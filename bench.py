@@ -105,6 +105,10 @@ C1_SHAPES = [(2048, 2048), (6144, 2048), (2048, 6144), (73448, 2048)]
 MALL_BYTES = 256 << 20  # MI355X last-level (Infinity) cache
 
 
+# workgroup sizes (KiB per workgroup) the streaming floor is taken over
+STREAM_WG_KIB = (8, 12, 16, 24, 32, 48, 64, 96)
+
+
 def gemv_sweep(T):
     """matmul_w (src/tensor.rs:315-338) at the decode GEMV shapes through the
     kernel-level entry point tmg_gemv_bf16.  W BF16 N(0, 0.02) and x N(0, 1)
@@ -112,7 +116,9 @@ def gemv_sweep(T):
     copies of W (>= 1 GiB) that none is still in the last-level cache;
     MALL-hot: the same number of launches on one copy.  Bytes per launch =
     2*out*in + 4*in + 4*out; each figure is the per-launch average over
-    graph replays (HIP events on the launch stream)."""
+    graph replays (HIP events on the launch stream).  Beside each shape, the
+    streaming floor of its weight bytes (tmg_profile_stream, the best of
+    STREAM_WG_KIB)."""
     import numpy as np
 
     from tinyminigo_amd import hip as H
@@ -153,10 +159,16 @@ def gemv_sweep(T):
             row[f"{kind}_us"] = round(us, 3)
             row[f"{kind}_GB_s"] = round(nbytes / (us * 1e-6) / 1e9, 1)
             del g
-        res.append(row)
         del ws, w0, xd, yd
+        # the floor: a kernel that only streams the same weight bytes,
+        # HBM-cold, at the best of several workgroup sizes
+        fl = min((T.profile_stream(wbytes, kib)[0], kib) for kib in STREAM_WG_KIB)
+        row["stream_floor_us"], row["stream_floor_wg_kib"] = round(fl[0], 3), fl[1]
+        row["cold_above_floor_us"] = round(row["cold_us"] - fl[0], 3)
+        res.append(row)
         log(f"gemv {out}x{inp}: cold {row['cold_us']} us ({row['cold_GB_s']} GB/s), "
-            f"hot {row['hot_us']} us ({row['hot_GB_s']} GB/s), max abs err vs oracle {row['max_abs_err']:.2e}")
+            f"hot {row['hot_us']} us ({row['hot_GB_s']} GB/s), streaming floor {fl[0]:.3f} us, "
+            f"max abs err vs oracle {row['max_abs_err']:.2e}")
     return res
 
 
@@ -164,19 +176,37 @@ TRAFFIC_FILES = {w: os.path.join(os.path.dirname(os.path.abspath(__file__)), "pr
                  for w, f in (("bf16", "decode_1b_gemv_traffic.md"), ("i8", "decode_1b_i8_gemv_traffic.md"))}
 
 
-def pmc_traffic(kernel, weights="bf16"):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
-    summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known size);
-    None when the summary has no line for it."""
+def summary_line(path, tag, kernel):
+    """The `tag: kernel=... key=value ...` line of a committed profile summary
+    for `kernel`, as a dict, or None."""
     try:
-        for line in open(TRAFFIC_FILES[weights]):
-            if line.startswith("traffic-bytes-per-launch:"):
+        for line in open(path):
+            if line.startswith(tag + ":"):
                 f = dict(kv.split("=", 1) for kv in line.split(":", 1)[1].split())
                 if f.get("kernel") == kernel:
-                    return int(f["bytes"])
+                    return f
     except OSError:
         pass
     return None
+
+
+def pmc_traffic(kernel, weights="bf16"):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel of known size)
+    and the commit of the tree it was measured on; (None, None) when the
+    summary has no line for it."""
+    f = summary_line(TRAFFIC_FILES[weights], "traffic-bytes-per-launch", kernel)
+    return (int(f["bytes"]), f.get("tree")) if f else (None, None)
+
+
+STATS_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_1b_kernel_stats.md")
+
+
+def rocprof_avg(kernel):
+    """The rocprofv3 --kernel-trace --stats average duration (us) of `kernel`
+    in the committed 1B decode summary, and its tree; (None, None) if absent."""
+    f = summary_line(STATS_FILE, "rocprof-avg-us", kernel)
+    return (float(f["us"]), f.get("tree")) if f else (None, None)
 
 
 SAMPLED = dict(temperature=0.8, top_k=50, top_p=0.9, repetition_penalty=1.1, seed=42)
@@ -191,6 +221,29 @@ def kernel_table(m, cache, tok, reps=3):
         for name, nbytes, ms, launches in m.profile_decode_step(tok, cache):
             per.setdefault(name, [launches, nbytes, []])[2].append(ms)
     return {k: (v[0], v[1], float(np.median(v[2]))) for k, v in per.items()}
+
+
+def step_floor(m, tok, cache, per, step_bytes):
+    """tmg_profile_step_floor at the cache's position: the greedy step
+    replayed from its graph, and the same launch chain with every kernel
+    replaced by a streaming phase of its grid and bytes (weights and one
+    dependent activation load, nothing else).  Per kind: the real kernel's
+    graph-replay time (tmg_profile_decode_step, `per`) beside its phase's."""
+    f = m.profile_step_floor(tok, cache)
+    kinds = {}
+    for name, nbytes, fbytes, fms, launches, nwg in f["kinds"]:
+        real = per.get(name)
+        kinds[name] = {"launches": launches, "workgroups": nwg, "bytes": nbytes, "phase_bytes": fbytes,
+                       "phase_us": round(fms * 1e3, 3), "real_us": round(real[2] * 1e3, 3) if real else None,
+                       "above_phase_us": round((real[2] - fms) * 1e3, 3) if real else None}
+    step_us, floor_us = f["step_ms"] * 1e3, f["floor_ms"] * 1e3
+    log(f"step floor: step {step_us:.1f} us, streaming chain {floor_us:.1f} us, empty launch "
+        f"{f['empty_launch_ms'] * 1e3:.3f} us")
+    return {"step_us": round(step_us, 2), "floor_us": round(floor_us, 2),
+            "empty_launch_us": round(f["empty_launch_ms"] * 1e3, 3),
+            "step_hbm_frac": round(step_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "floor_hbm_frac": round(step_bytes / (floor_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "kinds": kinds}
 
 
 def extra_long_context(T, W, m, sync):
@@ -244,6 +297,21 @@ def extra_long_context(T, W, m, sync):
     }
 
 
+def generate_setup_secs(T, m, prompt, samp, sync, reps=5):
+    """Median time generate spends outside its prefill when it produces no
+    token: the KV cache's allocation, the sampling state's upload, the step
+    graph's capture and the cache's release (max_tokens = 0 returns right
+    after the prefill)."""
+    import numpy as np
+    out = []
+    for _ in range(reps):
+        sync()
+        t = time.perf_counter()
+        g = T.generate(m, prompt, T.GenParams(max_tokens=0, **samp))
+        out.append(time.perf_counter() - t - g.prefill_secs)
+    return float(np.median(out))
+
+
 def extra_four_b(T, W, model_dir, sync):
     """The 4B sampled workload (C4): 128-token prompt, 256 tokens with
     T=0.8, top-k 50, top-p 0.9, penalty 1.1, seed 42 through generate (the
@@ -256,6 +324,7 @@ def extra_four_b(T, W, model_dir, sync):
     K = wl.gen_tokens
     T.generate(m, prompt, T.GenParams(max_tokens=16, **SAMPLED))
     sync()
+    setup_s = generate_setup_secs(T, m, prompt, SAMPLED, sync)
     t = time.perf_counter()
     gen = T.generate(m, prompt, T.GenParams(max_tokens=K, **SAMPLED))
     wall_all = time.perf_counter() - t
@@ -271,6 +340,10 @@ def extra_four_b(T, W, model_dir, sync):
                     f"penalty 1.1, seed 42) through generate",
         "ms_per_token": round(ms_tok, 4), "tok_s": round(n / wall, 1),
         "prefill_ms": round(gen.prefill_secs * 1e3, 2),
+        # the decode window holds the call's set-up (KV cache allocation, the
+        # step graph's capture), as the reference's elapsed holds its own;
+        # measured alone, and the rate without it
+        "setup_ms": round(setup_s * 1e3, 3), "tok_s_excl_setup": round(n / (wall - setup_s), 1),
         "step_hbm": {"bytes_per_token": step_bytes, "n_ctx_avg": n_ctx,
                      "frac": round(step_bytes / (ms_tok * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
     }
@@ -351,6 +424,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true", help="skip the GEMV shape sweep")
+    ap.add_argument("--no-floor", action="store_true",
+                    help="skip the step-floor measurement (tmg_profile_step_floor)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time only the prefill of the workload's prompt (no decode, no graph launches)")
     ap.add_argument("--no-extras", action="store_true",
@@ -451,14 +526,15 @@ def main():
     prefill_s = float(np.median(pf))
     log(f"prefill {P} tokens: {prefill_s * 1e3:.2f} ms")
 
-    cap = P + max(K, Wm) + args.profile_steps + 8
-    gen = None
+    cap = P + max(K, Wm) + args.profile_steps + 18  # + the step-floor replays
+    gen, setup_s = None, None
     if sampled:
         # the product path: generate (prefill, device sampling, one id per
         # step to the host); decode tok/s as the reference's main.rs reports
         # it, (n - 1) / (elapsed - prefill)
         T.generate(m, prompt, T.GenParams(max_tokens=Wm, **samp))
         sync()
+        setup_s = generate_setup_secs(T, m, prompt, samp, sync)
         t = time.perf_counter()
         gen = T.generate(m, prompt, T.GenParams(max_tokens=K, **samp))
         wall_all = time.perf_counter() - t
@@ -466,7 +542,7 @@ def main():
         K_timed = len(gen.tokens) - 1
         ev_ms = None
         log(f"generate {len(gen.tokens)} sampled tokens: {wall_all * 1e3:.1f} ms incl. prefill "
-            f"{gen.prefill_secs * 1e3:.1f} ms -> {K_timed / wall:.1f} tok/s")
+            f"{gen.prefill_secs * 1e3:.1f} ms and set-up {setup_s * 1e3:.2f} ms -> {K_timed / wall:.1f} tok/s")
         cache = T.KvCache(m, cap)
         logits = m.forward_seq(prompt, cache)
         toks = [int(np.argmax(logits))]
@@ -507,12 +583,19 @@ def main():
     kernels = {k: {"launches": n, "avg_us": round(ms * 1e3, 2),
                    "GB_s": round(b / (ms * 1e-3) / 1e9, 1) if b else None,
                    "share": round(n * ms / step_kern_ms, 3)} for k, (n, b, ms) in per.items()}
-    traffic = pmc_traffic(name, args.weights) if args.workload == "1b" else None
+    traffic, traffic_tree = pmc_traffic(name, args.weights) if args.workload == "1b" else (None, None)
+    rp_us, rp_tree = rocprof_avg(name) if args.workload == "1b" and not i8 else (None, None)
 
     sweep = None if (args.no_sweep or args.workload != "1b" or i8) else gemv_sweep(T)
 
+    # the step next to its floor (graph replays; skipped when the step's
+    # kernels are launched one by one, as under the profiler)
+    floor = None
+    if args.workload == "1b" and not i8 and not args.no_floor and os.environ.get("TMG_DECODE_GRAPH", "1") != "0":
+        floor = step_floor(m, tok, cache, per, step_bytes)
+
     # the other two model workloads, reported beside the headline (1b line only)
-    extras = {}
+    extras = {} if setup_s is None else {"generate_setup_ms": round(setup_s * 1e3, 3)}
     if args.workload == "1b" and not i8 and not sampled and not args.no_extras:
         extras["c3_long_context"] = extra_long_context(T, W, m, sync)
 
@@ -564,8 +647,13 @@ def main():
         "roofline": {"bound": "hbm", "kernel": name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_per_launch": nbytes, "avg_launch_us": round(kern_ms * 1e3, 3),
-                     "launches_per_step": n_launch},
+                     "launches_per_step": n_launch, "traffic_tree": traffic_tree,
+                     # the same kernel's rocprofv3 average (eager launches) in the
+                     # committed summary, and the fraction of peak it gives
+                     "rocprof_avg_us": rp_us, "rocprof_tree": rp_tree,
+                     "frac_rocprof": round(nbytes / (rp_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if rp_us else None},
         "kernels": kernels,
+        "step_floor": floor,
         "gemv_sweep": sweep,
         **extras,
         "cpu_baseline": cpu,

@@ -80,14 +80,17 @@ int tmg_config_load(const char *config_json_path, tmg_config *out);
 
 /* Model::load (reference src/model.rs:384-389 -> load_model_safetensors,
  * src/model.rs:181-244): config.json must sit next to the .safetensors file
- * (src/config.rs:174-184).  Weight matrices must be BF16; they are uploaded
- * raw to HBM on `device`.  Norm weights and the embedding may be BF16, F16 or
- * F32 (converted as in src/safetensors_loader.rs:103-147).  With TMG_I8=1 in
- * the environment (the reference's gate, src/model.rs:57-76) the q, k, v, o,
- * gate, up and down projections are quantized to per-row int8 at load
- * (tmg_quantize_i8): decode steps stream the int8 rows (tmg_gemv_i8's
- * arithmetic), prefill multiplies by the same codes, dequantized, in f32
- * (src/tensor.rs:795-858); lm_head stays BF16. */
+ * (src/config.rs:174-184).  BF16 weight matrices are uploaded raw to HBM on
+ * `device`; F16 and F32 ones are widened to f32 rows (WMat::F32,
+ * src/model.rs:49-55) and multiplied as f32 (tmg_gemv_f32's arithmetic in
+ * decode, an fp32 GEMM in prefill).  Norm weights and the embedding may be
+ * BF16, F16 or F32 (converted as in src/safetensors_loader.rs:103-147).  With
+ * TMG_I8=1 in the environment (the reference's gate, src/model.rs:57-76) the
+ * q, k, v, o, gate, up and down projections are quantized to per-row int8 at
+ * load (tmg_quantize_i8, from the f32 values for F16/F32 matrices): decode
+ * steps stream the int8 rows (tmg_gemv_i8's arithmetic), prefill multiplies
+ * by the same codes, dequantized, in f32 (src/tensor.rs:795-858); lm_head is
+ * not quantized. */
 int tmg_model_load(const char *safetensors_path, int device, tmg_model **out);
 
 /* A TMB1 file (reference src/tmb.rs) is accepted by tmg_model_load too: a
@@ -254,6 +257,42 @@ typedef struct tmg_kernel_record {
  * No counterpart in the reference (measurement only). */
 int tmg_profile_decode_step(tmg_model *model, tmg_cache *cache, uint32_t token, tmg_kernel_record *records,
                             size_t cap, size_t *n_records);
+
+typedef struct tmg_floor_record {
+    char name[48];       /* kernel kind of the step */
+    double bytes;        /* algorithmic HBM bytes of one launch of that kind */
+    double floor_bytes;  /* bytes one streaming phase in its place reads */
+    float floor_ms;      /* average duration of one such phase */
+    uint32_t launches;   /* launches of this kind in one decode step */
+    uint32_t workgroups; /* grid of the kind's launch, and of its phase */
+} tmg_floor_record;
+
+/* The decode step next to its floor, at the cache's current position.  The
+ * greedy step is captured as the decode loop captures it and replayed as
+ * consecutive steps (*step_ms per step).  Every launch of it is then replaced
+ * by a streaming phase with the same grid that reads the launch's
+ * algorithmic bytes (to whole 4-KiB blocks per workgroup, all in flight at
+ * once) from a slab of its own (larger than the last-level cache) and dots
+ * them with the previous phase's output: the step's launch chain and weight
+ * stream with none of its other work.  *floor_ms is that
+ * chain per replay, one record per kind gives its phases back to back, and
+ * *empty_ms is one empty 256-workgroup launch in a graph.  Needs 9 free
+ * cache rows past the length; leaves the cache as it was.  Allocates the
+ * slab (about the step's bytes) for the call.  No counterpart in the
+ * reference (measurement only). */
+int tmg_profile_step_floor(tmg_model *model, tmg_cache *cache, uint32_t token, tmg_floor_record *records,
+                           size_t cap, size_t *n_records, float *step_ms, float *floor_ms, float *empty_ms);
+
+/* The streaming rate of the device: *us per launch of a kernel that streams
+ * `bytes` (rounded up to whole workgroups; *bytes_read) of HBM-cold data as
+ * workgroups of 256 threads reading wg_kib KiB each (a multiple of 4 in
+ * [4, 128]), all of a workgroup's loads in flight at once, dotted with a
+ * constant activation, one store per workgroup.  Launches replayed back to
+ * back from a graph that rotates over more than 1 GiB of copies, timed by
+ * HIP events on a stream of its own.  The floor a GEMV of that many weight
+ * bytes can reach.  Allocates about 1 GiB for the call.  No counterpart in
+ * the reference (measurement only). */
+int tmg_profile_stream(size_t bytes, uint32_t wg_kib, int device, float *us, size_t *bytes_read);
 
 #ifdef __cplusplus
 }

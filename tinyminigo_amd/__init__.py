@@ -7,11 +7,12 @@ prefill.  This package binds it with ctypes behind the reference's model API.
 """
 from ._lib import TmgError, lib
 from .model import (
-    GenOutput, GenParams, KvCache, Model, ModelConfig, argmax_f32, gemv_bf16, gemv_f32, gemv_i8, generate, generate_batch, quantize_i8, repack_tmb, stdrng_uniform, synth_model,
-    synth_normal_bf16, synth_normal_f32, synth_tokens,
+    GenOutput, GenParams, KvCache, Model, ModelConfig, argmax_f32, gemv_bf16, gemv_f32, gemv_i8, generate,
+    generate_batch, profile_stream, quantize_i8, repack_tmb, stdrng_uniform, synth_model, synth_normal_bf16,
+    synth_normal_f32, synth_tokens,
 )
 
 __all__ = [
     "TmgError", "lib", "argmax_f32", "GenOutput", "GenParams", "KvCache", "Model", "ModelConfig", "gemv_bf16", "gemv_f32", "gemv_i8",
-    "generate", "generate_batch", "quantize_i8", "repack_tmb", "stdrng_uniform", "synth_model", "synth_normal_bf16", "synth_normal_f32", "synth_tokens",
+    "generate", "generate_batch", "profile_stream", "quantize_i8", "repack_tmb", "stdrng_uniform", "synth_model", "synth_normal_bf16", "synth_normal_f32", "synth_tokens",
 ]

@@ -71,6 +71,11 @@ class tmg_kernel_record(C.Structure):
     _fields_ = [("name", C.c_char * 48), ("bytes", C.c_double), ("ms", C.c_float), ("launches", C.c_uint32)]
 
 
+class tmg_floor_record(C.Structure):
+    _fields_ = [("name", C.c_char * 48), ("bytes", C.c_double), ("floor_bytes", C.c_double), ("floor_ms", C.c_float),
+                ("launches", C.c_uint32), ("workgroups", C.c_uint32)]
+
+
 class tmg_synth_spec(C.Structure):
     _fields_ = [
         ("hidden_size", C.c_uint32),
@@ -129,6 +134,9 @@ SIGNATURES = {
     "tmg_decode_greedy": (C.c_int, [P, P, C.c_uint32, C.c_uint32, PU32, PF]),
     "tmg_profile_decode_step": (
         C.c_int, [P, P, C.c_uint32, C.POINTER(tmg_kernel_record), C.c_size_t, C.POINTER(C.c_size_t)]),
+    "tmg_profile_step_floor": (
+        C.c_int, [P, P, C.c_uint32, C.POINTER(tmg_floor_record), C.c_size_t, C.POINTER(C.c_size_t), PF, PF, PF]),
+    "tmg_profile_stream": (C.c_int, [C.c_size_t, C.c_uint32, C.c_int, PF, C.POINTER(C.c_size_t)]),
     "tmg_synth_model": (C.c_int, [C.c_char_p, C.POINTER(tmg_synth_spec)]),
     "tmg_synth_tokens": (C.c_int, [C.c_uint64, C.c_size_t, C.c_uint32, PU32]),
     "tmg_synth_normal_bf16": (C.c_int, [C.c_uint64, C.c_char_p, C.c_size_t, C.c_float, PU16]),

@@ -259,6 +259,17 @@ inline size_t skinny_counters(int max_m) { return (size_t)((max_m + 63) / 64) * 
 // Copy row `row` of x[T,H] to dst[H] (last prefill row -> decode residual).
 hipError_t launch_copy_row(const float *x, int row, int H, float *dst, hipStream_t s);
 
+// ---- step floor (measurement only) ------------------------------------------
+
+// One streaming phase: nwg workgroups of 256 threads, each reading
+// nchunk x nb (1..32) 4-KiB blocks of w from w + b * nchunk * nb * 4 KiB and
+// dotting them with act[0..2047] (the previous phase's output); out[b] per
+// workgroup (out holds at least max(nwg, 2048) floats).
+hipError_t launch_stream_phase(const void *w, int nwg, int nb, int nchunk, const float *act, float *out,
+                               hipStream_t s);
+// nwg workgroups of 256 threads that do nothing.
+hipError_t launch_empty(int nwg, hipStream_t s);
+
 // ---- decode attention -------------------------------------------------------
 
 // Decode attention with at most this many splits is merged in the o_proj

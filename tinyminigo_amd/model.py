@@ -17,13 +17,13 @@ import numpy as np
 import weakref
 
 from ._lib import (
-    ON_TOKEN, TmgError, check, finalizing, lib, register, tmg_config, tmg_gen_params, tmg_kernel_record,
-    tmg_synth_spec,
+    ON_TOKEN, TmgError, check, finalizing, lib, register, tmg_config, tmg_floor_record, tmg_gen_params,
+    tmg_kernel_record, tmg_synth_spec,
 )
 
 __all__ = [
     "ModelConfig", "Model", "KvCache", "GenParams", "GenOutput", "generate", "gemv_bf16", "gemv_i8", "quantize_i8", "repack_tmb",
-    "argmax_f32",
+    "argmax_f32", "profile_stream",
     "generate_batch",
     "synth_model", "synth_tokens", "synth_normal_bf16", "synth_normal_f32", "TmgError",
 ]
@@ -157,6 +157,21 @@ class Model:
         check(lib.tmg_profile_decode_step(self._h, cache._h, int(token), recs, 64, C.byref(n)))
         return [(recs[i].name.decode(), recs[i].bytes, recs[i].ms, recs[i].launches) for i in range(n.value)]
 
+    def profile_step_floor(self, token: int, cache: "KvCache"):
+        """The greedy step at the cache's position next to its floor (every
+        launch replaced by a streaming phase of the same grid and bytes; the
+        cache is left as it was): dict with step_ms, floor_ms, empty_launch_ms
+        and kinds, a list of (name, algorithmic bytes, phase bytes, phase ms,
+        launches per step, workgroups)."""
+        recs = (tmg_floor_record * 64)()
+        n = C.c_size_t()
+        step, floor, empty = C.c_float(), C.c_float(), C.c_float()
+        check(lib.tmg_profile_step_floor(self._h, cache._h, int(token), recs, 64, C.byref(n), C.byref(step),
+                                         C.byref(floor), C.byref(empty)))
+        kinds = [(recs[i].name.decode(), recs[i].bytes, recs[i].floor_bytes, recs[i].floor_ms, recs[i].launches,
+                  recs[i].workgroups) for i in range(n.value)]
+        return {"step_ms": step.value, "floor_ms": floor.value, "empty_launch_ms": empty.value, "kinds": kinds}
+
 
 class KvCache:
     """KvCache (src/model.rs:250-332) as a preallocated HBM slab of max_pos rows."""
@@ -259,6 +274,15 @@ def generate(model: Model, prompt_tokens: Sequence[int], params: GenParams,
         raise err[0]
     return GenOutput(tokens=[int(x) for x in out[:n_out.value]], logits_first_step=first,
                      prefill_secs=secs.value)
+
+
+def profile_stream(nbytes: int, wg_kib: int, device: int = 0):
+    """tmg_profile_stream: (us per launch, bytes read) of a kernel that only
+    streams nbytes of HBM-cold data in workgroups of wg_kib KiB."""
+    us = C.c_float()
+    got = C.c_size_t()
+    check(lib.tmg_profile_stream(int(nbytes), int(wg_kib), int(device), C.byref(us), C.byref(got)))
+    return us.value, got.value
 
 
 def stdrng_uniform(seed: int, n: int) -> np.ndarray:
