@@ -101,8 +101,10 @@ def W():
 
 # --- kernel level: the decode GEMV (C1 shapes and ragged ones) ---------------
 
+# in = 2560 and 5120: 320-thread workgroups, one and two chunks of 2560
 @pytest.mark.parametrize("out,inp", [(2048, 2048), (6144, 2048), (2048, 6144), (73448, 2048), (24, 64),
-                                     (100, 136), (8, 10240), (1, 8), (2560, 4096)])
+                                     (100, 136), (8, 10240), (1, 8), (2560, 4096), (6144, 2560), (7, 2560),
+                                     (100, 5120)])
 def test_gemv_bf16_vs_oracle(T, O, out, inp):
     from tinyminigo_amd.hip import DeviceBuffer, synchronize
     print(f"gemv {out}x{inp}", flush=True)
@@ -467,6 +469,26 @@ def test_decode_attention_split_modes(T, O, untied, max_pos):
         if i % 37 == 0 or i == n - 1:
             close_logits(a, b, f"pos {i}")
     assert gc.total_len() == n
+
+
+def test_hidden_2560_model_vs_oracle(T, O, W):
+    """Hidden 2560 (the 4B shapes, 2 layers, vocab 1000): QKV with the
+    embedding gather, gate/up and the lm_head run 320-thread workgroups over
+    one 2560-element chunk, the lm_head's argmax over 125 workgroup keys.
+    Logits at every step and the greedy ids against the oracle."""
+    import dataclasses
+    wl = dataclasses.replace(W.FOUR_B, name="mid-h2560-l2-v1000", num_hidden_layers=2, vocab_size=1000,
+                             weight_seed=23)
+    p = W.ensure_model(wl, model_root())
+    g, o = T.Model.load(p), O.OracleModel.load(p)
+    ids = [int(t) for t in T.synth_tokens(37, 60, wl.vocab_size)]
+    gc, oc = T.KvCache(g, 80), o.new_cache()
+    close_logits(g.forward_seq(ids[:40], gc), o.forward_seq(ids[:40], oc), "prefill")
+    for i, t in enumerate(ids[40:]):
+        close_logits(g.forward_token(t, gc), o.forward_token(t, oc), f"decode {i}")
+    prompt = ids[:24]
+    assert T.generate(g, prompt, T.GenParams(max_tokens=24)).tokens == O.generate(o, prompt, 24).tokens
+    g.close()
 
 
 # --- C4: the 4B-class model, 128-token prompt + 256 sampled tokens ------------

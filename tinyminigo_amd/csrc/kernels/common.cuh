@@ -162,10 +162,12 @@ __device__ __forceinline__ T multi_wave_sum(T (&v)[R], int lane) {
     return group_sum<(64 >> LR)>(cur[0]);
 }
 
-// Block (256-thread) reductions of N values at once; every thread receives
-// the results.  `scratch` must hold 4*N floats.
-template <int N>
+// Block reductions of N values at once over NW wavefronts (256 threads by
+// default); every thread receives the results.  `scratch` must hold NW*N
+// floats.  The wave sums are added as ((w0 + w1) + (w2 + w3)) + w4 + ...
+template <int N, int NW = kBlock / 64>
 __device__ __forceinline__ void block_sum_n(float (&v)[N], float *scratch) {
+    static_assert(NW >= 4, "at least four wavefronts");
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
 #pragma unroll
     for (int i = 0; i < N; i++) v[i] = wave_sum(v[i]);
@@ -174,7 +176,12 @@ __device__ __forceinline__ void block_sum_n(float (&v)[N], float *scratch) {
         for (int i = 0; i < N; i++) scratch[w * N + i] = v[i];
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < N; i++) v[i] = (scratch[i] + scratch[N + i]) + (scratch[2 * N + i] + scratch[3 * N + i]);
+    for (int i = 0; i < N; i++) {
+        float s = (scratch[i] + scratch[N + i]) + (scratch[2 * N + i] + scratch[3 * N + i]);
+#pragma unroll
+        for (int k = 4; k < NW; k++) s += scratch[k * N + i];
+        v[i] = s;
+    }
     __syncthreads();
 }
 

@@ -19,32 +19,35 @@
 namespace tmg {
 namespace {
 
-template <int KC, int R, int PRO, int EPI>
-__global__ __launch_bounds__(kBlock) void gemv_kernel(const GemvArgs a) {
-    __shared__ float red[4][R];
-    __shared__ float scratch[4];
+// NT threads per workgroup (kBlock, or kWideBlock for rows of 2560 -- and
+// multiples -- that 2048-element chunks would leave a partial chunk of).
+template <int KC, int R, int PRO, int EPI, int NT = kBlock>
+__global__ __launch_bounds__(NT) void gemv_kernel(const GemvArgs a) {
+    constexpr int NW = NT / 64;
+    __shared__ float red[NW][R];
+    __shared__ float scratch[NW];
     WeightRegs<KC, R> W;
     float xv[KC][8];
     if constexpr (PRO == PRO_EMBED_NORM) {
         // the gathered row depends on the token id: weights first
-        gemv_load<KC, R>(a, blockIdx.x, W);
+        gemv_load<KC, R, NT>(a, blockIdx.x, W);
         const int pos = EPI == EPI_QKV ? *a.pos : 0;
-        gemv_embed_prologue<KC>(a, *a.token, xv, scratch, blockIdx.x == 0);
-        gemv_finish<KC, R, EPI>(a, blockIdx.x, pos, W, xv, red);
+        gemv_embed_prologue<KC, NT>(a, *a.token, xv, scratch, blockIdx.x == 0);
+        gemv_finish<KC, R, EPI, false, NT>(a, blockIdx.x, pos, W, xv, red);
     } else {
         // activation-side loads, then the weights (see gemv.cuh)
         ActIn<KC, PRO> in;
-        act_issue<KC, PRO>(a, in);
+        act_issue<KC, PRO, NT>(a, in);
         EpiIn pre{};
         if constexpr (EPI == EPI_RESID) epi_issue_resid<R>(a, blockIdx.x, pre);
-        gemv_load<KC, R>(a, blockIdx.x, W);
+        gemv_load<KC, R, NT>(a, blockIdx.x, W);
         // keep the scalar loads below after the weight loads: a wait for them
         // would otherwise hold back the remaining weight loads
         __builtin_amdgcn_sched_barrier(0);
         const int pos = (EPI == EPI_QKV || PRO == PRO_ATTN_COMBINE) ? *a.pos : 0;
         if constexpr (EPI == EPI_QKV) epi_load_rope<R>(a, blockIdx.x, pos, pre);
-        act_finish<KC, PRO>(a, pos, in, xv, scratch);
-        gemv_finish<KC, R, EPI, true>(a, blockIdx.x, pos, W, xv, red, pre);
+        act_finish<KC, PRO, NT>(a, pos, in, xv, scratch);
+        gemv_finish<KC, R, EPI, true, NT>(a, blockIdx.x, pos, W, xv, red, pre);
     }
 }
 
@@ -144,8 +147,34 @@ hipError_t launch_kc(const GemvArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Rows of 2560 elements (the 4B-class hidden size) in 2048-element chunks
+// leave a second chunk three quarters empty: its clamped loads repeat the
+// row's last 16 bytes and its registers halve the waves per SIMD.  Such
+// rows (and multiples of 2560 that are not multiples of 2048) take
+// kWideBlock threads and whole chunks of 2560.
+constexpr int kWideBlock = 320;
+constexpr int kWideChunk = kWideBlock * 8;
+
+template <int KC, int PRO, int EPI>
+hipError_t launch_wide(const GemvArgs &a, hipStream_t s) {
+    constexpr int R = (EPI == EPI_SWIGLU && KC == 1) ? 16 : gemv_rows<KC>();
+    static_assert(EPI != EPI_LOGITS || gemv_rows<KC>() == 8, "the argmax partials are counted with 8 rows per workgroup");
+    hipLaunchKernelGGL((gemv_kernel<KC, R, PRO, EPI, kWideBlock>), dim3((a.out + R - 1) / R), dim3(kWideBlock), 0, s,
+                       a);
+    return hipGetLastError();
+}
+
 template <int PRO, int EPI>
 hipError_t launch_pe(const GemvArgs &a, hipStream_t s) {
+    if constexpr (PRO != PRO_ATTN_COMBINE) {
+        if (!a.W8 && !a.Wf && a.in % kChunk != 0 && a.in % kWideChunk == 0) {
+            switch (a.in / kWideChunk) {
+                case 1: return launch_wide<1, PRO, EPI>(a, s);
+                case 2: return launch_wide<2, PRO, EPI>(a, s);
+                default: break;  // wider rows: 2048-element chunks
+            }
+        }
+    }
     const int kc = (a.in + kChunk - 1) / kChunk;
     switch (kc) {
         case 1: return launch_kc<1, PRO, EPI>(a, s);

@@ -33,8 +33,9 @@ struct WeightRegs {
     u32x4 w[R][KC];
 };
 
-// Issue the loads of block `blk` (rows blk*R .. blk*R+R-1, clamped).
-template <int KC, int R>
+// Issue the loads of block `blk` (rows blk*R .. blk*R+R-1, clamped).  NT
+// threads per workgroup: a chunk is NT * 8 elements of a row.
+template <int KC, int R, int NT = kBlock>
 __device__ __forceinline__ void gemv_load(const GemvArgs &a, int blk, WeightRegs<KC, R> &W) {
     const int t = threadIdx.x;
     const int row0 = blk * R;
@@ -46,18 +47,18 @@ __device__ __forceinline__ void gemv_load(const GemvArgs &a, int blk, WeightRegs
         for (int c = 0; c < KC; c++) {
             // clamped instead of branched, so all loads issue back to back;
             // gemv_finish zeroes the chunks past the row end
-            const int k = c * kChunk + t * 8;
+            const int k = c * NT * 8 + t * 8;
             W.w[r][c] = __builtin_nontemporal_load(wr + (min(k, a.in - 8) >> 3));
         }
     }
 }
 
-template <int KC>
+template <int KC, int NT = kBlock>
 __device__ __forceinline__ void load_act(const float *src, const uint16_t *src_bf, int in, float (&xv)[KC][8]) {
     const int t = threadIdx.x;
 #pragma unroll
     for (int c = 0; c < KC; c++) {
-        const int k = c * kChunk + t * 8;
+        const int k = c * NT * 8 + t * 8;
         if (k < in) {
             if (src_bf) {
                 const uint4 u = *reinterpret_cast<const uint4 *>(src_bf + k);
@@ -88,12 +89,12 @@ __device__ __forceinline__ void load_act(const float *src, const uint16_t *src_b
     }
 }
 
-template <int KC>
+template <int KC, int NT = kBlock>
 __device__ __forceinline__ void load_norm_w(const GemvArgs &a, float (&wv)[KC][8]) {
     const int t = threadIdx.x;
 #pragma unroll
     for (int c = 0; c < KC; c++) {
-        const int k = c * kChunk + t * 8;
+        const int k = c * NT * 8 + t * 8;
         float4 w0 = make_float4(0.f, 0.f, 0.f, 0.f), w1 = w0;
         if (k < a.in) {
             w0 = *reinterpret_cast<const float4 *>(a.norm_w + k);
@@ -112,8 +113,8 @@ __device__ __forceinline__ void load_norm_w(const GemvArgs &a, float (&wv)[KC][8
 
 // RMSNorm of the block's activation in registers (reference rms_norm_into,
 // src/tensor.rs:969-977; batch association src/tensor.rs:946-954).
-// `scratch` holds 4 floats of LDS.
-template <int KC, int PRO>
+// `scratch` holds NT / 64 floats of LDS.
+template <int KC, int PRO, int NT = kBlock>
 __device__ __forceinline__ void rms_scale(const GemvArgs &a, float (&xv)[KC][8], const float (&wv)[KC][8],
                                           float *scratch) {
     const int t = threadIdx.x;
@@ -122,11 +123,11 @@ __device__ __forceinline__ void rms_scale(const GemvArgs &a, float (&xv)[KC][8],
     for (int c = 0; c < KC; c++)
 #pragma unroll
         for (int j = 0; j < 8; j++) ss[0] += xv[c][j] * xv[c][j];
-    block_sum_n<1>(ss, scratch);
+    block_sum_n<1, NT / 64>(ss, scratch);
     const float inv = 1.0f / sqrtf(ss[0] / (float)a.in + a.eps);
 #pragma unroll
     for (int c = 0; c < KC; c++) {
-        const int k = c * kChunk + t * 8;
+        const int k = c * NT * 8 + t * 8;
         if (k < a.in) {
 #pragma unroll
             for (int j = 0; j < 8; j++) {
@@ -143,28 +144,28 @@ __device__ __forceinline__ void rms_scale(const GemvArgs &a, float (&xv)[KC][8],
 // Prologue of the layer-0 QKV GEMV: the embedding row of token `tok`
 // (src/model.rs:401-403; BF16 rows widen exactly), stored as the residual
 // stream by one workgroup, then RMSNorm (rms_norm_into, src/tensor.rs:969-977).
-// `scratch` holds 4 floats of LDS.
-template <int KC>
+// `scratch` holds NT / 64 floats of LDS.
+template <int KC, int NT = kBlock>
 __device__ __forceinline__ void gemv_embed_prologue(const GemvArgs &a, int tok, float (&xv)[KC][8], float *scratch,
                                                     bool store_x) {
     const int t = threadIdx.x;
     const int in = a.in;
     if (a.embed_bf16)
-        load_act<KC>(nullptr, a.embed_bf16 + (size_t)tok * in, in, xv);
+        load_act<KC, NT>(nullptr, a.embed_bf16 + (size_t)tok * in, in, xv);
     else
-        load_act<KC>(a.embed_f32 + (size_t)tok * in, nullptr, in, xv);
+        load_act<KC, NT>(a.embed_f32 + (size_t)tok * in, nullptr, in, xv);
     if (store_x) {
 #pragma unroll
         for (int c = 0; c < KC; c++) {
-            const int k = c * kChunk + t * 8;
+            const int k = c * NT * 8 + t * 8;
             if (k < in)
 #pragma unroll
                 for (int j = 0; j < 8; j++) a.x_store[k + j] = xv[c][j];
         }
     }
     float wv[KC][8];
-    load_norm_w<KC>(a, wv);
-    rms_scale<KC, PRO_NORM>(a, xv, wv, scratch);
+    load_norm_w<KC, NT>(a, wv);
+    rms_scale<KC, PRO_NORM, NT>(a, xv, wv, scratch);
 }
 
 // Epilogue inputs loaded ahead of the weights: the residual of row blk*R+t
@@ -181,27 +182,32 @@ __device__ __forceinline__ float pick4(const float (&v)[4], int i) {
     return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
 }
 
-// Value of local row i of a block from the four per-wave partials in `red`:
-// the f32 sum (BF16 rows), or for int8 rows the exact integer dot times the
-// activation scale and the row scale, y = (dot as f32) * xs * scale[o]
-// (matmul_w_into's WMat::I8 arm, src/tensor.rs:349-353).
-template <int R, bool Q8>
+// Value of local row i of a block from the NW per-wave partials in `red`:
+// the f32 sum ((w0 + w1) + (w2 + w3)) + w4 ... (BF16 and f32 rows), or for
+// int8 rows (four waves) the exact integer dot times the activation scale
+// and the row scale, y = (dot as f32) * xs * scale[o] (matmul_w_into's
+// WMat::I8 arm, src/tensor.rs:349-353).
+template <int R, bool Q8, int NW = 4>
 __device__ __forceinline__ float row_value(float (*red)[R], int i, float xs, float sc) {
     // the product is rounded before any residual add, as the reference
     // stores y and adds it afterwards (no contraction into an FMA)
 #pragma clang fp contract(off)
     if constexpr (Q8) {
+        static_assert(NW == 4, "int8 rows run four waves");
         const int d = (__float_as_int(red[0][i]) + __float_as_int(red[1][i])) +
                       (__float_as_int(red[2][i]) + __float_as_int(red[3][i]));
         return ((float)d * xs) * sc;
     } else {
-        return (red[0][i] + red[1][i]) + (red[2][i] + red[3][i]);
+        float v = (red[0][i] + red[1][i]) + (red[2][i] + red[3][i]);
+#pragma unroll
+        for (int w = 4; w < NW; w++) v += red[w][i];
+        return v;
     }
 }
 
 // FMAs over a loaded block of BF16 rows and the per-wave reduction into
-// `red` (LDS of 4*R floats).
-template <int KC, int R>
+// `red` (LDS of NT / 64 * R floats).
+template <int KC, int R, int NT = kBlock>
 __device__ __forceinline__ void gemv_dot(const GemvArgs &a, const WeightRegs<KC, R> &W, const float (&xv)[KC][8],
                                          float (*red)[R]) {
     const int t = threadIdx.x;
@@ -216,7 +222,7 @@ __device__ __forceinline__ void gemv_dot(const GemvArgs &a, const WeightRegs<KC,
             // duplicated Inf or NaN weight would survive a zero activation);
             // the test is uniform, so full chunks keep their registers
             u32x4 u = W.w[r][c];
-            if ((c + 1) * kChunk > a.in && c * kChunk + t * 8 >= a.in) u = u32x4{0u, 0u, 0u, 0u};
+            if ((c + 1) * NT * 8 > a.in && c * NT * 8 + t * 8 >= a.in) u = u32x4{0u, 0u, 0u, 0u};
             s0 = fmaf(xv[c][0], bf16_lo(u.x), s0);
             s1 = fmaf(xv[c][1], bf16_hi(u.x), s1);
             s0 = fmaf(xv[c][2], bf16_lo(u.y), s0);
@@ -237,7 +243,7 @@ __device__ __forceinline__ void gemv_dot(const GemvArgs &a, const WeightRegs<KC,
 // __syncthreads).  With PRE the residual / RoPE inputs come from `pre`
 // instead of memory; with Q8 the rows are int8 (row scales in pre.sc, xs the
 // activation scale).
-template <int R, int EPI, bool PRE, bool Q8>
+template <int R, int EPI, bool PRE, bool Q8, int NW = 4>
 __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int blk, int pos, float (*red)[R], const EpiIn &pre,
                                               float xs) {
     const int t = threadIdx.x;
@@ -245,7 +251,7 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int blk, int po
     if constexpr (EPI == EPI_STORE || EPI == EPI_RESID || EPI == EPI_LOGITS) {
         if (t < R) {
             const int row = row0 + t;
-            const float v = row_value<R, Q8>(red, t, xs, pre.sc[0]);
+            const float v = row_value<R, Q8, NW>(red, t, xs, pre.sc[0]);
             const bool ok = row < a.out;
             if (ok) {
                 if constexpr (EPI == EPI_RESID)
@@ -268,8 +274,8 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int blk, int po
     } else {
         if (t < R / 2) {
             const int P = row0 / 2 + t;  // global pair index
-            const float va = row_value<R, Q8>(red, 2 * t, xs, pre.sc[0]);
-            const float vb = row_value<R, Q8>(red, 2 * t + 1, xs, pre.sc[1]);
+            const float va = row_value<R, Q8, NW>(red, 2 * t, xs, pre.sc[0]);
+            const float vb = row_value<R, Q8, NW>(red, 2 * t + 1, xs, pre.sc[1]);
             if (2 * P + 1 < a.out) {
                 if constexpr (EPI == EPI_SWIGLU) {
                     a.y[P] = swiglu(va, vb);
@@ -305,12 +311,12 @@ __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, int blk, int po
 // `red` is LDS of 4*R floats.  Returns after the epilogue; the caller
 // separates consecutive calls with a __syncthreads (red is reused).  With
 // PRE the residual / RoPE inputs come from `pre` instead of memory.
-template <int KC, int R, int EPI, bool PRE = false>
+template <int KC, int R, int EPI, bool PRE = false, int NT = kBlock>
 __device__ __forceinline__ void gemv_finish(const GemvArgs &a, int blk, int pos, const WeightRegs<KC, R> &W,
                                             const float (&xv)[KC][8], float (*red)[R], const EpiIn &pre = EpiIn{}) {
-    gemv_dot<KC, R>(a, W, xv, red);
+    gemv_dot<KC, R, NT>(a, W, xv, red);
     __syncthreads();
-    gemv_epilogue<R, EPI, PRE, false>(a, blk, pos, red, pre, 0.0f);
+    gemv_epilogue<R, EPI, PRE, false, NT / 64>(a, blk, pos, red, pre, 0.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -527,13 +533,13 @@ struct ActIn {
 
 // PRO in {PLAIN, NORM, NORM_BATCH, ATTN_COMBINE}; ATTN_COMBINE requires
 // a.nsplit <= kFusedSplits.
-template <int KC, int PRO>
+template <int KC, int PRO, int NT = kBlock>
 __device__ __forceinline__ void act_issue(const GemvArgs &a, ActIn<KC, PRO> &in) {
     const int t = threadIdx.x;
     if constexpr (PRO == PRO_ATTN_COMBINE) {
 #pragma unroll
         for (int c = 0; c < KC; c++) {
-            const int k = c * kChunk + t * 8;
+            const int k = c * NT * 8 + t * 8;
             const bool ok = k < a.in;
             const int h = k / a.hd, d = k - h * a.hd;
             const int g = h / a.group, hq = h - g * a.group;
@@ -552,13 +558,13 @@ __device__ __forceinline__ void act_issue(const GemvArgs &a, ActIn<KC, PRO> &in)
             }
         }
     } else {
-        load_act<KC>(a.x, nullptr, a.in, in.xv);
-        if constexpr (ActIn<KC, PRO>::kNorm) load_norm_w<KC>(a, in.wv);
+        load_act<KC, NT>(a.x, nullptr, a.in, in.xv);
+        if constexpr (ActIn<KC, PRO>::kNorm) load_norm_w<KC, NT>(a, in.wv);
     }
 }
 
 // The prologue's arithmetic: the split merge, or the copy of x and its RMSNorm.
-template <int KC, int PRO>
+template <int KC, int PRO, int NT = kBlock>
 __device__ __forceinline__ void act_finish(const GemvArgs &a, int pos, ActIn<KC, PRO> &in, float (&xv)[KC][8],
                                            float *scratch) {
     const int t = threadIdx.x;
@@ -566,7 +572,7 @@ __device__ __forceinline__ void act_finish(const GemvArgs &a, int pos, ActIn<KC,
         const int active = active_splits(pos + 1, a.nsplit, a.attn_block);
 #pragma unroll
         for (int c = 0; c < KC; c++) {
-            const int k = c * kChunk + t * 8;
+            const int k = c * NT * 8 + t * 8;
 #pragma unroll
             for (int j = 0; j < 8; j++) xv[c][j] = 0.0f;
             if (k >= a.in) continue;
@@ -599,7 +605,7 @@ __device__ __forceinline__ void act_finish(const GemvArgs &a, int pos, ActIn<KC,
         for (int c = 0; c < KC; c++)
 #pragma unroll
             for (int j = 0; j < 8; j++) xv[c][j] = in.xv[c][j];
-        if constexpr (ActIn<KC, PRO>::kNorm) rms_scale<KC, PRO>(a, xv, in.wv, scratch);
+        if constexpr (ActIn<KC, PRO>::kNorm) rms_scale<KC, PRO, NT>(a, xv, in.wv, scratch);
     }
 }
 
