@@ -120,8 +120,10 @@ hipError_t launch_kc(const GemvArgs &a, hipStream_t s) {
     // the split-merge prologue re-reads every split's partials per
     // workgroup: over a 4096-wide attention output 16 rows per workgroup,
     // which halve that traffic, are faster (4B o_proj 9.0 -> 7.8 us); over
-    // 2048 slower (1B 4.3 -> 4.6 us)
-    constexpr int R = (PRO == PRO_ATTN_COMBINE && KC == 2) ? 16 : gemv_rows<KC>();
+    // 2048 slower (1B 4.3 -> 4.6 us).  The one-chunk gate/up GEMV also takes
+    // 16 rows (half the workgroups, each with the RMSNorm prologue): 1B
+    // 9.70 -> 9.46 us, the step 0.747 -> 0.745 ms
+    constexpr int R = (PRO == PRO_ATTN_COMBINE && KC == 2) || (EPI == EPI_SWIGLU && KC == 1) ? 16 : gemv_rows<KC>();
     const int grid = (a.out + R - 1) / R;
     if (!a.W8 && a.Wf) {
         // (the split-merge prologue is fused only over attention outputs of
