@@ -397,15 +397,15 @@ constexpr int kWideAttnSplits = 32;
 static_assert(kAttnThreads == kBlock, "the host sizes the attention partition for kBlock threads");
 
 // The instantiation whose chunk (= partition block) is a.block positions:
-// the short-context width (decode only) or kAttnBlockLong.
+// the short-context width (decode of short caches, prefill rows at four or
+// more query heads per KV head) or kAttnBlockLong.
 template <int HD, int GROUP, bool SPEC>
 hipError_t launch_attn_group(const AttnArgs &a, dim3 grid, hipStream_t s) {
     const int blk = a.block ? a.block : kAttnBlockLong;
     if (blk == attn_chunk(HD, GROUP, kBlock, kAttnBlockLong)) {
         hipLaunchKernelGGL((attn_kernel<HD, GROUP, SPEC, kBlock, kAttnBlockLong>), grid, dim3(kBlock), 0, s, a);
-    } else if (SPEC && blk == attn_chunk(HD, GROUP, kBlock, kAttnBlockShort)) {
-        if constexpr (SPEC)
-            hipLaunchKernelGGL((attn_kernel<HD, GROUP, SPEC, kBlock, kAttnBlockShort>), grid, dim3(kBlock), 0, s, a);
+    } else if (blk == attn_chunk(HD, GROUP, kBlock, kAttnBlockShort)) {
+        hipLaunchKernelGGL((attn_kernel<HD, GROUP, SPEC, kBlock, kAttnBlockShort>), grid, dim3(kBlock), 0, s, a);
     } else {
         return hipErrorInvalidValue;
     }
