@@ -950,6 +950,131 @@ __global__ __launch_bounds__(PAIR ? 2 * kBlock : kBlock, PAIR ? 1 : 2) void gemm
                                        out, &pre);
 }
 
+// The split-K short-prompt GEMM over 128-row tiles: eight wavefronts, waves
+// 4-7 taking rows 64-127 of the tile against the same 64 tokens.  The
+// activation tiles (hi and lo, 4 bytes per element against the weights' 2)
+// are staged once per 128 weight rows instead of once per 64, a third less
+// DMA per weight byte; each wave's MFMAs, split-K exchange and epilogue are
+// those of gemm_skinny_kernel for its own 64 rows.  One workgroup per CU
+// (a 96 KB ring).
+constexpr int kSk2Ops = 4;  // DMA instructions per wave per step
+template <int EPI>
+__global__ __launch_bounds__(2 * kBlock, 1) void gemm_skinny_wide_kernel(const GemmArgs a, int nsplit, int n_tiles) {
+    // stage: W rows 0-63, W rows 64-127, X hi, X lo
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[kSkStages * 4 * kSkTile];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int wq = wave & 3, half = wave >> 2;
+    const int r = lane & 15, q = lane >> 4;
+    const int m_tiles = (a.M + 127) >> 7;
+    const int rest = blockIdx.x >> 3;
+    const int nt = rest % n_tiles;
+    const int g = (rest / n_tiles) * 8 + (blockIdx.x & 7);
+    if (g >= m_tiles * nsplit) return;  // padding blocks of the XCD grouping
+    const int mt = g % m_tiles, ks = g / m_tiles;
+    const int K = a.K, nk = K >> 6;
+    const int s0 = ks * nk / nsplit, ns = (ks + 1) * nk / nsplit - s0;
+    const int m0 = mt * 128 + half * 64, n0 = nt * 64;
+    // DMA: wave w fills row groups 2 wq, 2 wq + 1 of its half's W tile and of
+    // X hi (waves 0-3) or X lo (waves 4-7)
+    const uint16_t *src[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int row = (2 * wq + i) * 8 + (lane >> 3);
+        const int lc = (lane & 7) ^ (row & 7);
+        const size_t kofs = (size_t)s0 * 64 + lc * 8;
+        src[0][i] = a.W + (size_t)min(m0 + row, a.M - 1) * K + kofs;
+        src[1][i] = (half ? a.Blo : a.Bhi) + (size_t)min(n0 + row, a.N - 1) * K + kofs;
+    }
+    auto stage = [&](int p) { return smem + (p % kSkStages) * 4 * kSkTile; };
+    auto issue = [&](int p) {
+        unsigned char *dst = stage(p);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            __builtin_amdgcn_global_load_lds(src[0][i] + p * 64, dst + half * kSkTile + (2 * wq + i) * 1024, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(src[1][i] + p * 64, dst + (2 + half) * kSkTile + (2 * wq + i) * 1024, 16, 0, 0);
+        }
+    };
+    static_assert(kSkStages == 3, "wait counts assume one stage in flight behind the current one");
+    if (0 < ns) issue(0);
+    if (1 < ns) issue(1);
+    f32x4 acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int rb = wq * 16 + r;
+    for (int p = 0; p < ns; p++) {
+        // stage p's DMAs of this wave are complete once at most stage p + 1's
+        // are outstanding (only DMAs are outstanding: they complete in order)
+        if (p + 1 < ns)
+            __builtin_amdgcn_s_waitcnt(0x0F70 | kSk2Ops);  // vmcnt(kSk2Ops)
+        else
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __builtin_amdgcn_s_barrier();  // every wave's DMAs of stage p landed; stage p-1's reads are done
+        if (p + 2 < ns) issue(p + 2);
+        const unsigned char *st = stage(p);
+        const unsigned char *sa = st + half * kSkTile, *sh = st + 2 * kSkTile, *sl = st + 3 * kSkTile;
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+            const int lc = kk * 4 + q;
+            bf16x8 fa[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int ra = i * 16 + r;
+                fa[i] = *reinterpret_cast<const bf16x8 *>(sa + ra * 128 + ((lc ^ (ra & 7)) * 16));
+            }
+            const bf16x8 fh = *reinterpret_cast<const bf16x8 *>(sh + rb * 128 + ((lc ^ (rb & 7)) * 16));
+            const bf16x8 fl = *reinterpret_cast<const bf16x8 *>(sl + rb * 128 + ((lc ^ (rb & 7)) * 16));
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fh, acc[i], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fl, acc[i], 0, 0, 0);
+        }
+    }
+    // the ring is free for the output staging once every wave is past its reads
+    __builtin_amdgcn_s_barrier();
+    if (m0 >= a.M) return;  // the second half of the last row tile lies past the rows
+    EpiPre<EPI, 4> pre;
+    epi_prefetch<EPI, 4>(a, m0, n0 + wq * 16, pre);
+    if (nsplit > 1) {
+        // as in gemm_skinny_kernel, per 64-row half: device-scope partials,
+        // a per-quarter counter, the last wave to arrive adds the partials
+        // in split order
+        const int m64 = (a.M + 63) >> 6;  // 64-row tiles: the counters and partials are laid out per 64 rows
+        const int slot = (nt * m64 + mt * 2 + half) * 4 + wq;
+        float *part = a.part + ((size_t)slot * nsplit + ks) * 1024 + lane;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) st_dev(part + (i * 4 + e) * 64, acc[i][e]);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        unsigned old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(&a.cnt[slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = __builtin_amdgcn_readfirstlane(old);
+        if (old != (unsigned)(nsplit - 1)) return;
+        const float *p0 = a.part + (size_t)slot * nsplit * 1024 + lane;
+        float pv[kSkMaxSplit][16];
+#pragma unroll
+        for (int sp = 0; sp < kSkMaxSplit; sp++)
+            if (sp < nsplit)
+#pragma unroll
+                for (int e = 0; e < 16; e++) pv[sp][e] = ld_dev(p0 + (size_t)sp * 1024 + e * 64);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[i][e] = pv[0][i * 4 + e];
+#pragma unroll
+        for (int sp = 1; sp < kSkMaxSplit; sp++)
+            if (sp < nsplit)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[i][e] += pv[sp][i * 4 + e];
+        if (lane == 0) __hip_atomic_store(&a.cnt[slot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const f32x4 out[4][1] = {{acc[0]}, {acc[1]}, {acc[2]}, {acc[3]}};
+    stage_epilogue<EPI, 4, 1, 4, true>(a, reinterpret_cast<float *>(smem) + wave * 16 * kStagePitch, m0, n0 + wq * 16,
+                                       out, &pre);
+}
+
 hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
     // split K while the grid stays within one workgroup per CU, or while
     // splits keep at least 20 K steps within three workgroups per CU; at most
@@ -980,11 +1105,33 @@ hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
         }
         return hipGetLastError();
     }
+    // one token tile: 64-row tiles of four waves (128-row tiles measured
+    // slower there: 1B 64-token prefill 1.62 -> 1.81 ms)
+    if (n_tiles == 1) {
+        switch (epi) {
+            case GEPI_STORE: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_STORE, false>), grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
+            case GEPI_RESID: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_RESID, false>), grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
+            case GEPI_SWIGLU: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_SWIGLU, false>), grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
+            case GEPI_QKV: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_QKV, false>), grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
+    // two or more token tiles: 128-row tiles (the activation tiles staged
+    // once per 128 weight rows; 4B 128-token prefill 5.83 -> 5.58 ms), K
+    // split while the grid stays within one workgroup (eight waves, a 96 KB
+    // ring) per CU
+    const int m2 = (a.M + 127) / 128;
+    int ns2 = 1;
+    if (a.part && a.cnt)
+        while (ns2 * 2 <= kSkMaxSplit && nk / (ns2 * 2) >= 2 && m2 * n_tiles * ns2 * 2 <= 256) ns2 *= 2;
+    if (ns2 > 1 && (size_t)m_tiles * n_tiles * ns2 * 4096 > kSkinnyPartFloats) return hipErrorInvalidValue;
+    const dim3 grid2((m2 * ns2 + 7) / 8 * n_tiles * 8);
     switch (epi) {
-        case GEPI_STORE: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_STORE, false>), grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
-        case GEPI_RESID: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_RESID, false>), grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
-        case GEPI_SWIGLU: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_SWIGLU, false>), grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
-        case GEPI_QKV: hipLaunchKernelGGL((gemm_skinny_kernel<GEPI_QKV, false>), grid, dim3(kBlock), 0, s, a, nsplit, n_tiles); break;
+        case GEPI_STORE: hipLaunchKernelGGL((gemm_skinny_wide_kernel<GEPI_STORE>), grid2, dim3(2 * kBlock), 0, s, a, ns2, n_tiles); break;
+        case GEPI_RESID: hipLaunchKernelGGL((gemm_skinny_wide_kernel<GEPI_RESID>), grid2, dim3(2 * kBlock), 0, s, a, ns2, n_tiles); break;
+        case GEPI_SWIGLU: hipLaunchKernelGGL((gemm_skinny_wide_kernel<GEPI_SWIGLU>), grid2, dim3(2 * kBlock), 0, s, a, ns2, n_tiles); break;
+        case GEPI_QKV: hipLaunchKernelGGL((gemm_skinny_wide_kernel<GEPI_QKV>), grid2, dim3(2 * kBlock), 0, s, a, ns2, n_tiles); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
