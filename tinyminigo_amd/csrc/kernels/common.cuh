@@ -98,6 +98,13 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// log2 of a power-of-two count of values per lane, at most 64 (one per lane).
+template <int R>
+__host__ __device__ constexpr int log2_pow2() {
+    static_assert(R == 1 || R == 2 || R == 4 || R == 8 || R == 16 || R == 32 || R == 64, "R must be 2^k <= 64");
+    return R == 64 ? 6 : R == 32 ? 5 : R == 16 ? 4 : R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
+}
+
 // Reduce R values per lane across the 64-lane wavefront with a transposed
 // butterfly: log2(R) exchange steps (lane halves 32 and 16 by permlane swaps,
 // 8 by DPP) that halve the live values, then a plain butterfly within the
@@ -105,8 +112,7 @@ __device__ __forceinline__ float wave_max(float v) {
 // (lane >> (6 - log2 R)).
 template <int R, class T>
 __device__ __forceinline__ T multi_wave_sum(T (&v)[R], int lane) {
-    static_assert(R == 1 || R == 2 || R == 4 || R == 8 || R == 16 || R == 32 || R == 64, "R must be 2^k <= 64");
-    constexpr int LR = R == 64 ? 6 : R == 32 ? 5 : R == 16 ? 4 : R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
+    constexpr int LR = log2_pow2<R>();
     T cur[R];
 #pragma unroll
     for (int i = 0; i < R; i++) cur[i] = v[i];

@@ -234,7 +234,7 @@ __device__ __forceinline__ void gemv_dot(const GemvArgs &a, const WeightRegs<KC,
         }
         acc[r] = s0 + s1;
     }
-    constexpr int LR = R == 16 ? 4 : R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
+    constexpr int LR = log2_pow2<R>();  // row i's sum lands in the lanes whose top LR bits are i
     const float sum = multi_wave_sum<R>(acc, lane);
     if ((lane & ((64 >> LR) - 1)) == 0) red[wave][lane >> (6 - LR)] = sum;
 }
@@ -381,7 +381,7 @@ __device__ __forceinline__ void gemv_dotf(const GemvArgs &a, const WeightRegsF<K
         }
         acc[r] = s0 + s1;
     }
-    constexpr int LR = R == 16 ? 4 : R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
+    constexpr int LR = log2_pow2<R>();  // row i's sum lands in the lanes whose top LR bits are i
     const float sum = multi_wave_sum<R>(acc, lane);
     if ((lane & ((64 >> LR) - 1)) == 0) red[wave][lane >> (6 - LR)] = sum;
 }
@@ -506,7 +506,7 @@ __device__ __forceinline__ void gemv_dot8(const WeightRegs8<KC, R> &W, const int
         }
         acc[r] = d;
     }
-    constexpr int LR = R == 16 ? 4 : R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
+    constexpr int LR = log2_pow2<R>();  // row i's sum lands in the lanes whose top LR bits are i
     const int sum = multi_wave_sum<R>(acc, lane);
     if ((lane & ((64 >> LR) - 1)) == 0) red[wave][lane >> (6 - LR)] = __int_as_float(sum);
 }
