@@ -100,6 +100,26 @@ def test_batch_of_more_than_eight_with_norm_hand_off(T, O, W):
         assert got[b] == T.generate(g, prompts[b], T.GenParams(max_tokens=20)).tokens, f"sequence {b} alone"
 
 
+def test_batch_of_more_than_sixty_four(T, O, W):
+    """70 sequences: the step's GEMMs have two token tiles, so they run the
+    128-row split-K tiles, with each sequence's own position and cache in
+    the QKV epilogue and the RMSNorm handed between the GEMMs (hidden 256).
+    Every sequence's ids are the oracle's generate."""
+    import dataclasses
+    wl = dataclasses.replace(W.TINY, name="tiny-llama-h256-q4-k2-d64-i512-s23", hidden_size=256,
+                             num_attention_heads=4, num_key_value_heads=2, head_dim=64, intermediate_size=512,
+                             tied_lm_head=False, weight_seed=23, rms_norm_eps=1e-5)
+    p = W.ensure_model(wl, model_root())
+    g, o = T.Model.load(p), O.OracleModel.load(p)
+    lens = [1 + (7 * i) % 40 for i in range(70)]
+    prompts = [[int(t) for t in T.synth_tokens(300 + i, n, wl.vocab_size)] for i, n in enumerate(lens)]
+    print("batch hidden 256 x70", flush=True)
+    got, _ = T.generate_batch(g, prompts, 12)
+    for b, pr in enumerate(prompts):
+        assert got[b] == O.generate(o, pr, 12).tokens, f"sequence {b}"
+    g.close()
+
+
 def test_batch_tied_and_k_not_multiple_of_64(T, O, W, tiny_path):
     import dataclasses
     wl = dataclasses.replace(W.TINY, name="tiny-llama-h96-kv3-i160-s13", hidden_size=96, num_attention_heads=6,

@@ -591,6 +591,37 @@ def test_short_prompt_odd_k_steps_vs_oracle(T, O, W):
             close_logits(g.forward_token(ids[i], gc), o.forward_token(ids[i], oc), f"decode at {i}")
 
 
+def test_short_prompt_128_row_tiles_past_the_last_row(T, O, W):
+    # prompts of 65-255 tokens run the 128-row split-K GEMM tiles; on hidden
+    # 192 the o_proj and down GEMMs have 192 rows, so the second tile's
+    # upper half lies past the last row (its waves return before the split
+    # exchange and the epilogue), down (K = 320, five steps) splits 2 + 3
+    # steps, and the last token tile is partial (100 = 64 + 36, 190 = 2 x 64
+    # + 62); a rerun is bitwise identical
+    import dataclasses
+    wl = dataclasses.replace(W.TINY, name="tiny-llama-h192-kv6-i320-s17", hidden_size=192, num_attention_heads=12,
+                             num_key_value_heads=6, intermediate_size=320, weight_seed=17)
+    p = W.ensure_model(wl, model_root())
+    g, o = T.Model.load(p), O.OracleModel.load(p)
+    ids = [int(t) for t in T.synth_tokens(73, 194, wl.vocab_size)]
+    for n in (100, 190):
+        print(f"h192 prefill {n}", flush=True)
+        gc, oc = T.KvCache(g, 200), o.new_cache()
+        a = g.forward_seq(ids[:n], gc)
+        close_logits(a, o.forward_seq(ids[:n], oc), f"prefill {n}")
+        for layer in range(wl.num_hidden_layers):
+            for x, y in ((gc.keys_flat(layer), oc.keys_flat(layer)), (gc.values_flat(layer), oc.values_flat(layer))):
+                d = np.abs(x - y)
+                assert np.all(d <= ABS_TOL + REL_TOL * np.abs(y)), f"prefill {n} layer {layer} kv: {d.max():.3e}"
+        for i in range(n, n + 4):
+            close_logits(g.forward_token(ids[i], gc), o.forward_token(ids[i], oc), f"decode at {i}")
+        gc2 = T.KvCache(g, 200)
+        assert np.array_equal(a, g.forward_seq(ids[:n], gc2))
+        gc.close()
+        gc2.close()
+    g.close()
+
+
 def test_long_prefill_chunks_vs_oracle(T, O, W, one_b):
     # 1B model: a 700-token prefill, a second 333-token chunk starting at 700
     # (MFMA attention with start > 0, partial query blocks), then decode steps
