@@ -232,6 +232,8 @@ hipError_t launch_mt_kt(const GemvArgs &a, hipStream_t s) {
 template <int KC, int PRO, int EPI>
 hipError_t launch_mt_kc(const GemvArgs &a, hipStream_t s) {
     if constexpr (KC <= 3) {
+        if constexpr (KC == 1)
+            if (gemv_mt_group(KC, a.nb) == 8) return launch_mt_kt<KC, 8, PRO, EPI>(a, s);
         if (gemv_mt_group(KC, a.nb) == 4) return launch_mt_kt<KC, 4, PRO, EPI>(a, s);
     }
     return launch_mt_kt<KC, 2, PRO, EPI>(a, s);

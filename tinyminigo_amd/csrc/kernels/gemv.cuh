@@ -658,13 +658,21 @@ __device__ __forceinline__ void epi_load_rope(const GemvArgs &a, int blk, int po
 // one transposed butterfly, and runs the epilogue per (row, sequence).
 // ---------------------------------------------------------------------------
 
-// Activation rows per group: 2 for two sequences, else 4 (2 above three
-// chunks); activation registers TG * KC * 8.
-__host__ __device__ constexpr int gemv_mt_group(int KC, int nb) { return (nb <= 2 || KC > 3) ? 2 : 4; }
+// Activation rows per group: 2 for two sequences; rows of one chunk take
+// all of five to eight sequences in one group (one load round trip, one norm
+// and one dot reduction per launch; 8 sequences of the 1B model 1.537 ->
+// 1.518 ms per step); else 4 (2 above three chunks).  Activation registers
+// TG * KC * 8.
+__host__ __device__ constexpr int gemv_mt_group(int KC, int nb) {
+    return (nb <= 2 || KC > 3) ? 2 : (KC == 1 && nb > 4) ? 8 : 4;
+}
 // Rows per workgroup: every workgroup reads each group's activation rows
 // from L2, so more rows per workgroup mean fewer re-reads per weight byte;
-// R * TG dots stay within 32 (registers, and two waves per SIMD).
-__host__ __device__ constexpr int gemv_mt_rows(int KC, int TG) { return KC == 1 ? 32 / TG : KC <= 3 ? 16 / TG : 4; }
+// R * TG dots stay within 32 (registers, and two waves per SIMD), 64 for a
+// group of eight over one chunk (4 rows there were slower: 1.71 ms).
+__host__ __device__ constexpr int gemv_mt_rows(int KC, int TG) {
+    return KC == 1 ? (TG == 8 ? 8 : 32 / TG) : KC <= 3 ? 16 / TG : 4;
+}
 
 // Raw loads of activation rows b0 .. b0+TG-1 (zeros past a.nb).
 template <int KC, int TG>
@@ -751,7 +759,7 @@ __device__ __forceinline__ void mt_dot(const GemvArgs &a, const WeightRegs<KC, R
         }
     }
     constexpr int N = R * TG;
-    constexpr int LN = N == 64 ? 6 : N == 32 ? 5 : N == 16 ? 4 : N == 8 ? 3 : N == 4 ? 2 : N == 2 ? 1 : 0;
+    constexpr int LN = log2_pow2<N>();
     const float sum = multi_wave_sum<N>(acc, lane);
     if ((lane & ((64 >> LN) - 1)) == 0) red[wave][lane >> (6 - LN)] = sum;
 }
