@@ -109,15 +109,25 @@ int enqueue_batch_step_mt(tmg_model *m, const Batch &bt) {
         aa.hd = m->hd;
         aa.T = B;
         aa.scale = 1.0f / sqrtf((float)m->hd);
-        aa.nsplit = 1;
         aa.pos_seq = bt.pos;
         aa.k_seq = bt.kptr;
         aa.v_seq = bt.vptr;
         aa.kv_layer_off = layer_off;
         aa.part = m->attn_part;
         aa.part_ml = m->attn_ml;
-        aa.out_f32 = bt.attn;
+        // each sequence's context dealt to up to 8 splits in short blocks
+        // (the partial buffers hold kMaxSplits splits of one row: B x splits
+        // at most that), merged per row by attn_combine_kernel
+        const int blk = attn_chunk(m->hd, m->nq / m->nkv, kAttnThreads, kAttnBlockShort);
+        const int ns = std::min<int>(std::min(8, kMaxSplits / B), (int)((bt.max_pos + blk - 1) / blk));
+        aa.nsplit = std::max(ns, 1);
+        aa.block = aa.nsplit > 1 ? blk : 0;
+        aa.out_f32 = aa.nsplit > 1 ? nullptr : bt.attn;
         TMG_HIPB(launch_attn(aa, s));
+        if (aa.nsplit > 1) {
+            aa.out_f32 = bt.attn;
+            TMG_HIPB(launch_attn_combine(aa, s));
+        }
 
         GemvArgs oa{};
         oa.W = ly.o;

@@ -355,20 +355,23 @@ __global__ __launch_bounds__(NT) void attn_kernel(const AttnArgs a) {
     attn_item<HD, GROUP, false, NT, CHW>(a, split, g, ti, qpos, active, sm);
 }
 
-// Merge of the split-K partials of decode row 0, one workgroup per query
-// head: the split statistics (max m_s, sum l_s) are reduced once per
-// workgroup, then 256 threads = (256 / hd) split lanes x hd dims accumulate
-// sum_s e^(m_s - M) o_s[d] with all their partial loads in flight, and the
-// split lanes are summed through LDS.  out = that / sum_s e^(m_s - M) l_s.
+// Merge of the split-K partials of a decode launch, one workgroup per
+// (query head, row): the split statistics (max m_s, sum l_s) are reduced
+// once per workgroup, then 256 threads = (256 / hd) split lanes x hd dims
+// accumulate sum_s e^(m_s - M) o_s[d] with all their partial loads in
+// flight, and the split lanes are summed through LDS.  out = that /
+// sum_s e^(m_s - M) l_s.  Row ti's position is pos_seq[ti] (batched decode)
+// or the cache position + ti.
 __global__ __launch_bounds__(kBlock) void attn_combine_kernel(const AttnArgs a) {
     __shared__ float s_w[kBlock];
     __shared__ float s_o[kBlock];
     __shared__ float scratch[4];
-    const int h = blockIdx.x, t = threadIdx.x;
+    const int h = blockIdx.x, ti = blockIdx.y, t = threadIdx.x;
     const int group = a.nq / a.nkv;
     const int g = h / group, hq = h - g * group;
-    const int active = active_splits(*a.pos_dev + 1, a.nsplit, a.block ? a.block : kAttnBlockLong);
-    const size_t base = (size_t)g * a.nsplit * group + hq;
+    const int qpos = a.pos_seq ? a.pos_seq[ti] : (a.pos_dev ? *a.pos_dev : a.start) + ti;
+    const int active = active_splits(qpos + 1, a.nsplit, a.block ? a.block : kAttnBlockLong);
+    const size_t base = ((size_t)ti * a.nkv + g) * a.nsplit * group + hq;
     float m = -INFINITY, l = 0.0f;
     if (t < active) {
         const float2 ml = *reinterpret_cast<const float2 *>(a.part_ml + (base + (size_t)t * group) * 2);
@@ -391,7 +394,7 @@ __global__ __launch_bounds__(kBlock) void attn_combine_kernel(const AttnArgs a) 
     if (t < a.hd) {
         float o = s_o[t];
         for (int j = 1; j < step; j++) o += s_o[j * a.hd + t];
-        a.out_f32[h * a.hd + t] = o / L[0];
+        a.out_f32[(size_t)ti * a.nq * a.hd + h * a.hd + t] = o / L[0];
     }
 }
 
@@ -641,8 +644,8 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_attn_combine(const AttnArgs &a, hipStream_t s) {
-    if (a.nsplit > kBlock || a.hd > kBlock || kBlock % a.hd != 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nq), dim3(kBlock), 0, s, a);
+    if (a.nsplit > kBlock || a.hd > kBlock || kBlock % a.hd != 0 || a.T < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(a.nq, a.T), dim3(kBlock), 0, s, a);
     return hipGetLastError();
 }
 

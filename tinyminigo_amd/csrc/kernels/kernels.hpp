@@ -147,8 +147,9 @@ hipError_t launch_attn(const AttnArgs &a, hipStream_t s);
 // shapes it takes, and the launch.
 bool attn_prefill_supported(const AttnArgs &a);
 hipError_t launch_attn_prefill(const AttnArgs &a, hipStream_t s);
-// Merges the split-K partials of a decode attention launch into out_f32
-// (used when the merge is not fused into the o_proj GEMV prologue).
+// Merges the split-K partials of a decode attention launch (a.T rows) into
+// out_f32 [T][nq*hd]: where the merge is not fused into the o_proj GEMV
+// prologue (more than kFusedSplits splits; batched decode).
 hipError_t launch_attn_combine(const AttnArgs &a, hipStream_t s);
 
 struct FinalizeArgs {
