@@ -46,12 +46,12 @@ struct Scope {
     std::vector<hipGraph_t> graphs;
     std::vector<hipGraphExec_t> execs;
     ~Scope() {
+        // replays enqueued before an early return finish before their
+        // graphs and buffers go
+        if (!mem.empty() || !execs.empty()) (void)hipDeviceSynchronize();
         for (auto x : execs) (void)hipGraphExecDestroy(x);
         for (auto g : graphs) (void)hipGraphDestroy(g);
-        if (!mem.empty()) {
-            (void)hipDeviceSynchronize();
-            for (auto p : mem) (void)hipFree(p);
-        }
+        for (auto p : mem) (void)hipFree(p);
     }
 };
 
