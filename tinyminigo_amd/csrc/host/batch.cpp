@@ -399,11 +399,12 @@ extern "C" int tmg_generate_batch(tmg_model *m, const uint32_t *const *prompts, 
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     auto cleanup = [&]() {
+        // replays still queued on an early return finish first
+        (void)hipStreamSynchronize(m->stream);
         if (exec) (void)hipGraphExecDestroy(exec);
         if (graph) (void)hipGraphDestroy(graph);
         if (e0) (void)hipEventDestroy(e0);
         if (e1) (void)hipEventDestroy(e1);
-        (void)hipStreamSynchronize(m->stream);
     };
     struct Guard {
         decltype(cleanup) &f;

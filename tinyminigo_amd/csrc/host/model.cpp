@@ -1209,14 +1209,19 @@ extern "C" int tmg_profile_decode_step(tmg_model *m, tmg_cache *c, uint32_t toke
             if (rc) break;
             TMG_HIP(e);
         }
-        // destroys the replay graph on every path out of this iteration
+        // destroys the replay graph on every path out of this iteration,
+        // after the replays queued on the stream
         struct ExecGuard {
             hipGraphExec_t &x;
+            hipStream_t s;
             ~ExecGuard() {
-                if (x) (void)hipGraphExecDestroy(x);
+                if (x) {
+                    (void)hipStreamSynchronize(s);
+                    (void)hipGraphExecDestroy(x);
+                }
                 x = nullptr;
             }
-        } guard{ex};
+        } guard{ex, m->stream};
         auto replay = [&]() -> int {
             if (use_graph)
                 return hipGraphLaunch(ex, m->stream) == hipSuccess ? TMG_OK
