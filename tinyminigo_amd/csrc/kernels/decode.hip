@@ -122,8 +122,13 @@ hipError_t launch_kc(const GemvArgs &a, hipStream_t s) {
     // which halve that traffic, are faster (4B o_proj 9.0 -> 7.8 us); over
     // 2048 slower (1B 4.3 -> 4.6 us).  The one-chunk gate/up GEMV also takes
     // 16 rows (half the workgroups, each with the RMSNorm prologue): 1B
-    // 9.70 -> 9.46 us, the step 0.747 -> 0.745 ms
-    constexpr int R = (PRO == PRO_ATTN_COMBINE && KC == 2) || (EPI == EPI_SWIGLU && KC == 1) ? 16 : gemv_rows<KC>();
+    // 9.70 -> 9.46 us, the step 0.747 -> 0.745 ms.  The plain GEMV
+    // (tmg_gemv_bf16) over one chunk takes 4 rows (16 KB per workgroup):
+    // HBM-cold 2048 x 2048 3.44 -> 3.35 us, 73448 x 2048 45.9 -> 45.1 us;
+    // over three chunks 4 rows were slower (2048 x 6144 5.95 -> 6.14 us)
+    constexpr int R = (PRO == PRO_ATTN_COMBINE && KC == 2) || (EPI == EPI_SWIGLU && KC == 1) ? 16
+                      : (PRO == PRO_PLAIN && EPI == EPI_STORE && KC == 1)                    ? 4
+                                                                                              : gemv_rows<KC>();
     const int grid = (a.out + R - 1) / R;
     if (!a.W8 && a.Wf) {
         // (the split-merge prologue is fused only over attention outputs of
