@@ -830,10 +830,12 @@ static int cmp_desc(const void *a, const void *b) {
  *     from 0 in words 12-13, stream 0 in words 14-15, 12 rounds; next_u32
  *     returns the blocks' 16 words in order;
  *   - StandardUniform f32 (rand): (next_u32 >> 8) * 2^-24.
- * The ChaCha block function is pinned by the RFC 7539 vectors at 20 rounds,
- * the XSH-RR output function by the PCG reference demo sequence; the
- * constants specific to the crates are restated, not pinned (no vectors of
- * theirs are available offline). */
+ * The ChaCha block function is pinned by the RFC 7539 vectors at 20 rounds
+ * and by the all-zero key and IV vectors of the ChaCha test-vector draft
+ * (draft-strombergson-chacha-test-vectors-00, TC1) at 8 and 12 rounds, the
+ * XSH-RR output function by the PCG reference demo sequence; the constants
+ * specific to the crates (the seed expansion increment, the f32 conversion)
+ * are restated, not pinned (no vectors of theirs are available offline). */
 
 static uint32_t om_rotl32(uint32_t x, int n) { return (x << n) | (x >> (32 - n)); }
 

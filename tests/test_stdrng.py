@@ -3,11 +3,12 @@ f32, src/model.rs:629 and src/tensor.rs:1204): the oracle's restatement
 against published vectors, and the library's own copy against the oracle.
 
 rand 0.10.2 / rand_core 0.10.1 / chacha20 0.10.2 are not in the reference
-tree.  The ChaCha block function is pinned by RFC 7539 (20 rounds; the
-12-round StdRng runs the same double round six times), the PCG XSH-RR output
-function by the PCG reference demo; the crates' own constants (seed
-expansion increment, 12 rounds, the f32 conversion) are restated and
-unpinned."""
+tree.  The ChaCha block function is pinned by RFC 7539 (20 rounds) and, at
+8 and 12 rounds, by the all-zero key and IV vectors of the ChaCha test-vector
+draft (draft-strombergson-chacha-test-vectors-00, TC1, 256-bit key), so the
+12-round block StdRng uses is pinned; the PCG XSH-RR output function by the
+PCG reference demo; the crates' own constants (seed expansion increment, the
+f32 conversion) are restated and unpinned."""
 import numpy as np
 import pytest
 
@@ -27,6 +28,19 @@ def test_chacha_block_rfc7539():
     assert b"".join(int(x).to_bytes(4, "little") for x in z).hex() == (
         "76b8e0ada0f13d90405d6ae55386bd28bdd219b8a08ded1aa836efcc8b770dc7"
         "da41597c5157488d7724e03fb8d84a376a43b8f41518a11cc387b669b2ee6586")
+
+
+def test_chacha_8_and_12_round_blocks():
+    # draft-strombergson-chacha-test-vectors-00, TC1 (all-zero 256-bit key and
+    # 64-bit IV, block 0): ChaCha8 and ChaCha12 keystream (ChaCha20's is RFC
+    # 7539 A.1 above)
+    def ks(rounds):
+        z = O.chacha_block(np.zeros(8, np.uint32), 0, 0, rounds)
+        return b"".join(int(x).to_bytes(4, "little") for x in z).hex()
+    assert ks(8) == ("3e00ef2f895f40d67f5bb8e81f09a5a12c840ec3ce9a7f3b181be188ef711a1e"
+                     "984ce172b9216f419f445367456d5619314a42a3da86b001387bfdb80e0cfe42")
+    assert ks(12) == ("9bf49a6a0755f953811fce125f2683d50429c3bb49e074147e0089a52eae155f"
+                      "0564f879d27ae3c02ce82834acfa8c793a629f2ca0de6919610be82f411326be")
 
 
 def test_chacha_rounds_and_counter():
