@@ -104,7 +104,7 @@ def W():
 # in = 2560 and 5120: 320-thread workgroups, one and two chunks of 2560
 @pytest.mark.parametrize("out,inp", [(2048, 2048), (6144, 2048), (2048, 6144), (73448, 2048), (24, 64),
                                      (100, 136), (8, 10240), (1, 8), (2560, 4096), (6144, 2560), (7, 2560),
-                                     (100, 5120)])
+                                     (100, 5120), (1001, 2048), (6, 1000)])
 def test_gemv_bf16_vs_oracle(T, O, out, inp):
     from tinyminigo_amd.hip import DeviceBuffer, synchronize
     print(f"gemv {out}x{inp}", flush=True)
