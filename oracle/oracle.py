@@ -60,6 +60,7 @@ def _load_lib():
         "om_sample": (S, [PF, S, F, S, F, F, PU32, PF, C.POINTER(S)]),
         "om_chacha_block": (None, [PU32, C.c_uint64, C.c_uint64, C.c_int, PU32]),
         "om_pcg_xsh_rr": (C.c_uint32, [C.c_uint64]),
+        "om_uniform_f32": (C.c_float, [C.c_uint32]),
         "om_stdrng_key": (None, [C.c_uint64, PU32]),
         "om_stdrng_uniform": (None, [C.c_uint64, S, PF]),
         "om_model_new": (C.c_void_p, [C.c_void_p]),
@@ -292,6 +293,11 @@ def chacha_block(key, counter: int, stream: int, rounds: int) -> np.ndarray:
 
 def pcg_xsh_rr(state: int) -> int:
     return int(lib.om_pcg_xsh_rr(state))
+
+
+def uniform_f32(word: int) -> float:
+    """StandardUniform f32 of one next_u32 word (exact in f32)."""
+    return float(lib.om_uniform_f32(word))
 
 
 def stdrng_key(seed: int) -> np.ndarray:

@@ -833,9 +833,12 @@ static int cmp_desc(const void *a, const void *b) {
  * The ChaCha block function is pinned by the RFC 7539 vectors at 20 rounds
  * and by the all-zero key and IV vectors of the ChaCha test-vector draft
  * (draft-strombergson-chacha-test-vectors-00, TC1) at 8 and 12 rounds, the
- * XSH-RR output function by the PCG reference demo sequence; the constants
- * specific to the crates (the seed expansion increment, the f32 conversion)
- * are restated, not pinned (no vectors of theirs are available offline). */
+ * XSH-RR output function by the PCG reference demo sequence, and the three
+ * crate-specific steps by the crates' own value-stability vectors: the seed
+ * expansion by rand_core's test_seed_from_u64 (seed 0 -> 5029875928683246316),
+ * StdRng's key layout, counter, stream and word order by rand's
+ * test_stdrng_construction (rngs/std.rs), and the f32 conversion by rand's
+ * StandardUniform f32 value_stability test (distr/float.rs). */
 
 static uint32_t om_rotl32(uint32_t x, int n) { return (x << n) | (x >> (32 - n)); }
 
@@ -882,13 +885,17 @@ OM_API void om_stdrng_key(uint64_t seed, uint32_t key[8]) {
     }
 }
 
+/* StandardUniform f32 of one next_u32 word: its top 24 bits times 2^-24
+ * (exact), so the draws lie in [0, 1). */
+OM_API float om_uniform_f32(uint32_t word) { return (float)(word >> 8) * (1.0f / 16777216.0f); }
+
 /* The first n StandardUniform f32 draws of StdRng::seed_from_u64(seed). */
 OM_API void om_stdrng_uniform(uint64_t seed, size_t n, float *out) {
     uint32_t key[8], blk[16];
     om_stdrng_key(seed, key);
     for (size_t j = 0; j < n; j++) {
         if (j % 16 == 0) om_chacha_block(key, (uint64_t)(j / 16), 0, 12, blk);
-        out[j] = (float)(blk[j % 16] >> 8) * (1.0f / 16777216.0f);
+        out[j] = om_uniform_f32(blk[j % 16]);
     }
 }
 

@@ -315,10 +315,10 @@ def test_sampling_teacher_forced(T, O, untied, temp, k, p, pen):
 @pytest.mark.parametrize("temp,k,p,pen,seed", [(0.8, 50, 0.9, 1.1, 42), (1.0, 0, 1.0, 1.0, 7),
                                                (0.9, 0, 0.8, 1.0, 123), (1.1, 200, 0.95, 1.2, 2024)])
 def test_sampled_stream_matches_reference_rng(T, O, untied, temp, k, p, pen, seed):
-    # A consistency check, not parity: free running (not teacher-forced), the
-    # library's StdRng restatement and the oracle's (two restatements of the
-    # same published algorithm, with no test vector from the reference's
-    # crates) give the same sampled ids for the same seed.
+    # Free running (not teacher-forced): the library's StdRng draws and the
+    # oracle's (the oracle's stream pinned by the rand crates' own
+    # value-stability vectors, tests/test_stdrng.py) drive the same sampled
+    # ids for the same seed as the oracle's generate.
     g, o, wl = untied
     prompt = [int(t) for t in T.synth_tokens(31, 10, wl.vocab_size)]
     out = T.generate(g, prompt, T.GenParams(max_tokens=40, temperature=temp, top_k=k, top_p=p,

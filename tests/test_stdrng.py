@@ -7,8 +7,9 @@ tree.  The ChaCha block function is pinned by RFC 7539 (20 rounds) and, at
 8 and 12 rounds, by the all-zero key and IV vectors of the ChaCha test-vector
 draft (draft-strombergson-chacha-test-vectors-00, TC1, 256-bit key), so the
 12-round block StdRng uses is pinned; the PCG XSH-RR output function by the
-PCG reference demo; the crates' own constants (seed expansion increment, the
-f32 conversion) are restated and unpinned."""
+PCG reference demo; the crates' own steps (the seed expansion, StdRng's key
+layout, counter, stream and word order, the f32 conversion) by the
+value-stability vectors those crates' own tests hold."""
 import numpy as np
 import pytest
 
@@ -41,6 +42,41 @@ def test_chacha_8_and_12_round_blocks():
                      "984ce172b9216f419f445367456d5619314a42a3da86b001387bfdb80e0cfe42")
     assert ks(12) == ("9bf49a6a0755f953811fce125f2683d50429c3bb49e074147e0089a52eae155f"
                       "0564f879d27ae3c02ce82834acfa8c793a629f2ca0de6919610be82f411326be")
+
+
+def test_rand_crates_value_stability_vectors():
+    """The known answers of the crates' own value-stability tests, through
+    the oracle's functions."""
+    M, INC, MASK = 6364136223846793005, 11634580027462260723, 2**64 - 1
+    # rand_core, test_seed_from_u64: an 8-byte seed from seed_from_u64(0) reads
+    # back as 5029875928683246316; StdRng's 32-byte seed starts with the same
+    # two PCG32 outputs
+    key0 = [int(x) for x in O.stdrng_key(0)]
+    assert key0[0] | (key0[1] << 32) == 5029875928683246316
+    # rand, rngs/std.rs test_stdrng_construction: StdRng::from_seed of this
+    # seed gives next_u64 10719222850664546238; a second StdRng seeded from the
+    # next 32 bytes of the first gives 14064965282130556830
+    seed = bytes([1, 0, 0, 0, 23, 0, 0, 0, 200, 1, 0, 0, 210, 30, 0, 0] + [0] * 16)
+    key = np.frombuffer(seed, "<u4").astype(np.uint32)
+    w = [int(x) for x in O.chacha_block(key, 0, 0, 12)]
+    assert w[0] | (w[1] << 32) == 10719222850664546238
+    w2 = [int(x) for x in O.chacha_block(np.array(w[2:10], np.uint32), 0, 0, 12)]
+    assert w2[0] | (w2[1] << 32) == 14064965282130556830
+    # rand, distr/float.rs value_stability: StandardUniform f32 draws from the
+    # tests' Pcg32::new(0x6f44f5646c2a7334, INC) source (increment (INC << 1) | 1,
+    # the state stepped once after adding it, each output taken from the state
+    # before its step)
+    inc = ((INC << 1) | 1) & MASK
+    st = ((0x6f44f5646c2a7334 + inc) * M + inc) & MASK
+    draws = []
+    for _ in range(3):
+        draws.append(np.float32(O.uniform_f32(O.pcg_xsh_rr(st))))
+        st = (st * M + inc) & MASK
+    assert draws == [np.float32(0.0035963655), np.float32(0.7346052), np.float32(0.09778172)]
+    # and the oracle's draws of seed 0 are the conversion of that stream's words
+    u = O.stdrng_uniform(0, 2)
+    b = O.chacha_block(np.array(key0, np.uint32), 0, 0, 12)
+    assert [float(x) for x in u] == [O.uniform_f32(int(b[0])), O.uniform_f32(int(b[1]))]
 
 
 def test_chacha_rounds_and_counter():
