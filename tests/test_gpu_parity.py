@@ -491,6 +491,27 @@ def test_hidden_2560_model_vs_oracle(T, O, W):
     g.close()
 
 
+def test_attention_output_3072_merge_in_o_proj(T, O, W):
+    """A 3072-wide attention output (24 query heads of 128 over 6 KV heads):
+    the o_proj merges the attention splits in its prologue with 512-thread
+    workgroups whose one 4096-element chunk is three quarters full.  Logits
+    at every decode step and the greedy ids against the oracle."""
+    import dataclasses
+    wl = dataclasses.replace(W.FOUR_B, name="mid-h512-q24-k6-d128-i1024-l2-v1000", hidden_size=512,
+                             num_attention_heads=24, num_key_value_heads=6, head_dim=128, intermediate_size=1024,
+                             num_hidden_layers=2, vocab_size=1000, weight_seed=29)
+    p = W.ensure_model(wl, model_root())
+    g, o = T.Model.load(p), O.OracleModel.load(p)
+    ids = [int(t) for t in T.synth_tokens(41, 70, wl.vocab_size)]
+    gc, oc = T.KvCache(g, 96), o.new_cache()
+    close_logits(g.forward_seq(ids[:30], gc), o.forward_seq(ids[:30], oc), "prefill")
+    for i, t in enumerate(ids[30:]):
+        close_logits(g.forward_token(t, gc), o.forward_token(t, oc), f"decode {i}")
+    prompt = ids[:16]
+    assert T.generate(g, prompt, T.GenParams(max_tokens=24)).tokens == O.generate(o, prompt, 24).tokens
+    g.close()
+
+
 # --- C4: the 4B-class model, 128-token prompt + 256 sampled tokens ------------
 
 @pytest.fixture(scope="module")

@@ -118,17 +118,17 @@ __global__ __launch_bounds__(kBlock) void gemv_f32_kernel(const GemvArgs a) {
 template <int KC, int PRO, int EPI>
 hipError_t launch_kc(const GemvArgs &a, hipStream_t s) {
     // the split-merge prologue re-reads every split's partials per
-    // workgroup: over a 4096-wide attention output 16 rows per workgroup,
-    // which halve that traffic, are faster (4B o_proj 9.0 -> 7.8 us); over
-    // 2048 slower (1B 4.3 -> 4.6 us).  The one-chunk gate/up GEMV also takes
-    // 16 rows (half the workgroups, each with the RMSNorm prologue): 1B
-    // 9.70 -> 9.46 us, the step 0.747 -> 0.745 ms.  The plain GEMV
-    // (tmg_gemv_bf16) over one chunk takes 4 rows (16 KB per workgroup):
-    // HBM-cold 2048 x 2048 3.44 -> 3.35 us, 73448 x 2048 45.9 -> 45.1 us;
-    // over three chunks 4 rows were slower (2048 x 6144 5.95 -> 6.14 us)
-    constexpr int R = (PRO == PRO_ATTN_COMBINE && KC == 2) || (EPI == EPI_SWIGLU && KC == 1) ? 16
-                      : (PRO == PRO_PLAIN && EPI == EPI_STORE && KC == 1)                    ? 4
-                                                                                              : gemv_rows<KC>();
+    // workgroup; over a 2048-wide attention output 16 rows per workgroup
+    // instead of 8 were slower (1B o_proj 4.3 -> 4.6 us).  The one-chunk
+    // gate/up GEMV takes 16 rows (half the workgroups, each with the RMSNorm
+    // prologue): 1B 9.70 -> 9.46 us, the step 0.747 -> 0.745 ms.  The plain
+    // GEMV (tmg_gemv_bf16) over one chunk takes 4 rows (16 KB per
+    // workgroup): HBM-cold 2048 x 2048 3.44 -> 3.35 us, 73448 x 2048 45.9 ->
+    // 45.1 us; over three chunks 4 rows were slower (2048 x 6144 5.95 ->
+    // 6.14 us)
+    constexpr int R = (EPI == EPI_SWIGLU && KC == 1)                      ? 16
+                      : (PRO == PRO_PLAIN && EPI == EPI_STORE && KC == 1) ? 4
+                                                                          : gemv_rows<KC>();
     const int grid = (a.out + R - 1) / R;
     if (!a.W8 && a.Wf) {
         // (the split-merge prologue is fused only over attention outputs of
@@ -148,6 +148,8 @@ hipError_t launch_kc(const GemvArgs &a, hipStream_t s) {
             hipLaunchKernelGGL((gemv_i8_kernel<KC, R8, PRO, EPI>), dim3((a.out + R8 - 1) / R8), dim3(kBlock), 0, s,
                                a);
         }
+    } else if constexpr (PRO == PRO_ATTN_COMBINE && KC > 1) {
+        return hipErrorInvalidValue;  // BF16 rows of 2049-4096: launch_merge_wide
     } else {
         hipLaunchKernelGGL((gemv_kernel<KC, R, PRO, EPI>), dim3(grid), dim3(kBlock), 0, s, a);
     }
@@ -171,9 +173,29 @@ hipError_t launch_wide(const GemvArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// The split merge over an attention output of 2049-4096 elements (the
+// 4B-class o_proj): 512 threads with one 4096-element chunk each, so a
+// wavefront issues half the loads of two chunks at 256 threads (24 partial
+// and 16 weight loads, within the 63 that vmcnt counts) and holds 156
+// VGPRs instead of 256 plus 46 spilled to AGPRs: 4B o_proj 8.25 -> 7.21 us,
+// the sampled 4B step 1.920 -> 1.883 ms.  16 rows per workgroup (each
+// workgroup re-reads all the split partials, so fewer rows re-read them
+// more often: 8 rows took 9.4 us).
+constexpr int kMergeBlock = 512;
+
+template <int PRO, int EPI>
+hipError_t launch_merge_wide(const GemvArgs &a, hipStream_t s) {
+    constexpr int R = 16;
+    hipLaunchKernelGGL((gemv_kernel<1, R, PRO, EPI, kMergeBlock>), dim3((a.out + R - 1) / R), dim3(kMergeBlock), 0, s,
+                       a);
+    return hipGetLastError();
+}
+
 template <int PRO, int EPI>
 hipError_t launch_pe(const GemvArgs &a, hipStream_t s) {
-    if constexpr (PRO != PRO_ATTN_COMBINE) {
+    if constexpr (PRO == PRO_ATTN_COMBINE) {
+        if (!a.W8 && !a.Wf && a.in > kChunk && a.in <= kMergeBlock * 8) return launch_merge_wide<PRO, EPI>(a, s);
+    } else {
         if (!a.W8 && !a.Wf && a.in % kChunk != 0 && a.in % kWideChunk == 0) {
             switch (a.in / kWideChunk) {
                 case 1: return launch_wide<1, PRO, EPI>(a, s);
