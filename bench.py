@@ -591,7 +591,7 @@ def main():
     # the step next to its floor (graph replays; skipped when the step's
     # kernels are launched one by one, as under the profiler)
     floor = None
-    if args.workload == "1b" and not i8 and not args.no_floor and os.environ.get("TMG_DECODE_GRAPH", "1") != "0":
+    if args.workload in ("1b", "4b") and not i8 and not args.no_floor and os.environ.get("TMG_DECODE_GRAPH", "1") != "0":
         floor = step_floor(m, tok, cache, per, step_bytes)
 
     # the other two model workloads, reported beside the headline (1b line only)
