@@ -246,17 +246,18 @@ def step_floor(m, tok, cache, per, step_bytes):
             "kinds": kinds}
 
 
-def extra_long_context(T, W, m, sync):
+def extra_long_context(T, W, m, sync, with_floor=True):
     """The long-context workload (C3) on the already loaded 1B model: an
     8192-token prefill, then 128 greedy decode steps from the captured step
     graph (warmed on the same cache, which is reset and refilled before the
-    timed steps).  Reports the step rate, the KV share of the step bytes and
-    the decode attention kernel's rate at that context."""
+    timed steps).  Reports the step rate, the KV share of the step bytes, the
+    decode attention kernel's rate at that context and, with_floor, the step
+    next to its streaming floor at the final position."""
     import numpy as np
     wl = W.LONG_CTX
     prompt = [int(t) for t in wl.prompt()]
     P, K = wl.prompt_len, wl.gen_tokens
-    c = T.KvCache(m, P + K + 8)
+    c = T.KvCache(m, P + K + 24)  # + the step-floor replays
     sync()
     t = time.perf_counter()
     lg = m.forward_seq(prompt, c)
@@ -281,6 +282,7 @@ def extra_long_context(T, W, m, sync):
     step_bytes = wl.decode_bytes(int(round(n_ctx)))
     per = kernel_table(m, c, int(toks[-1]))
     attn = per.get("attn_decode")
+    floor = step_floor(m, int(toks[-1]), c, per, step_bytes) if with_floor else None
     c.close()
     log(f"8k: prefill {prefill_s * 1e3:.1f} ms (first, with scratch allocation: {first_prefill_s * 1e3:.1f} ms), "
         f"decode {ms_step:.4f} ms/step")
@@ -294,6 +296,7 @@ def extra_long_context(T, W, m, sync):
         "prefill_ms": round(prefill_s * 1e3, 2), "prefill_tok_s": round(P / prefill_s, 1),
         "prefill_tflops": round(wl.prefill_flops(P) / prefill_s / 1e12, 1),
         "first_prefill_ms": round(first_prefill_s * 1e3, 2),
+        "step_floor": floor,
     }
 
 
@@ -597,7 +600,8 @@ def main():
     # the other two model workloads, reported beside the headline (1b line only)
     extras = {} if setup_s is None else {"generate_setup_ms": round(setup_s * 1e3, 3)}
     if args.workload == "1b" and not i8 and not sampled and not args.no_extras:
-        extras["c3_long_context"] = extra_long_context(T, W, m, sync)
+        extras["c3_long_context"] = extra_long_context(
+            T, W, m, sync, with_floor=not args.no_floor and os.environ.get("TMG_DECODE_GRAPH", "1") != "0")
 
     cpu = None
     if not args.no_cpu:
