@@ -191,24 +191,27 @@ hipError_t launch_merge_wide(const GemvArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// The residual GEMV over rows of 10240 (the 4B-class down projection): 640
-// threads with two 5120-element chunks instead of five 2048-element chunks
-// at 256 threads (12 loads per wavefront instead of 30, 58 VGPRs instead of
-// 128), 4 rows per workgroup: 11.13 -> 10.91 us per launch (8 rows: 12.4).
-constexpr int kDownBlock = 640;
-
-template <int PRO, int EPI>
+// The residual GEMV over the down projection's long rows, 4 rows per
+// workgroup, in wider workgroups with fewer chunks per thread than 2048-
+// element chunks at 256 threads:
+// - rows of 10240 (4B-class): 640 threads, two 5120-element chunks (12 loads
+//   per wavefront instead of 30, 58 VGPRs instead of 128): 11.13 -> 10.91 us
+//   per launch (8 rows: 12.4);
+// - rows of 6144 (1B-class): 768 threads, one 6144-element chunk (6 loads
+//   per wavefront instead of 30): 5.98 -> 6.05 us replayed alone, but the
+//   step 0.7461 -> 0.7424 ms (8 rows: 0.7433).
+template <int KC, int NT, int PRO, int EPI>
 hipError_t launch_down_wide(const GemvArgs &a, hipStream_t s) {
     constexpr int R = 4;
-    hipLaunchKernelGGL((gemv_kernel<2, R, PRO, EPI, kDownBlock>), dim3((a.out + R - 1) / R), dim3(kDownBlock), 0, s,
-                       a);
+    hipLaunchKernelGGL((gemv_kernel<KC, R, PRO, EPI, NT>), dim3((a.out + R - 1) / R), dim3(NT), 0, s, a);
     return hipGetLastError();
 }
 
 template <int PRO, int EPI>
 hipError_t launch_pe(const GemvArgs &a, hipStream_t s) {
     if constexpr (PRO == PRO_PLAIN && EPI == EPI_RESID) {
-        if (!a.W8 && !a.Wf && a.in == 2 * kDownBlock * 8) return launch_down_wide<PRO, EPI>(a, s);
+        if (!a.W8 && !a.Wf && a.in == 2 * 640 * 8) return launch_down_wide<2, 640, PRO, EPI>(a, s);
+        if (!a.W8 && !a.Wf && a.in == 768 * 8) return launch_down_wide<1, 768, PRO, EPI>(a, s);
     }
     if constexpr (PRO == PRO_ATTN_COMBINE) {
         if (!a.W8 && !a.Wf && a.in > kChunk && a.in <= kMergeBlock * 8) return launch_merge_wide<PRO, EPI>(a, s);
