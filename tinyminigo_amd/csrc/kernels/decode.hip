@@ -119,16 +119,17 @@ template <int KC, int PRO, int EPI>
 hipError_t launch_kc(const GemvArgs &a, hipStream_t s) {
     // the split-merge prologue re-reads every split's partials per
     // workgroup; over a 2048-wide attention output 16 rows per workgroup
-    // instead of 8 were slower (1B o_proj 4.3 -> 4.6 us).  The one-chunk
-    // gate/up GEMV takes 16 rows (half the workgroups, each with the RMSNorm
-    // prologue): 1B 9.70 -> 9.46 us, the step 0.747 -> 0.745 ms.  The plain
-    // GEMV (tmg_gemv_bf16) over one chunk takes 4 rows (16 KB per
-    // workgroup): HBM-cold 2048 x 2048 3.44 -> 3.35 us, 73448 x 2048 45.9 ->
-    // 45.1 us; over three chunks 4 rows were slower (2048 x 6144 5.95 ->
-    // 6.14 us)
-    constexpr int R = (EPI == EPI_SWIGLU && KC == 1)                      ? 16
-                      : (PRO == PRO_PLAIN && EPI == EPI_STORE && KC == 1) ? 4
-                                                                          : gemv_rows<KC>();
+    // instead of 8 were slower (1B o_proj 4.37 -> 4.77 us, the step 0.7414
+    // -> 0.7528 ms).  The one-chunk gate/up and QKV GEMVs take 16 rows (half
+    // the workgroups, each with the RMSNorm prologue): 1B gate/up 9.70 ->
+    // 9.46 us, the step 0.747 -> 0.745 ms; QKV 5.11 -> 4.98 us, the step
+    // 0.7414 -> 0.7403 ms.  The plain GEMV (tmg_gemv_bf16) over one chunk
+    // takes 4 rows (16 KB per workgroup): HBM-cold 2048 x 2048 3.44 -> 3.35
+    // us, 73448 x 2048 45.9 -> 45.1 us; over three chunks 4 rows were slower
+    // (2048 x 6144 5.95 -> 6.14 us)
+    constexpr int R = ((EPI == EPI_SWIGLU || (EPI == EPI_QKV && PRO == PRO_NORM)) && KC == 1) ? 16
+                      : (PRO == PRO_PLAIN && EPI == EPI_STORE && KC == 1)                     ? 4
+                                                                                               : gemv_rows<KC>();
     const int grid = (a.out + R - 1) / R;
     if (!a.W8 && a.Wf) {
         // (the split-merge prologue is fused only over attention outputs of
