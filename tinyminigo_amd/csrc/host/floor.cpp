@@ -145,7 +145,9 @@ extern "C" int tmg_profile_step_floor(tmg_model *m, tmg_cache *c, uint32_t token
     int rc;
     Scope sc;
 
-    // the step as the decode loop captures it (greedy selection)
+    // the step as the decode loop captures it (greedy selection, the
+    // attention form of a step at the cache's position)
+    FormGuard form(c);
     if ((rc = set_state(m, c, (int)token, true))) return rc;
     LaunchRecorder rec;
     hipGraphExec_t step_ex = nullptr;

@@ -98,7 +98,12 @@ extern "C" int tmg_generate(tmg_model *m, const uint32_t *prompt, size_t n_promp
         stdrng_uniform(p->seed, draws.size(), draws.data());
         TMG_HIPG(hipMemcpy(c->draws, draws.data(), draws.size() * 4, hipMemcpyHostToDevice));
     }
-    if (step_graphs_enabled() && (rc = get_step_graph(m, c, mode))) return rc;
+    // step j writes position n_prompt + j: the graphs of the first and the
+    // last step's attention forms
+    if (step_graphs_enabled() &&
+        ((rc = get_step_graph(m, c, mode, step_form(c, n_prompt))) ||
+         (p->max_tokens > 0 && (rc = get_step_graph(m, c, mode, step_form(c, n_prompt + p->max_tokens - 1))))))
+        return rc;
 
     // prefill (timed like the reference, src/model.rs:622-624)
     auto t0 = std::chrono::steady_clock::now();
@@ -126,7 +131,7 @@ extern "C" int tmg_generate(tmg_model *m, const uint32_t *prompt, size_t n_promp
     size_t produced = 0;
     for (size_t i = 0; i < max_tokens; i++) {
         while (enq < max_tokens && enq < i + kWindow) {
-            if ((rc = launch_step(m, c, mode))) return rc;
+            if ((rc = launch_step(m, c, mode, n_prompt + enq))) return rc;
             TMG_HIPG(hipEventRecord(ring.ev[(enq + 1) % (kWindow + 1)], m->stream));
             enq++;
         }

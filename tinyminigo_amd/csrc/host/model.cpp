@@ -469,6 +469,7 @@ int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mod
         aa.nsplit = c->attn_nsplit;
         aa.block = c->attn_block;
         aa.cap = (int)c->max_pos;
+        aa.spec_splits = c->capture_spec_all ? c->attn_nsplit : 0;
         aa.part = m->attn_part;
         aa.part_ml = m->attn_ml;
         aa.out_f32 = c->attn_nsplit == 1 ? m->attn_out : nullptr;
@@ -571,10 +572,21 @@ int enqueue_select(tmg_model *m, tmg_cache *c, int mode, int advance_pos) {
     return TMG_OK;
 }
 
-int get_step_graph(tmg_model *m, tmg_cache *c, int mode) {
-    if (c->graphs[mode]) return TMG_OK;
+int step_form(const tmg_cache *c, uint64_t pos) {
+    // all splits active: ceil((pos + 1) / block) >= nsplit.  Where they are,
+    // the first-block loads of splits kSpecSplits.. need not wait for the
+    // position read (8K context: 15.5 -> 15.15 us per layer); on a long
+    // cache at a short context they would stream every inactive split's
+    // first block
+    return c->attn_nsplit > kSpecSplits && pos + 1 > (uint64_t)(c->attn_nsplit - 1) * (uint64_t)c->attn_block;
+}
+
+int get_step_graph(tmg_model *m, tmg_cache *c, int mode, int form) {
+    if (c->graphs[form][mode]) return TMG_OK;
     TMG_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+    c->capture_spec_all = form == 1;
     int rc = enqueue_decode_step(m, c, nullptr, mode);
+    c->capture_spec_all = false;
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(m->stream, &g);
     if (rc) {
@@ -588,8 +600,8 @@ int get_step_graph(tmg_model *m, tmg_cache *c, int mode) {
         (void)hipGraphDestroy(g);
         TMG_HIP(e);
     }
-    c->graph_src[mode] = g;
-    c->graphs[mode] = ex;
+    c->graph_src[form][mode] = g;
+    c->graphs[form][mode] = ex;
     return TMG_OK;
 }
 
@@ -603,11 +615,17 @@ bool step_graphs_enabled() {
     return on;
 }
 
-int launch_step(tmg_model *m, tmg_cache *c, int mode) {
-    if (!step_graphs_enabled()) return enqueue_decode_step(m, c, nullptr, mode);
-    int rc = get_step_graph(m, c, mode);
+int launch_step(tmg_model *m, tmg_cache *c, int mode, uint64_t pos) {
+    const int form = step_form(c, pos);
+    if (!step_graphs_enabled()) {
+        c->capture_spec_all = form == 1;
+        const int rc = enqueue_decode_step(m, c, nullptr, mode);
+        c->capture_spec_all = false;
+        return rc;
+    }
+    int rc = get_step_graph(m, c, mode, form);
     if (rc) return rc;
-    TMG_HIP(hipGraphLaunch(c->graphs[mode], m->stream));
+    TMG_HIP(hipGraphLaunch(c->graphs[form][mode], m->stream));
     return TMG_OK;
 }
 
@@ -977,10 +995,11 @@ extern "C" void tmg_cache_free(tmg_cache *c) {
     if (!c) return;
     (void)hipSetDevice(c->model->device);
     (void)hipStreamSynchronize(c->model->stream);
-    for (int i = 0; i < 4; i++) {
-        if (c->graphs[i]) (void)hipGraphExecDestroy(c->graphs[i]);
-        if (c->graph_src[i]) (void)hipGraphDestroy(c->graph_src[i]);
-    }
+    for (int f = 0; f < 2; f++)
+        for (int i = 0; i < 4; i++) {
+            if (c->graphs[f][i]) (void)hipGraphExecDestroy(c->graphs[f][i]);
+            if (c->graph_src[f][i]) (void)hipGraphDestroy(c->graph_src[f][i]);
+        }
     (void)hipFree(c->seen);
     (void)hipFree(c->cand);
     (void)hipFree(c->gsc);
@@ -1047,7 +1066,7 @@ extern "C" int tmg_forward_token(tmg_model *m, tmg_cache *c, uint32_t token, flo
     (void)hipSetDevice(m->device);
     int rc;
     if ((rc = set_state(m, c, (int)token, false))) return rc;
-    if ((rc = launch_step(m, c, SEL_ARGMAX))) return rc;
+    if ((rc = launch_step(m, c, SEL_ARGMAX, c->len))) return rc;
     c->len += 1;
     return fetch_logits(m, logits);
 }
@@ -1135,13 +1154,17 @@ extern "C" int tmg_decode_greedy(tmg_model *m, tmg_cache *c, uint32_t token, uin
     (void)hipSetDevice(m->device);
     int rc;
     if ((rc = set_state(m, c, (int)token, true))) return rc;
-    // the step graph is captured before the first timing event
-    if (step_graphs_enabled() && (rc = get_step_graph(m, c, SEL_ARGMAX))) return rc;
+    // the step graphs (the forms of the first and the last step) are
+    // captured before the first timing event
+    if (step_graphs_enabled() && n_steps > 0 &&
+        ((rc = get_step_graph(m, c, SEL_ARGMAX, step_form(c, c->len))) ||
+         (rc = get_step_graph(m, c, SEL_ARGMAX, step_form(c, (uint64_t)c->len + n_steps - 1)))))
+        return rc;
     EventPair ev;
     TMG_HIP(ev.create());
     TMG_HIP(hipEventRecord(ev.e0, m->stream));
     for (uint32_t i = 0; i < n_steps; i++)
-        if ((rc = launch_step(m, c, SEL_ARGMAX))) return rc;
+        if ((rc = launch_step(m, c, SEL_ARGMAX, (uint64_t)c->len + i))) return rc;
     TMG_HIP(hipEventRecord(ev.e1, m->stream));
     TMG_HIP(hipEventSynchronize(ev.e1));
     float el = 0.f;
@@ -1161,6 +1184,7 @@ extern "C" int tmg_profile_decode_step(tmg_model *m, tmg_cache *c, uint32_t toke
     (void)hipSetDevice(m->device);
     int rc;
     // the kernels of one step, in launch order
+    FormGuard form(c);
     LaunchRecorder all;
     all.none = true;
     if ((rc = enqueue_decode_step(m, c, &all, SEL_ARGMAX))) return rc;

@@ -101,9 +101,13 @@ struct tmg_cache {
     float *draws = nullptr;              // [max_pos + 2] uniform draw per step (sampling)
     float *gsc = nullptr;                // kSampleScratchBytes(V) of the whole-vocabulary sampler
     int samp_use_k = 0, samp_use_p = 0;  // the running generate call's top-k / nucleus
-    // one captured step graph per token-selection mode (tmg::SelectMode)
-    hipGraphExec_t graphs[4] = {nullptr, nullptr, nullptr, nullptr};
-    hipGraph_t graph_src[4] = {nullptr, nullptr, nullptr, nullptr};
+    // one captured step graph per token-selection mode (tmg::SelectMode) and
+    // attention form: [1] where every split is active (long contexts of
+    // caches with more than kSpecSplits splits), every split loads its first
+    // block before the position read; [0] otherwise
+    hipGraphExec_t graphs[2][4] = {};
+    hipGraph_t graph_src[2][4] = {};
+    bool capture_spec_all = false;  // set while [1] is being captured
 };
 
 namespace tmg {
@@ -151,11 +155,24 @@ enum SelectMode {
 
 int enqueue_decode_step(tmg_model *m, tmg_cache *c, LaunchRecorder *rec, int mode);
 int enqueue_select(tmg_model *m, tmg_cache *c, int mode, int advance_pos);
-int get_step_graph(tmg_model *m, tmg_cache *c, int mode);
-// One decode step on the model's stream: the cache's captured graph for
-// `mode`, or (TMG_DECODE_GRAPH=0) the same kernels launched one by one.
+// The attention form of a step writing position pos (1: every split active
+// on a cache with more than kSpecSplits splits).
+int step_form(const tmg_cache *c, uint64_t pos);
+int get_step_graph(tmg_model *m, tmg_cache *c, int mode, int form);
+// For its lifetime, steps enqueued directly (measurement captures) take the
+// attention form of a step at the cache's position.
+struct FormGuard {
+    tmg_cache *c;
+    explicit FormGuard(tmg_cache *c_) : c(c_) { c->capture_spec_all = step_form(c, c->len) == 1; }
+    ~FormGuard() { c->capture_spec_all = false; }
+    FormGuard(const FormGuard &) = delete;
+    FormGuard &operator=(const FormGuard &) = delete;
+};
+// One decode step writing position pos on the model's stream: the cache's
+// captured graph for `mode` and the step's attention form, or
+// (TMG_DECODE_GRAPH=0) the same kernels launched one by one.
 bool step_graphs_enabled();
-int launch_step(tmg_model *m, tmg_cache *c, int mode);
+int launch_step(tmg_model *m, tmg_cache *c, int mode, uint64_t pos);
 int set_state(tmg_model *m, tmg_cache *c, int token, bool reset_step);
 int run_prefill(tmg_model *m, tmg_cache *c, const uint32_t *tokens, size_t n);
 int ensure_rope(tmg_model *m, int npos);

@@ -385,14 +385,14 @@ __global__ __launch_bounds__(kBlock) void quantize_i8_f32_kernel(const float *w,
 // them across the XCDs' L2s without any in-kernel fence.
 // ---------------------------------------------------------------------------
 
-// SPEC (decode): splits below kSpecSplits load their first chunk before the
-// position is read (see attn_item).
+// SPEC (decode): splits below a.spec_splits (default kSpecSplits) load their
+// first chunk before the position is read (see attn_item).
 template <int HD, int GROUP, bool SPEC, int NT = kBlock, int CHW = kAttnBlockLong>
 __global__ __launch_bounds__(NT) void attn_kernel(const AttnArgs a) {
     __shared__ AttnShared<HD, GROUP, NT> sm;
     const int split = blockIdx.x, g = blockIdx.y, ti = blockIdx.z;
     if constexpr (SPEC) {
-        if (split < kSpecSplits) {
+        if (split < (a.spec_splits > 0 ? a.spec_splits : kSpecSplits)) {
             attn_item<HD, GROUP, true, NT, CHW>(a, split, g, ti, 0, 0, sm);
             return;
         }

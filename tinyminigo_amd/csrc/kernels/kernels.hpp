@@ -114,6 +114,7 @@ struct AttnArgs {
     int nsplit;       // grid.x
     int block;        // positions per block of the split partition (decode; 0 means kAttnBlockLong)
     int cap;          // rows of k_cache / v_cache (bounds the speculative first-chunk loads; 0 disables them)
+    int spec_splits;  // splits that load their first chunk before the position read (0: kSpecSplits)
     float *part;      // [T][nkv][nsplit][group][hd] partial outputs
     float *part_ml;   // [T][nkv][nsplit][group][2] (max of the log2-scaled scores, sum)
     float *out_f32;   // [T][nq*hd] when one split covers the row, or null
