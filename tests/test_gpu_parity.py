@@ -748,6 +748,13 @@ def test_long_context_8k_vs_oracle_fixture(T, W, one_b):
     got = [first] + [int(t) for t in toks]
     want = [int(t) for t in fx["ids"]]
     assert got == want, f"first divergence at {next(i for i, (x, y) in enumerate(zip(got, want)) if x != y)}"
+    c.close()
+    # generate on the same prompt: its own cache of more than 8 splits, every
+    # step past the position where all splits are active, so it replays the
+    # step graph in which every split loads its first block speculatively
+    print("8k generate", flush=True)
+    out = T.generate(g, ids, T.GenParams(max_tokens=24))
+    assert out.tokens == want[:24]
 
 
 def test_long_context_8k_decode_logits_vs_oracle_fixture(T, W, one_b):
